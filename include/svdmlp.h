@@ -1,0 +1,111 @@
+/*
+ * svdmlp.h - C ABI of libsvdmlp.so, the MI355X (gfx950) implementation of the
+ * SVD-compressed LLaMA MLP hot path:
+ *
+ *     h = SiLU(x . Ug . Vg) * (x . Uu . Vu)          (fused Gate/Up)
+ *     y = h . Ud . Vd                                 (low-rank XUV Down)
+ *
+ * Conventions (every entry point):
+ *   - All pointers are device pointers owned by the caller (including the
+ *     outputs and the workspace); the library never allocates.  Matrices are
+ *     dense and row-major with the leading dimension equal to the row length.
+ *   - Factor layouts follow kernels/reference.py: U is (d_in, r), V is
+ *     (r, d_out) ("natural" layout).  Setting SVDMLP_U_LINEAR / SVDMLP_V_LINEAR
+ *     declares the PyTorch Linear layout instead: U given as (r, d_in) and V as
+ *     (d_out, r) (the checkpoint's *_v_proj / *_u_proj tensors, as consumed by
+ *     the reference's nki_mm, test_speedup.py:658-666).
+ *   - act_dtype is SVDMLP_BF16 or SVDMLP_F32.  w_dtype is the factor dtype:
+ *     equal to act_dtype, or SVDMLP_FP8_E4M3 with bf16 activations, in which
+ *     case every factor carries one fp32 scale per output column (U: r scales,
+ *     V: d_out scales) and the scale pointers must be non-NULL.
+ *   - Arithmetic: fp32 accumulation; with bf16 activations the rank-r
+ *     intermediate and h are rounded to bf16 (round-to-nearest-even) at each
+ *     GEMM boundary and the output is rounded once, as the reference does.
+ *   - Work is enqueued on `stream` (a hipStream_t) and is asynchronous.
+ *   - Return value: 0 on success; SVDMLP_EINVAL for an invalid argument (the
+ *     message is available from svdmlp_last_error(), thread-local); SVDMLP_EHIP
+ *     for a HIP runtime error.
+ *   - Calls on different streams with distinct workspaces may run concurrently.
+ */
+#ifndef SVDMLP_H
+#define SVDMLP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SVDMLP_VERSION 100 /* 1.0.0 */
+
+/* element types */
+#define SVDMLP_F32 0
+#define SVDMLP_BF16 1
+#define SVDMLP_FP8_E4M3 2
+
+/* layout flags */
+#define SVDMLP_U_LINEAR 0x1u /* U stored (r, d_in) instead of (d_in, r) */
+#define SVDMLP_V_LINEAR 0x2u /* V stored (d_out, r) instead of (r, d_out) */
+#define SVDMLP_OUT_T 0x4u    /* gate_up: write h transposed, (ff, T) */
+#define SVDMLP_X_T 0x8u      /* xuv: input given transposed, (d_in, T) */
+
+/* status codes */
+#define SVDMLP_OK 0
+#define SVDMLP_EINVAL (-1)
+#define SVDMLP_EHIP (-2)
+
+/* Library version (SVDMLP_VERSION of the build). */
+int svdmlp_version(void);
+
+/* Message describing the last failed call on this thread ("" if none). */
+const char* svdmlp_last_error(void);
+
+/*
+ * Workspace bytes needed by svdmlp_gate_up, svdmlp_xuv and svdmlp_svd_mlp for
+ * T tokens, hidden size d, intermediate size ff and (maximum) rank r.  The
+ * same workspace may be reused by consecutive calls on one stream.
+ * Replaces the VMEM planning of test_speedup.py:208-258 (the TPU kernels keep
+ * XU in VMEM scratch; here the rank-r intermediate lives in this buffer).
+ */
+size_t svdmlp_workspace_bytes(int64_t T, int64_t d, int64_t ff, int64_t r, int32_t w_dtype);
+
+/*
+ * Fused Gate/Up with the SwiGLU epilogue:
+ *   h = SiLU((x . ug) . vg) * ((x . uu) . vu),  x (T, d), h (T, ff)
+ * (or h^T (ff, T) with SVDMLP_OUT_T).  Gate and up must have equal shapes.
+ * Replaces kernels/reference.py:54-72 (fused_gate_up_ref) and the Pallas
+ * launcher fused_mlp_up_T, test_speedup.py:522-544 (which returns (I, S)).
+ */
+int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                   const float* s_ug, const float* s_vg, const float* s_uu, const float* s_vu, void* h,
+                   int64_t T, int64_t d, int64_t ff, int64_t r, int32_t act_dtype, int32_t w_dtype,
+                   uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Low-rank projection y = (x . u) . v, x (T, d_in) (or x^T (d_in, T) with
+ * SVDMLP_X_T), u (d_in, r), v (r, d_out), y (T, d_out).
+ * Replaces kernels/reference.py:75-82 (fused_xuv_ref) and the Pallas launcher
+ * fused_three_mm_XTUV, test_speedup.py:500-519 (which takes x as (I, S)).
+ */
+int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, const float* s_v, void* y,
+               int64_t T, int64_t din, int64_t dout, int64_t r, int32_t act_dtype, int32_t w_dtype,
+               uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * The whole SVD-MLP layer, y = xuv(gate_up(x)), with h rounded to the
+ * activation dtype between the two halves (kernels/reference.py:85-93,
+ * svd_mlp_ref; test_speedup.py:631-655, svd_mlp_with_fused_kernel).  Gate/up
+ * rank r_gu and down rank r_d may differ.  h does not leave the workspace; at
+ * decode shapes it is never materialised at all.
+ */
+int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                   const void* ud, const void* vd, const float* const* scales /* 6 or NULL */, void* y,
+                   int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
+                   int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVDMLP_H */

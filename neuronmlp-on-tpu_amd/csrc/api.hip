@@ -1,0 +1,478 @@
+// C ABI of libsvdmlp.so (declared in include/svdmlp.h).
+//
+// Stage plans
+//   prefill (T > 64, or shapes the decode kernels do not take):
+//     XU    = X . U                 tiled MFMA GEMM; split-K with fp32 atomics
+//                                   when there are too few output tiles
+//     h     = SiLU(XUg.Vg)*(XUu.Vu) dual-branch GEMM, SwiGLU epilogue
+//     y     = (h . Ud) . Vd         the same two GEMM kinds
+//   decode (bf16 activations, T <= 64, aligned shapes):
+//     zero fp32 accumulators -> X.[Ug|Uu] -> XU.[Vg|Vu] -> SwiGLU(g,u).Ud -> .Vd
+//     every stage streams its factor once from HBM (split-K, fp32 atomics);
+//     h is formed on the fly from the fp32 gate/up sums and never stored.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+#include <string>
+
+#include "dispatch.hpp"
+#include "svdmlp.h"
+
+using namespace svdmlp;
+
+namespace {
+
+constexpr int64_t kDecodeMaxT = 64;
+constexpr int kTargetBlocks = 384;  // ~1.5 blocks per CU on 256 CUs
+
+thread_local std::string g_err;
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return SVDMLP_EINVAL;
+}
+
+int check(hipError_t e, const char* what, const char* why = nullptr) {
+  if (e == hipSuccess) return SVDMLP_OK;
+  if (e == hipErrorInvalidValue && why) return fail("%s: %s", what, why);
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return SVDMLP_EHIP;
+}
+
+size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
+
+struct Ws {
+  size_t xu_bf16;  // [2][T][r] bf16 (gate, up) rank-r intermediate
+  size_t xu32;     // [3][T][r] fp32 (gate, up, down) split-K accumulators
+  size_t gu32;     // [2][T][big] fp32 gate/up sums (decode)
+  size_t h;        // [T][big] h of the fused layer (4 bytes/elem worst case)
+  size_t y32;      // [T][big] fp32 output accumulator (decode)
+  size_t total;
+};
+
+Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
+  const int64_t big = std::max(d, ff);
+  const bool dec = T <= kDecodeMaxT;
+  Ws w;
+  size_t off = 0;
+  w.xu_bf16 = off;
+  off += a256(2 * T * r * 2);
+  w.xu32 = off;
+  off += a256(3 * T * r * 4);
+  w.gu32 = off;
+  off += dec ? a256(2 * T * big * 4) : 0;
+  w.h = off;
+  off += a256(T * big * 4);
+  w.y32 = off;
+  off += dec ? a256(T * big * 4) : 0;
+  w.total = off;
+  return w;
+}
+
+bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+struct Common {
+  int act, wt;
+  bool f32;
+  hipStream_t st;
+};
+
+int check_types(int32_t act, int32_t wt) {
+  if (act == SVDMLP_BF16 && (wt == SVDMLP_BF16 || wt == SVDMLP_FP8_E4M3)) return SVDMLP_OK;
+  if (act == SVDMLP_F32 && wt == SVDMLP_F32) return SVDMLP_OK;
+  return fail("unsupported dtype combination: activations %d, weights %d (supported: bf16/bf16, "
+              "bf16/fp8_e4m3, f32/f32)", act, wt);
+}
+
+int srcb_of(int wt) { return wt == SVDMLP_FP8_E4M3 ? SRC_FP8 : (wt == SVDMLP_F32 ? SRC_F32 : SRC_BF16); }
+
+int choose_splits(int blocks, int K, int BK, int* k_split) {
+  int splits = 1;
+  if (blocks < kTargetBlocks) splits = std::min((kTargetBlocks + blocks - 1) / blocks, std::max(1, K / 512));
+  int ks = (K + splits - 1) / splits;
+  ks = (ks + BK - 1) / BK * BK;
+  *k_split = ks;
+  return (K + ks - 1) / ks;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill stages
+// ---------------------------------------------------------------------------
+
+// out_b = A . U_b for b < batch (gate/up share A).  Writes bf16 rank-r
+// intermediates (xu_bf16) when there are enough tiles, otherwise zeroes and
+// accumulates fp32 split-K partials (xu32).  *a_src reports what the next
+// stage reads.
+int prefill_xu(const Common& c, const Operand& a, bool a_kc, const void* const* u, const float* const* su, bool u_lin,
+               int T, int K, int r, int batch, bool vec, char* ws, const Ws& L, int32_t xu_slot, int* a_src,
+               const void** xu_out, int64_t* xu_bstride) {
+  const int BK = c.f32 ? 32 : 64;
+  GemmParams p{};
+  for (int b = 0; b < batch; ++b) {
+    p.a[b] = a;
+    p.b[b] = Operand{u[b], nullptr, u_lin ? K : r};
+    p.scale[b] = su ? su[b] : nullptr;
+  }
+  p.M = T;
+  p.N = r;
+  p.K = K;
+  p.mtiles = (T + kGemmBM - 1) / kGemmBM;
+  p.ntiles = (r + kGemmBN - 1) / kGemmBN;
+  p.ldo = r;
+  p.out_bstride = (int64_t)T * r;
+  int k_split = 0;
+  const int splits = choose_splits(p.mtiles * p.ntiles * batch, K, BK, &k_split);
+  p.k_split = k_split;
+  GemmDesc d{c.f32, c.f32 ? SRC_F32 : SRC_BF16, srcb_of(c.wt), a_kc, u_lin, 1, EPI_STORE, false, c.f32, vec};
+  float* xu32 = reinterpret_cast<float*>(ws + L.xu32) + (int64_t)xu_slot * T * r;
+  if (splits > 1) {
+    int rc = check(launch_fill_zero(xu32, (int64_t)batch * T * r, c.st), "zero rank-r accumulator");
+    if (rc) return rc;
+    d.epi = EPI_ATOMIC;
+    p.out = xu32;
+    *a_src = SRC_F32;
+    *xu_out = xu32;
+  } else if (c.f32) {
+    p.out = xu32;
+    *a_src = SRC_F32;
+    *xu_out = xu32;
+  } else {
+    p.out = ws + L.xu_bf16;
+    *a_src = SRC_BF16;
+    *xu_out = ws + L.xu_bf16;
+  }
+  *xu_bstride = p.out_bstride;
+  const char* why = nullptr;
+  return check(gemm_launch(d, p, splits, batch, c.st, &why), "XU stage", why);
+}
+
+// out = SiLU(XUg . Vg) * (XUu . Vu)
+int prefill_swiglu(const Common& c, int a_src, const void* xu, int64_t xu_bstride, const void* vg, const void* vu,
+                   const float* svg, const float* svu, bool v_lin, int T, int r, int ff, bool vec, bool out_t,
+                   void* out) {
+  GemmParams p{};
+  const size_t esz = (a_src == SRC_F32) ? 4 : 2;
+  p.a[0] = Operand{xu, nullptr, r};
+  p.a[1] = Operand{static_cast<const char*>(xu) + xu_bstride * esz, nullptr, r};
+  p.b[0] = Operand{vg, nullptr, v_lin ? r : ff};
+  p.b[1] = Operand{vu, nullptr, v_lin ? r : ff};
+  p.scale[0] = svg;
+  p.scale[1] = svu;
+  p.out = out;
+  p.ldo = out_t ? T : ff;
+  p.M = T;
+  p.N = ff;
+  p.K = r;
+  p.mtiles = (T + kGemmBM - 1) / kGemmBM;
+  p.ntiles = (ff + kGemmBN - 1) / kGemmBN;
+  p.k_split = r;
+  GemmDesc d{c.f32, a_src, srcb_of(c.wt), true, v_lin, 2, EPI_SWIGLU, out_t, c.f32, vec};
+  const char* why = nullptr;
+  return check(gemm_launch(d, p, 1, 1, c.st, &why), "gate/up XUV stage", why);
+}
+
+// y = XU . V
+int prefill_v(const Common& c, int a_src, const void* xu, const void* v, const float* sv, bool v_lin, int T, int r,
+              int dout, bool vec, void* y) {
+  GemmParams p{};
+  p.a[0] = Operand{xu, nullptr, r};
+  p.b[0] = Operand{v, nullptr, v_lin ? r : dout};
+  p.scale[0] = sv;
+  p.out = y;
+  p.ldo = dout;
+  p.M = T;
+  p.N = dout;
+  p.K = r;
+  p.mtiles = (T + kGemmBM - 1) / kGemmBM;
+  p.ntiles = (dout + kGemmBN - 1) / kGemmBN;
+  p.k_split = r;
+  GemmDesc d{c.f32, a_src, srcb_of(c.wt), true, v_lin, 1, EPI_STORE, false, c.f32, vec};
+  const char* why = nullptr;
+  return check(gemm_launch(d, p, 1, 1, c.st, &why), "XUV stage", why);
+}
+
+// ---------------------------------------------------------------------------
+// Decode stages
+// ---------------------------------------------------------------------------
+
+int decode_mt(int64_t T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
+
+int decode_stage(const Common& c, int T, int K, int nseg, const Operand* a, int srca, const void* const* w,
+                 const float* const* sw, bool w_lin, const int* N, float* const* out, const char* what) {
+  DecodeParams p{};
+  p.nseg = nseg;
+  p.T = T;
+  p.K = K;
+  int tiles = 0;
+  for (int s = 0; s < nseg; ++s) {
+    p.a[s] = a[s];
+    p.seg[s].w = w[s];
+    p.seg[s].scale = sw ? sw[s] : nullptr;
+    p.seg[s].out = out[s];
+    p.seg[s].ldw = w_lin ? K : N[s];
+    p.seg[s].ldo = N[s];
+    p.seg[s].N = N[s];
+    p.seg[s].ntiles = (N[s] + kDecTileN - 1) / kDecTileN;
+    tiles += p.seg[s].ntiles;
+  }
+  // K slice per block: enough blocks to cover the chip ~2x, slices of >= 128.
+  int64_t ks = ((int64_t)K * tiles + 511) / 512;
+  ks = std::max<int64_t>(128, (ks + 127) / 128 * 128);
+  ks = std::min<int64_t>(ks, ((int64_t)K + 31) / 32 * 32);
+  p.k_split = (int)ks;
+  const int splits = (int)(((int64_t)K + ks - 1) / ks);
+  DecodeDesc d{decode_mt(T), srca, srcb_of(c.wt), w_lin};
+  const char* why = nullptr;
+  return check(launch_decode(d, p, tiles * splits, c.st, &why), what, why);
+}
+
+bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, bool vec) {
+  if (c.f32 || T > kDecodeMaxT || !vec) return false;
+  for (int64_t v : dims)
+    if (v % 8) return false;
+  return true;
+}
+
+int validate_dims(int64_t T, int64_t a, int64_t b, int64_t r) {
+  if (T <= 0 || a <= 0 || b <= 0 || r <= 0)
+    return fail("dimensions must be positive, got T=%lld, %lld, %lld, r=%lld", (long long)T, (long long)a,
+                (long long)b, (long long)r);
+  const int64_t lim = (int64_t)1 << 30;
+  if (T >= lim || a >= lim || b >= lim || r >= lim || T * std::max(a, b) >= ((int64_t)1 << 40))
+    return fail("dimensions too large");
+  return SVDMLP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int svdmlp_version(void) { return SVDMLP_VERSION; }
+
+const char* svdmlp_last_error(void) { return g_err.c_str(); }
+
+size_t svdmlp_workspace_bytes(int64_t T, int64_t d, int64_t ff, int64_t r, int32_t w_dtype) {
+  (void)w_dtype;
+  if (T <= 0 || d <= 0 || ff <= 0 || r <= 0) return 0;
+  return ws_layout(T, d, ff, r).total;
+}
+
+int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                   const float* s_ug, const float* s_vg, const float* s_uu, const float* s_vu, void* h,
+                   int64_t T, int64_t d, int64_t ff, int64_t r, int32_t act_dtype, int32_t w_dtype,
+                   uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_dims(T, d, ff, r);
+  if (rc) return rc;
+  if ((rc = check_types(act_dtype, w_dtype))) return rc;
+  if (!x || !ug || !vg || !uu || !vu || !h || !workspace) return fail("null pointer argument");
+  const bool fp8 = w_dtype == SVDMLP_FP8_E4M3;
+  if (fp8 && (!s_ug || !s_vg || !s_uu || !s_vu)) return fail("fp8 weights need per-column scales");
+  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_OUT_T)) return fail("unsupported flags 0x%x", flags);
+  if (fp8 && (flags & (SVDMLP_U_LINEAR | SVDMLP_V_LINEAR))) return fail("fp8 weights must use the natural layout");
+  const Ws L = ws_layout(T, d, ff, r);
+  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
+  const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR, out_t = flags & SVDMLP_OUT_T;
+  bool vec = d % 8 == 0 && ff % 8 == 0 && r % 8 == 0 && (!out_t || T % 8 == 0);
+  for (const void* q : {x, ug, vg, uu, vu, (const void*)h, (const void*)workspace}) vec = vec && aligned16(q);
+  if (fp8 && !vec) return fail("fp8 weights need d, ff and r to be multiples of 8 and 16-byte aligned buffers");
+  char* ws = static_cast<char*>(workspace);
+
+  if (decode_ok(c, T, {d, ff, r}, vec)) {
+    float* xu32 = reinterpret_cast<float*>(ws + L.xu32);
+    float* g32 = reinterpret_cast<float*>(ws + L.gu32);
+    float* u32 = g32 + T * ff;
+    rc = check(launch_fill_zero(xu32, (int64_t)(L.h - L.xu32) / 4, c.st), "zero accumulators");
+    if (rc) return rc;
+    const Operand ax{x, nullptr, d};
+    const Operand a1[2] = {ax, ax};
+    const void* w1[2] = {ug, uu};
+    const float* s1[2] = {s_ug, s_uu};
+    const int n1[2] = {(int)r, (int)r};
+    float* o1[2] = {xu32, xu32 + T * r};
+    rc = decode_stage(c, T, d, 2, a1, SRC_BF16, w1, fp8 ? s1 : nullptr, u_lin, n1, o1, "decode X.U");
+    if (rc) return rc;
+    const Operand a2[2] = {Operand{xu32, nullptr, r}, Operand{xu32 + T * r, nullptr, r}};
+    const void* w2[2] = {vg, vu};
+    const float* s2[2] = {s_vg, s_vu};
+    const int n2[2] = {(int)ff, (int)ff};
+    float* o2[2] = {g32, u32};
+    rc = decode_stage(c, T, r, 2, a2, SRC_F32, w2, fp8 ? s2 : nullptr, v_lin, n2, o2, "decode XU.V");
+    if (rc) return rc;
+    return check(launch_finalize(g32, u32, ff, static_cast<uint16_t*>(h), out_t ? T : ff, T, ff, true, out_t, c.st),
+                 "SwiGLU finalize");
+  }
+
+  const Operand ax{x, nullptr, d};
+  const void* us[2] = {ug, uu};
+  const float* sus[2] = {s_ug, s_uu};
+  int a_src = 0;
+  const void* xu = nullptr;
+  int64_t xu_bs = 0;
+  rc = prefill_xu(c, ax, true, us, fp8 ? sus : nullptr, u_lin, T, d, r, 2, vec, ws, L, 0, &a_src, &xu, &xu_bs);
+  if (rc) return rc;
+  return prefill_swiglu(c, a_src, xu, xu_bs, vg, vu, fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr, v_lin, T, r, ff,
+                        vec, out_t, h);
+}
+
+int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, const float* s_v, void* y,
+               int64_t T, int64_t din, int64_t dout, int64_t r, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+               void* workspace, size_t ws_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_dims(T, din, dout, r);
+  if (rc) return rc;
+  if ((rc = check_types(act_dtype, w_dtype))) return rc;
+  if (!x || !u || !v || !y || !workspace) return fail("null pointer argument");
+  const bool fp8 = w_dtype == SVDMLP_FP8_E4M3;
+  if (fp8 && (!s_u || !s_v)) return fail("fp8 weights need per-column scales");
+  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_X_T)) return fail("unsupported flags 0x%x", flags);
+  if (fp8 && (flags & (SVDMLP_U_LINEAR | SVDMLP_V_LINEAR))) return fail("fp8 weights must use the natural layout");
+  const Ws L = ws_layout(T, din, dout, r);
+  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
+  const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR, x_t = flags & SVDMLP_X_T;
+  bool vec = din % 8 == 0 && dout % 8 == 0 && r % 8 == 0 && (!x_t || T % 8 == 0);
+  for (const void* q : {x, u, v, (const void*)y, (const void*)workspace}) vec = vec && aligned16(q);
+  if (fp8 && !vec) return fail("fp8 weights need d_in, d_out and r to be multiples of 8 and 16-byte aligned buffers");
+  char* ws = static_cast<char*>(workspace);
+
+  if (!x_t && decode_ok(c, T, {din, dout, r}, vec)) {
+    float* xd32 = reinterpret_cast<float*>(ws + L.xu32) + 2 * T * r;
+    float* y32 = reinterpret_cast<float*>(ws + L.y32);
+    rc = check(launch_fill_zero(xd32, T * r, c.st), "zero accumulators");
+    if (!rc) rc = check(launch_fill_zero(y32, T * dout, c.st), "zero accumulators");
+    if (rc) return rc;
+    const Operand a1[1] = {Operand{x, nullptr, din}};
+    const void* w1[1] = {u};
+    const float* s1[1] = {s_u};
+    const int n1[1] = {(int)r};
+    float* o1[1] = {xd32};
+    rc = decode_stage(c, T, din, 1, a1, SRC_BF16, w1, fp8 ? s1 : nullptr, u_lin, n1, o1, "decode X.U");
+    if (rc) return rc;
+    const Operand a2[1] = {Operand{xd32, nullptr, r}};
+    const void* w2[1] = {v};
+    const float* s2[1] = {s_v};
+    const int n2[1] = {(int)dout};
+    float* o2[1] = {y32};
+    rc = decode_stage(c, T, r, 1, a2, SRC_F32, w2, fp8 ? s2 : nullptr, v_lin, n2, o2, "decode XU.V");
+    if (rc) return rc;
+    return check(launch_finalize(y32, nullptr, dout, static_cast<uint16_t*>(y), dout, T, dout, false, false, c.st),
+                 "output finalize");
+  }
+
+  const Operand ax{x, nullptr, x_t ? T : din};
+  const void* us[1] = {u};
+  const float* sus[1] = {s_u};
+  int a_src = 0;
+  const void* xu = nullptr;
+  int64_t xu_bs = 0;
+  rc = prefill_xu(c, ax, !x_t, us, fp8 ? sus : nullptr, u_lin, T, din, r, 1, vec, ws, L, 2, &a_src, &xu, &xu_bs);
+  if (rc) return rc;
+  return prefill_v(c, a_src, xu, v, fp8 ? s_v : nullptr, v_lin, T, r, dout, vec, y);
+}
+
+int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu, const void* vu, const void* ud,
+                   const void* vd, const float* const* scales, void* y, int64_t T, int64_t d, int64_t ff,
+                   int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags, void* workspace,
+                   size_t ws_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
+  if (rc) return rc;
+  if ((rc = check_types(act_dtype, w_dtype))) return rc;
+  if (!x || !ug || !vg || !uu || !vu || !ud || !vd || !y || !workspace) return fail("null pointer argument");
+  const bool fp8 = w_dtype == SVDMLP_FP8_E4M3;
+  if (fp8) {
+    if (!scales) return fail("fp8 weights need per-column scales");
+    for (int i = 0; i < 6; ++i)
+      if (!scales[i]) return fail("fp8 weights need per-column scales");
+  }
+  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR)) return fail("unsupported flags 0x%x", flags);
+  if (fp8 && flags) return fail("fp8 weights must use the natural layout");
+  const int64_t r = std::max(r_gu, r_d);
+  const Ws L = ws_layout(T, d, ff, r);
+  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
+  const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR;
+  bool vec = d % 8 == 0 && ff % 8 == 0 && r_gu % 8 == 0 && r_d % 8 == 0;
+  for (const void* q : {x, ug, vg, uu, vu, ud, vd, (const void*)y, (const void*)workspace}) vec = vec && aligned16(q);
+  if (fp8 && !vec) return fail("fp8 weights need d, ff and ranks to be multiples of 8 and 16-byte aligned buffers");
+  char* ws = static_cast<char*>(workspace);
+  const float* S[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  if (fp8)
+    for (int i = 0; i < 6; ++i) S[i] = scales[i];
+
+  if (decode_ok(c, T, {d, ff, r_gu, r_d}, vec)) {
+    float* xu32 = reinterpret_cast<float*>(ws + L.xu32);
+    float* xg = xu32;
+    float* xuu = xu32 + T * r;
+    float* xd = xu32 + 2 * T * r;
+    float* g32 = reinterpret_cast<float*>(ws + L.gu32);
+    float* u32 = g32 + T * ff;
+    float* y32 = reinterpret_cast<float*>(ws + L.y32);
+    rc = check(launch_fill_zero(xu32, (int64_t)(L.total - L.xu32) / 4, c.st), "zero accumulators");
+    if (rc) return rc;
+    const Operand ax{x, nullptr, d};
+    {
+      const Operand a[2] = {ax, ax};
+      const void* w[2] = {ug, uu};
+      const float* s[2] = {S[0], S[2]};
+      const int n[2] = {(int)r_gu, (int)r_gu};
+      float* o[2] = {xg, xuu};
+      if ((rc = decode_stage(c, T, d, 2, a, SRC_BF16, w, s, u_lin, n, o, "decode X.U"))) return rc;
+    }
+    {
+      const Operand a[2] = {Operand{xg, nullptr, r_gu}, Operand{xuu, nullptr, r_gu}};
+      const void* w[2] = {vg, vu};
+      const float* s[2] = {S[1], S[3]};
+      const int n[2] = {(int)ff, (int)ff};
+      float* o[2] = {g32, u32};
+      if ((rc = decode_stage(c, T, r_gu, 2, a, SRC_F32, w, s, v_lin, n, o, "decode XU.V"))) return rc;
+    }
+    {
+      const Operand a[1] = {Operand{g32, u32, ff}};
+      const void* w[1] = {ud};
+      const float* s[1] = {S[4]};
+      const int n[1] = {(int)r_d};
+      float* o[1] = {xd};
+      if ((rc = decode_stage(c, T, ff, 1, a, SRC_SWIGLU, w, s, u_lin, n, o, "decode h.Ud"))) return rc;
+    }
+    {
+      const Operand a[1] = {Operand{xd, nullptr, r_d}};
+      const void* w[1] = {vd};
+      const float* s[1] = {S[5]};
+      const int n[1] = {(int)d};
+      float* o[1] = {y32};
+      if ((rc = decode_stage(c, T, r_d, 1, a, SRC_F32, w, s, v_lin, n, o, "decode XUd.Vd"))) return rc;
+    }
+    return check(launch_finalize(y32, nullptr, d, static_cast<uint16_t*>(y), d, T, d, false, false, c.st),
+                 "output finalize");
+  }
+
+  // Prefill: h stays in the workspace between the two halves.
+  const Operand ax{x, nullptr, d};
+  const void* us[2] = {ug, uu};
+  const float* sus[2] = {S[0], S[2]};
+  int a_src = 0;
+  const void* xu = nullptr;
+  int64_t xu_bs = 0;
+  rc = prefill_xu(c, ax, true, us, fp8 ? sus : nullptr, u_lin, T, d, r_gu, 2, vec, ws, L, 0, &a_src, &xu, &xu_bs);
+  if (rc) return rc;
+  void* hbuf = ws + L.h;
+  rc = prefill_swiglu(c, a_src, xu, xu_bs, vg, vu, S[1], S[3], v_lin, T, r_gu, ff, vec, false, hbuf);
+  if (rc) return rc;
+  const Operand ah{hbuf, nullptr, ff};
+  const void* ud1[1] = {ud};
+  const float* sud[1] = {S[4]};
+  rc = prefill_xu(c, ah, true, ud1, fp8 ? sud : nullptr, u_lin, T, ff, r_d, 1, vec, ws, L, 2, &a_src, &xu, &xu_bs);
+  if (rc) return rc;
+  return prefill_v(c, a_src, xu, vd, S[5], v_lin, T, r_d, d, vec, y);
+}
+
+}  // extern "C"

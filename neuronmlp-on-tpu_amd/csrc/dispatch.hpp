@@ -1,0 +1,66 @@
+// Runtime -> template dispatch for the SVD-MLP kernels.  Each launcher
+// returns hipSuccess, or hipErrorInvalidValue (with *why set) when the
+// requested combination has no compiled instance.
+#pragma once
+
+#include "decode.hpp"
+
+namespace svdmlp {
+
+struct GemmDesc {
+  bool tm_f32;   // MFMA type: fp32 (true) or bf16 (false)
+  int srca;      // SrcKind of A
+  int srcb;      // SrcKind of B
+  bool a_kc;     // A stored (M, K) with K contiguous; else (K, M)
+  bool b_kc;     // B stored (N, K) with K contiguous (Linear); else (K, N)
+  int nbr;       // 1 or 2 branches
+  int epi;       // EpiKind
+  bool out_t;    // transposed output
+  bool out_f32;  // fp32 output (EPI_STORE / EPI_SWIGLU)
+  bool vec;      // 16-byte vector path (aligned, multiples of 8)
+};
+
+struct DecodeDesc {
+  int mt;        // 16-row token tiles: 1, 2 or 4
+  int srca;      // SRC_BF16, SRC_F32 or SRC_SWIGLU
+  int srcb;      // SRC_BF16 or SRC_FP8
+  bool b_kc;     // Linear-layout weights
+};
+
+// Block tile of the prefill GEMM (rows x cols of C per 256-thread block).
+constexpr int kGemmBM = 128;
+constexpr int kGemmBN = 128;
+
+hipError_t launch_gemm_bf16(const GemmDesc& d, const GemmParams& p, int splits, int batch, hipStream_t st,
+                            const char** why);
+hipError_t launch_gemm_fp8(const GemmDesc& d, const GemmParams& p, int splits, int batch, hipStream_t st,
+                           const char** why);
+hipError_t launch_gemm_f32(const GemmDesc& d, const GemmParams& p, int splits, int batch, hipStream_t st,
+                           const char** why);
+hipError_t launch_decode(const DecodeDesc& d, const DecodeParams& p, int blocks, hipStream_t st,
+                         const char** why);
+hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
+hipError_t launch_finalize(const float* g, const float* u, int64_t ldi, uint16_t* out, int64_t ldo, int rows,
+                           int cols, bool swiglu, bool out_t, hipStream_t st);
+
+inline hipError_t gemm_launch(const GemmDesc& d, const GemmParams& p, int splits, int batch, hipStream_t st,
+                              const char** why) {
+  if (d.tm_f32) return launch_gemm_f32(d, p, splits, batch, st, why);
+  if (d.srcb == SRC_FP8) return launch_gemm_fp8(d, p, splits, batch, st, why);
+  return launch_gemm_bf16(d, p, splits, batch, st, why);
+}
+
+// Compile-time bool expansion helper.
+template <class F>
+inline hipError_t expand_bool(bool b, F&& f) {
+  return b ? f(std::true_type{}) : f(std::false_type{});
+}
+
+template <class Cfg>
+inline hipError_t run_gemm(const GemmParams& p, int splits, int batch, hipStream_t st) {
+  dim3 grid(p.mtiles * p.ntiles, splits, batch);
+  hipLaunchKernelGGL(gemm_kernel<Cfg>, grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace svdmlp

@@ -1,0 +1,26 @@
+"""svdmlp -- the SVD-compressed LLaMA MLP hot path on AMD Instinct MI355X.
+
+Host package over libsvdmlp.so (hand-written HIP kernels for gfx950):
+
+* :mod:`svdmlp.ops`     -- kernels/reference.py operator API
+  (``fused_gate_up``, ``fused_xuv``, ``svd_mlp``) on ROCm tensors.
+* :mod:`svdmlp.compat`  -- the test_speedup.py launcher API
+  (``fused_mlp_up_T``, ``fused_three_mm_XTUV``, ``svd_mlp_with_fused_kernel``,
+  ``nki_mm``, ``get_fused_*_params`` ...).
+* :mod:`svdmlp.config`  -- model shapes, ranks and block parameters.
+* :mod:`svdmlp.inputs`  -- seeded synthetic inputs of the benchmark configs.
+* :mod:`svdmlp.fp8`     -- fp8 e4m3fn per-channel factor quantization.
+"""
+
+from ._lib import SvdMlpError, load, version, workspace_bytes  # noqa: F401
+from .ops import (  # noqa: F401
+    QuantizedFactor,
+    fused_gate_up,
+    fused_xuv,
+    low_rank_dim,
+    silu,
+    svd_mlp,
+    svd_mlp_workspace,
+)
+
+__version__ = "1.0.0"

@@ -1,0 +1,91 @@
+"""Build libsvdmlp.so (HIP, gfx950) in-tree.
+
+    python -m svdmlp._build            # from neuronmlp-on-tpu_amd/
+
+Each ``csrc/*.hip`` translation unit is compiled by ``hipcc`` in parallel and
+linked into ``svdmlp/libsvdmlp.so`` next to this file, so the library travels
+with the source tree.  The shared library links ``libamdhip64.so.7`` by soname;
+imported after torch it binds to the HIP runtime torch already loaded, so
+streams and device pointers are shared with PyTorch.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+ROOT = PKG_DIR.parent  # neuronmlp-on-tpu_amd/
+CSRC = ROOT / "csrc"
+INCLUDE = ROOT.parent / "include"
+BUILD_DIR = ROOT / "_build"
+LIB_PATH = PKG_DIR / "libsvdmlp.so"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    # Packed fp32 ops stay disabled for all device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found; the SVD-MLP HIP library cannot be built")
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    text = "\n".join(l for l in proc.stdout.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{text}")
+    if text.strip():
+        print(text, file=sys.stderr)
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every HIP translation unit and link libsvdmlp.so; returns its path."""
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    objs = [BUILD_DIR / (s.stem + ".o") for s in srcs]
+    jobs = jobs or min(8, os.cpu_count() or 1, len(srcs))
+
+    def compile_one(pair):
+        src, obj = pair
+        cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), file=sys.stderr)
+        _run(cmd)
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        list(pool.map(compile_one, zip(srcs, objs)))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,286 @@
+"""SVD-MLP operators on MI355X: the kernels/reference.py API backed by HIP.
+
+    fused_gate_up(x, u_gate, v_gate, u_up, v_up)      kernels/reference.py:54-72
+    fused_xuv(x, u, v)                                kernels/reference.py:75-82
+    svd_mlp(x, ug, vg, uu, vu, ud, vd)                kernels/reference.py:85-93
+
+Arguments are CUDA (ROCm) tensors.  Factors use the reference's natural
+layout, ``u`` (d_in, r) and ``v`` (r, d_out); a factor that is the transpose
+view of a contiguous PyTorch ``Linear.weight`` (out, in) is passed to the
+kernels without a copy (layout flag).  Activations and factors are bfloat16
+or float32 (all the same dtype), or factors are :class:`QuantizedFactor`
+(fp8 e4m3fn + per-output-column fp32 scale) with bfloat16 activations.
+
+Every call goes to libsvdmlp.so; there is no CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+_ACT_CODES = {torch.bfloat16: _lib.SVDMLP_BF16, torch.float32: _lib.SVDMLP_F32}
+
+
+@dataclass(frozen=True)
+class QuantizedFactor:
+    """An fp8 e4m3fn factor in natural (d_in, d_out) layout with one fp32
+    scale per output column: ``w ~= data.float() * scale``."""
+
+    data: torch.Tensor  # (d_in, d_out), torch.float8_e4m3fn (or raw uint8 bits)
+    scale: torch.Tensor  # (d_out,), float32
+
+    @property
+    def shape(self) -> torch.Size:
+        return self.data.shape
+
+    @property
+    def dtype(self):
+        return self.data.dtype
+
+    @property
+    def device(self):
+        return self.data.device
+
+    def dim(self) -> int:
+        return self.data.dim()
+
+    def dequantize(self) -> torch.Tensor:
+        return self.data.view(torch.float8_e4m3fn).float() * self.scale.float()
+
+
+# ---------------------------------------------------------------------------
+# Validation (messages follow test_speedup.py:37-49,508-509,530-533)
+# ---------------------------------------------------------------------------
+
+def _shape(a) -> tuple[int, ...]:
+    return tuple(a.shape)
+
+
+def validate_arrays(*arrays) -> None:
+    """Reference ``_validate_arrays`` contract (test_speedup.py:42-49)."""
+    for a in arrays:
+        if a.dim() != 2 or min(_shape(a)) <= 0:
+            raise ValueError(f"expected a nonempty 2D array, got {_shape(a)}")
+    quant = [isinstance(a, QuantizedFactor) for a in arrays[1:]]
+    if any(quant):
+        if not all(quant):
+            raise TypeError("all inputs must have the same dtype")
+        if arrays[0].dtype != torch.bfloat16:
+            raise TypeError("fp8 factors require bfloat16 activations")
+        return
+    for a in arrays:
+        if a.dtype != arrays[0].dtype:
+            raise TypeError("all inputs must have the same dtype")
+    if arrays[0].dtype not in _ACT_CODES:
+        raise TypeError("supported dtypes are bfloat16 and float32")
+
+
+def _check_device(*tensors) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"SVD-MLP kernels run on a ROCm GPU; got tensors on {dev}")
+    for t in tensors:
+        if t.device != dev:
+            raise ValueError("all inputs must be on the same device")
+    return dev
+
+
+class _Factor:
+    """A factor prepared for the C ABI: keeps the tensor alive, records the
+    layout (natural or Linear) and the fp8 scale."""
+
+    __slots__ = ("tensor", "ptr", "linear", "scale", "scale_ptr", "rows", "cols")
+
+    def __init__(self, f):
+        if isinstance(f, QuantizedFactor):
+            data = f.data
+            if not data.is_contiguous():
+                data = data.contiguous()
+            scale = f.scale.to(torch.float32).contiguous()
+            if scale.dim() != 1 or scale.numel() != data.shape[1] or scale.device != data.device:
+                raise ValueError("fp8 factor scale must hold one value per output column")
+            self.tensor, self.linear = data, False
+            self.scale, self.scale_ptr = scale, scale.data_ptr()
+        else:
+            t = f
+            linear = False
+            if not t.is_contiguous():
+                if t.t().is_contiguous():
+                    linear = True
+                else:
+                    t = t.contiguous()
+            self.tensor, self.linear = t, linear
+            self.scale, self.scale_ptr = None, None
+        self.ptr = self.tensor.data_ptr()
+        self.rows, self.cols = int(f.shape[0]), int(f.shape[1])
+
+
+def _w_code(x: torch.Tensor, factors) -> int:
+    if isinstance(factors[0], QuantizedFactor):
+        return _lib.SVDMLP_FP8_E4M3
+    return _ACT_CODES[x.dtype]
+
+
+def _activation(x: torch.Tensor) -> torch.Tensor:
+    return x if x.is_contiguous() else x.contiguous()
+
+
+def _layout_flags(us, vs) -> int:
+    """One layout flag per factor kind; mixed layouts are made uniform."""
+    flags = 0
+    if all(f.linear for f in us):
+        flags |= _lib.SVDMLP_U_LINEAR
+    if all(f.linear for f in vs):
+        flags |= _lib.SVDMLP_V_LINEAR
+    return flags
+
+
+def _uniform(factors, linear: bool) -> None:
+    for f in factors:
+        if f.linear != linear:
+            # A mix of layouts: give the odd one out the uniform layout.
+            # f.tensor is always the logical (d_in, d_out) view.
+            f.tensor = f.tensor.t().contiguous().t() if linear else f.tensor.contiguous()
+            f.linear = linear
+            f.ptr = f.tensor.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _workspace(dev, T, d, ff, r, w_code) -> torch.Tensor:
+    nbytes = _lib.workspace_bytes(T, d, ff, r, w_code)
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+
+
+# ---------------------------------------------------------------------------
+# Operators
+# ---------------------------------------------------------------------------
+
+def fused_gate_up(x, u_gate, v_gate, u_up, v_up, *, out_transposed: bool = False) -> torch.Tensor:
+    """Returns (S, I) = silu(X @ Ug @ Vg) * (X @ Uu @ Vu) in x.dtype
+    (kernels/reference.py:54-72); (I, S) when ``out_transposed``."""
+    validate_arrays(x, u_gate, v_gate, u_up, v_up)
+    T, d = _shape(x)
+    if u_gate.shape[0] != d or v_gate.shape[0] != u_gate.shape[1]:
+        raise ValueError("X, U, V contraction dimensions do not match")
+    if _shape(u_up) != _shape(u_gate) or _shape(v_up) != _shape(v_gate):
+        raise ValueError("gate/up factors must have matching shapes")
+    r, ff = _shape(v_gate)
+    dev = _check_device(x, u_gate, v_gate, u_up, v_up)
+    lib = _lib.load()
+    x = _activation(x)
+    ug, vg, uu, vu = (_Factor(f) for f in (u_gate, v_gate, u_up, v_up))
+    _uniform((ug, uu), ug.linear and uu.linear)
+    _uniform((vg, vu), vg.linear and vu.linear)
+    flags = _layout_flags((ug, uu), (vg, vu)) | (_lib.SVDMLP_OUT_T if out_transposed else 0)
+    w_code = _w_code(x, (u_gate,))
+    out = torch.empty((ff, T) if out_transposed else (T, ff), dtype=x.dtype, device=dev)
+    ws = _workspace(dev, T, d, ff, r, w_code)
+    with torch.cuda.device(dev):
+        _lib.check(lib.svdmlp_gate_up(
+            x.data_ptr(), ug.ptr, vg.ptr, uu.ptr, vu.ptr,
+            ug.scale_ptr, vg.scale_ptr, uu.scale_ptr, vu.scale_ptr,
+            out.data_ptr(), T, d, ff, r, _ACT_CODES[x.dtype], w_code, flags,
+            ws.data_ptr(), ws.numel(), _stream(dev)))
+    return out
+
+
+def fused_xuv(x, u, v, *, x_transposed: bool = False) -> torch.Tensor:
+    """Returns (S, H) = X @ U @ V in x.dtype (kernels/reference.py:75-82).
+    With ``x_transposed`` the input is given as X^T, shape (I, S)."""
+    validate_arrays(x, u, v)
+    if x_transposed:
+        din, T = _shape(x)
+    else:
+        T, din = _shape(x)
+    if u.shape[0] != din or v.shape[0] != u.shape[1]:
+        raise ValueError("X, U, V contraction dimensions do not match")
+    r, dout = _shape(v)
+    dev = _check_device(x, u, v)
+    lib = _lib.load()
+    x = _activation(x)
+    fu, fv = _Factor(u), _Factor(v)
+    flags = _layout_flags((fu,), (fv,)) | (_lib.SVDMLP_X_T if x_transposed else 0)
+    w_code = _w_code(x, (u,))
+    out = torch.empty((T, dout), dtype=x.dtype, device=dev)
+    ws = _workspace(dev, T, din, dout, r, w_code)
+    with torch.cuda.device(dev):
+        _lib.check(lib.svdmlp_xuv(
+            x.data_ptr(), fu.ptr, fv.ptr, fu.scale_ptr, fv.scale_ptr, out.data_ptr(),
+            T, din, dout, r, _ACT_CODES[x.dtype], w_code, flags,
+            ws.data_ptr(), ws.numel(), _stream(dev)))
+    return out
+
+
+def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Full SVD SwiGLU block, fused_xuv(fused_gate_up(x)) with h rounded to
+    x.dtype in between (kernels/reference.py:85-93).  Gate/up rank and down
+    rank may differ.  ``workspace``/``out`` may be supplied to avoid
+    per-call allocation (see :func:`svd_mlp_workspace`)."""
+    validate_arrays(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
+    T, d = _shape(x)
+    if u_gate.shape[0] != d or v_gate.shape[0] != u_gate.shape[1]:
+        raise ValueError("X, U, V contraction dimensions do not match")
+    if _shape(u_up) != _shape(u_gate) or _shape(v_up) != _shape(v_gate):
+        raise ValueError("gate/up factors must have matching shapes")
+    r_gu, ff = _shape(v_gate)
+    if u_down.shape[0] != ff or v_down.shape[0] != u_down.shape[1] or v_down.shape[1] != d:
+        raise ValueError("X, U, V contraction dimensions do not match")
+    r_d = int(u_down.shape[1])
+    dev = _check_device(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
+    lib = _lib.load()
+    x = _activation(x)
+    fs = [_Factor(f) for f in (u_gate, v_gate, u_up, v_up, u_down, v_down)]
+    us, vs = (fs[0], fs[2], fs[4]), (fs[1], fs[3], fs[5])
+    _uniform(us, all(f.linear for f in us))
+    _uniform(vs, all(f.linear for f in vs))
+    flags = _layout_flags(us, vs)
+    w_code = _w_code(x, (u_gate,))
+    scale_arr = None
+    if w_code == _lib.SVDMLP_FP8_E4M3:
+        scale_arr = (ctypes.c_void_p * 6)(*[f.scale_ptr for f in fs])
+    if out is None:
+        out = torch.empty((T, d), dtype=x.dtype, device=dev)
+    elif out.shape != (T, d) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+        raise ValueError("out must be a contiguous (T, d) tensor of x.dtype on x.device")
+    if workspace is None:
+        workspace = svd_mlp_workspace(x, r=max(r_gu, r_d), ff=ff, w_code=w_code)
+    with torch.cuda.device(dev):
+        _lib.check(lib.svdmlp_svd_mlp(
+            x.data_ptr(), *(f.ptr for f in fs),
+            ctypes.addressof(scale_arr) if scale_arr is not None else None, out.data_ptr(),
+            T, d, ff, r_gu, r_d, _ACT_CODES[x.dtype], w_code, flags,
+            workspace.data_ptr(), workspace.numel(), _stream(dev)))
+    return out
+
+
+def svd_mlp_workspace(x: torch.Tensor, *, r: int, ff: int, w_code: int | None = None) -> torch.Tensor:
+    """Allocate the workspace svd_mlp needs for x's shape (reusable)."""
+    T, d = _shape(x)
+    code = _lib.SVDMLP_BF16 if w_code is None else w_code
+    return _workspace(x.device, T, d, ff, r, code)
+
+
+# ---------------------------------------------------------------------------
+# Host helpers of kernels/reference.py
+# ---------------------------------------------------------------------------
+
+def low_rank_dim(hidden_size: int, intermediate_size: int, compress_ratio: float) -> int:
+    """SVD rank aligned to 128 (kernels/reference.py:21-34): Python's
+    round-half-to-even of I*H*c / ((I+H)*128), times 128."""
+    numer = intermediate_size * hidden_size * compress_ratio
+    denom = (intermediate_size + hidden_size) * 128
+    return round(numer / denom) * 128
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """x * sigmoid(x) computed in float32 (kernels/reference.py:37-51)."""
+    return torch.nn.functional.silu(x.float())

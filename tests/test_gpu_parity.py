@@ -1,0 +1,229 @@
+"""Parity of the HIP kernels (through libsvdmlp.so's C ABI) with the CPU
+oracle on seeded inputs.
+
+Tolerances (relative Frobenius error against the oracle's math on the same
+inputs): bf16 1e-2 and fp8 3e-2; fp32 1e-4
+element-wise (tests_test_speedup_migration.py.before:23-25).  Full-size
+shapes are checked on a row subset: the rows of the layer are independent, so
+any subset is an exact parity check of those rows.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from svdmlp import compat, fp8, inputs, ops
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+FP8_TOL = 3e-2
+
+
+def _to(a, dtype, dev):
+    return inputs.to_torch(a, dtype, dev)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def _rounded(arrs, dtype):
+    return [inputs.as_float32(a, dtype) for a in arrs]
+
+
+def _rel(got, ref):
+    return O.relative_l2(got, ref)
+
+
+def _small(shapes, seed=123):
+    rng = np.random.default_rng(seed)
+    return [(rng.normal(size=s) / np.sqrt(s[0])).astype(np.float32) for s in shapes]
+
+
+# ---------------------------------------------------------------------------
+# small and odd shapes (tests_test_speedup_migration.py.before:47-92)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("S,H,R,I", [(1, 129, 131, 137), (129, 257, 257, 513), (3, 64, 32, 96)])
+def test_fused_gate_and_down_tail_blocks_fp32(gpu, S, H, R, I):
+    x, ug, vg, uu, vu, ud, vd = _small([(S, H), (H, R), (R, I), (H, R), (R, I), (I, R), (R, H)])
+    t = [_to(a, torch.float32, gpu) for a in (x, ug, vg, uu, vu, ud, vd)]
+    got_t = compat.fused_mlp_up_T(t[0], t[1], t[2], t[3], t[4])
+    hidden = O.fused_gate_up_ref(x, ug, vg, uu, vu)
+    assert tuple(got_t.shape) == (I, S)
+    np.testing.assert_allclose(_np(got_t), hidden.T, atol=1e-4, rtol=1e-4)
+    got = compat.fused_three_mm_XTUV(got_t, t[5], t[6])
+    assert tuple(got.shape) == (S, H)
+    np.testing.assert_allclose(_np(got), O.fused_xuv_ref(hidden, ud, vd), atol=1e-4, rtol=1e-4)
+
+
+def test_multiple_inner_tiles_fp32(gpu):
+    x, ug, vg, uu, vu = _small([(257, 513), (513, 513), (513, 1025), (513, 513), (513, 1025)])
+    t = [_to(a, torch.float32, gpu) for a in (x, ug, vg, uu, vu)]
+    got = compat.fused_mlp_up_T(*t, M_tiles_in_block=2, r_tiles_in_block=2, K_tiles_in_block=2,
+                                N_tiles_in_block=2, async_dma=False)
+    np.testing.assert_allclose(_np(got), O.fused_gate_up_ref(x, ug, vg, uu, vu).T, atol=1e-4, rtol=1e-4)
+
+
+def test_wrappers_preserve_pytorch_weight_order_fp32(gpu):
+    x, uu, vu, ug, vg, ud, vd = _small([(1, 129), (129, 131), (131, 137), (129, 131), (131, 137),
+                                        (137, 131), (131, 129)])
+    t = [_to(a, torch.float32, gpu) for a in (x, uu, vu, ug, vg, ud, vd)]
+    # nki_mm takes PyTorch Linear weights (out, in): contiguous transposes.
+    lin = [a.t().contiguous() for a in t[1:]]
+    got = compat.nki_mm(t[0], *lin)
+    expected = O.unfused_reference(x, uu, vu, ug, vg, ud, vd)
+    np.testing.assert_allclose(_np(got), expected, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("S,H,R,I", [(5, 136, 64, 200), (130, 256, 136, 520), (64, 128, 64, 256)])
+def test_bf16_small_shapes_all_entry_points(gpu, S, H, R, I):
+    f = _rounded(_small([(S, H), (H, R), (R, I), (H, R), (R, I), (I, R), (R, H)], seed=S), torch.bfloat16)
+    x, ug, vg, uu, vu, ud, vd = f
+    t = [_to(a, torch.bfloat16, gpu) for a in f]
+    h_ref = O.fused_gate_up_ref(x, ug, vg, uu, vu, "bfloat16")
+    assert _rel(_np(ops.fused_gate_up(t[0], t[1], t[2], t[3], t[4])), h_ref) < BF16_TOL
+    assert _rel(_np(ops.fused_xuv(_to(h_ref, torch.bfloat16, gpu), t[5], t[6])),
+                O.fused_xuv_ref(h_ref, ud, vd, "bfloat16")) < BF16_TOL
+    assert _rel(_np(ops.svd_mlp(*t)), O.svd_mlp_ref(*f, dtype="bfloat16")) < BF16_TOL
+
+
+def test_bf16_odd_shapes_take_the_unaligned_path(gpu):
+    f = _rounded(_small([(7, 129), (129, 131), (131, 137), (129, 131), (131, 137), (137, 131), (131, 129)]),
+                 torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in f]
+    assert _rel(_np(ops.svd_mlp(*t)), O.svd_mlp_ref(*f, dtype="bfloat16")) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------
+# the tiny layer (T=128, d=1024, ff=3584, r=256), fp32
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def tiny():
+    x, f = inputs.make_layer(inputs.SHAPES["tiny"], T=128, seed=0)
+    return x, f
+
+
+def test_tiny_config_fp32(gpu, tiny):
+    x, f = tiny
+    t = [_to(a, torch.float32, gpu) for a in (x, *f)]
+    got = _np(ops.svd_mlp(*t))
+    ref = O.svd_mlp_ref(x, *f)
+    np.testing.assert_allclose(got, ref, atol=1e-4, rtol=1e-4)
+    assert _rel(got, ref) < 1e-5
+    h = _np(ops.fused_gate_up(*t[:5]))
+    np.testing.assert_allclose(h, O.fused_gate_up_ref(x, *f[:4]), atol=1e-4, rtol=1e-4)
+
+
+def test_tiny_config_bf16(gpu, tiny):
+    x, f = tiny
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    got = _np(ops.svd_mlp(*t))
+    err = _rel(got, O.svd_mlp_ref(xb, *fb, dtype="bfloat16"))
+    assert err < BF16_TOL, err
+    # and against the fp32 golden arm of test_speedup.py (unrounded h)
+    assert _rel(got, O.unfused_reference(xb, fb[2], fb[3], fb[0], fb[1], fb[4], fb[5])) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs 2 and 3: LLaMA3-8B layer, prefill T=1024 and decode T<=64
+# ---------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def layer8b(gpu):
+    shape = inputs.SHAPES["8b"]
+    f = _rounded(inputs.make_factors(shape, seed=0), torch.bfloat16)
+    ft = [_to(a, torch.bfloat16, gpu) for a in f]
+    return shape, f, ft
+
+
+def _x(T, d, seed):
+    return inputs.as_float32(inputs.make_x(np.random.default_rng(seed), T, d), torch.bfloat16)
+
+
+def test_8b_prefill_T1024_row_subset(gpu, layer8b):
+    shape, f, ft = layer8b
+    x = _x(1024, shape.d, 11)
+    xt = _to(x, torch.bfloat16, gpu)
+    y = ops.svd_mlp(xt, *ft)
+    rows = np.r_[0:16, 120:136, 1008:1024, np.random.default_rng(0).choice(1024, 16, replace=False)]
+    ref = O.svd_mlp_ref(x[rows], *f, dtype="bfloat16")
+    got = _np(y)[rows]
+    err = _rel(got, ref)
+    print(f"8b T=1024 svd_mlp rel_l2={err:.3e}")
+    assert err < BF16_TOL
+    assert np.isfinite(_np(y)).all()
+    h = ops.fused_gate_up(xt, *ft[:4])
+    err_h = _rel(_np(h)[rows], O.fused_gate_up_ref(x[rows], *f[:4], dtype="bfloat16"))
+    assert err_h < BF16_TOL, err_h
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 64])
+def test_8b_decode(gpu, layer8b, T):
+    shape, f, ft = layer8b
+    x = _x(T, shape.d, 100 + T)
+    xt = _to(x, torch.bfloat16, gpu)
+    ref = O.svd_mlp_ref(x, *f, dtype="bfloat16")
+    err = _rel(_np(ops.svd_mlp(xt, *ft)), ref)
+    print(f"8b decode T={T} rel_l2={err:.3e}")
+    assert err < BF16_TOL
+    h_ref = O.fused_gate_up_ref(x, *f[:4], dtype="bfloat16")
+    h = ops.fused_gate_up(xt, *ft[:4])
+    assert _rel(_np(h), h_ref) < BF16_TOL
+    y = ops.fused_xuv(_to(h_ref, torch.bfloat16, gpu), ft[4], ft[5])
+    assert _rel(_np(y), O.fused_xuv_ref(h_ref, f[4], f[5], "bfloat16")) < BF16_TOL
+
+
+def test_decode_and_prefill_paths_agree(gpu, layer8b):
+    """T=64 runs the decode kernels, T=128 the tiled GEMMs; the first 64 rows
+    of the two must agree with each other and with the oracle."""
+    shape, f, ft = layer8b
+    x = _x(128, shape.d, 7)
+    y128 = _np(ops.svd_mlp(_to(x, torch.bfloat16, gpu), *ft))
+    y64 = _np(ops.svd_mlp(_to(x[:64], torch.bfloat16, gpu), *ft))
+    ref = O.svd_mlp_ref(x[:64], *f, dtype="bfloat16")
+    assert _rel(y64, ref) < BF16_TOL and _rel(y128[:64], ref) < BF16_TOL
+    assert _rel(y64, y128[:64]) < 5e-3
+
+
+def test_linear_layout_weights_bf16(gpu, layer8b):
+    """nki_mm-style (out, in) weights: the .T views reach the kernels
+    without copies; prefill and decode paths."""
+    shape, f, ft = layer8b
+    lin = [a.t().contiguous().t() for a in ft]   # (in, out) views over (out, in) storage
+    for T in (8, 256):
+        x = _x(T, shape.d, 300 + T)
+        rows = np.arange(min(T, 24))
+        got = _np(ops.svd_mlp(_to(x, torch.bfloat16, gpu), *lin))[rows]
+        assert _rel(got, O.svd_mlp_ref(x[rows], *f, dtype="bfloat16")) < BF16_TOL, T
+
+
+def test_replay_is_stable(gpu, layer8b):
+    shape, f, ft = layer8b
+    xt = _to(_x(1024, shape.d, 5), torch.bfloat16, gpu)
+    a = ops.svd_mlp(xt, *ft).float()
+    b = ops.svd_mlp(xt, *ft).float()
+    # split-K partial sums use fp32 atomics: replays agree to rounding.
+    assert torch.linalg.norm(a - b) / torch.linalg.norm(a) < 1e-3
+
+
+# ---------------------------------------------------------------------------
+# BASELINE config 5 (scaled down): fp8 e4m3 factors, bf16 activations
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T", [8, 256])
+def test_fp8_factors(gpu, T):
+    shape = inputs.LayerShape(1024, 2048, 512)
+    x, f = inputs.make_layer(shape, T=T, seed=9)
+    xb = inputs.as_float32(x, torch.bfloat16)
+    q = [fp8.quantize_per_channel(torch.from_numpy(a)) for a in f]
+    deq = [O.e4m3_decode(qq.data.view(torch.uint8).numpy()) * qq.scale.numpy() for qq in q]
+    qg = [ops.QuantizedFactor(qq.data.to(gpu), qq.scale.to(gpu)) for qq in q]
+    got = _np(ops.svd_mlp(_to(xb, torch.bfloat16, gpu), *qg))
+    err = _rel(got, O.svd_mlp_ref(xb, *deq, dtype="bfloat16"))
+    print(f"fp8 T={T} rel_l2={err:.3e}")
+    assert err < FP8_TOL

@@ -1,0 +1,176 @@
+"""Host-side contract of the package (no GPU): the reference's validation
+messages and exception types, block-parameter tables, VMEM budget checks,
+rank helpers and seeded generators."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from svdmlp import compat, config, inputs, ops
+
+
+def _t(shape, dtype=torch.float32):
+    return torch.zeros(shape, dtype=dtype)
+
+
+# ---------------------------------------------------------------------------
+# validation (test_speedup.py:37-49,508-509,530-533;
+# tests_test_speedup_migration.py.before:122-132)
+# ---------------------------------------------------------------------------
+
+def test_invalid_configuration_rejected_before_launch():
+    a = _t((8, 128))
+    b = _t((128, 128))
+    with pytest.raises(ValueError, match="positive integer"):
+        compat.fused_mlp_up_T(a, b, b, b, b, M_tiles_in_block=0)
+    with pytest.raises(ValueError, match="VMEM"):
+        compat.fused_mlp_up_T(a, b, b, b, b, M_tiles_in_block=1024)
+    with pytest.raises(ValueError, match="matching shapes"):
+        compat.fused_mlp_up_T(a, b, b, b[:, :64], b)
+    with pytest.raises(TypeError, match="same dtype"):
+        compat.fused_three_mm_XTUV(a.T, b, b.to(torch.bfloat16))
+
+
+def test_validation_messages_of_the_operator_api():
+    x, u, v = _t((4, 16)), _t((16, 8)), _t((8, 32))
+    with pytest.raises(ValueError, match="nonempty 2D array"):
+        ops.fused_xuv(_t((0, 16)), u, v)
+    with pytest.raises(ValueError, match="nonempty 2D array"):
+        ops.fused_xuv(_t((4, 16, 1)), u, v)
+    with pytest.raises(TypeError, match="supported dtypes are bfloat16 and float32"):
+        ops.fused_xuv(x.half(), u.half(), v.half())
+    with pytest.raises(ValueError, match="contraction dimensions do not match"):
+        ops.fused_xuv(x, _t((15, 8)), v)
+    with pytest.raises(ValueError, match="contraction dimensions do not match"):
+        ops.fused_gate_up(x, u, _t((7, 32)), u, v)
+    with pytest.raises(ValueError, match="gate/up factors must have matching shapes"):
+        ops.fused_gate_up(x, u, v, u, _t((8, 31)))
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    x, u, v = _t((4, 16)), _t((16, 8)), _t((8, 32))
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        ops.fused_xuv(x, u, v)
+
+
+def test_interpret_mode_has_no_cpu_fallback():
+    a = _t((8, 128))
+    b = _t((128, 128))
+    with pytest.raises(NotImplementedError, match="GPU only"):
+        compat.fused_mlp_up_T(a, b, b, b, b, interpret=True)
+
+
+def test_down_backend_validated():
+    a = _t((8, 128))
+    b = _t((128, 128))
+    with pytest.raises(ValueError, match="down_backend"):
+        compat.svd_mlp_with_fused_kernel(a, b, b, b, b, b, b, down_backend="xla")
+
+
+def test_fp8_factors_require_bf16_activations():
+    q = ops.QuantizedFactor(torch.zeros((16, 8), dtype=torch.float8_e4m3fn), torch.ones(8))
+    qv = ops.QuantizedFactor(torch.zeros((8, 32), dtype=torch.float8_e4m3fn), torch.ones(32))
+    with pytest.raises(TypeError, match="bfloat16"):
+        ops.fused_xuv(_t((4, 16)), q, qv)
+    with pytest.raises(TypeError, match="same dtype"):
+        ops.fused_xuv(_t((4, 16), torch.bfloat16), q, _t((8, 32), torch.bfloat16))
+
+
+# ---------------------------------------------------------------------------
+# block parameters and the VMEM budget (test_speedup.py:169-317)
+# ---------------------------------------------------------------------------
+
+def test_block_param_tables():
+    assert compat.get_fused_mlp_up_T_params(128) == dict(
+        M_tiles_in_block=4, r_tiles_in_block=2, K_tiles_in_block=1, N_tiles_in_block=2)
+    assert compat.get_fused_mlp_up_T_params(1024) == dict(
+        M_tiles_in_block=2, r_tiles_in_block=2, K_tiles_in_block=4, N_tiles_in_block=1)
+    assert compat.get_fused_mlp_up_T_params(600)["K_tiles_in_block"] == 2
+    assert compat.get_fused_three_mm_XTUV_params(1024)["K_tiles_in_block"] == 2
+    assert compat.get_fused_three_mm_XTUV_params(2048)["K_tiles_in_block"] == 4
+    with pytest.raises(ValueError, match="positive integer"):
+        compat.get_fused_mlp_up_T_params(0)
+    with pytest.raises(ValueError, match="positive integer"):
+        compat.get_fused_three_mm_XTUV_params(True)
+
+
+@pytest.mark.parametrize("S", [1, 8, 13, 127, 128, 129, 512, 1024])
+def test_default_vmem_for_target_models(S):
+    # tests_test_speedup_migration.py.before:110-119
+    for H, I, R in [(3072, 8192, 1792), (4096, 14336, 2560)]:
+        for gate, M, N, params in [(True, H, I, compat.get_fused_mlp_up_T_params(S)),
+                                   (False, I, H, compat.get_fused_three_mm_XTUV_params(S))]:
+            shape = compat._fusion_shape(M, R, S, N, torch.bfloat16, params["M_tiles_in_block"],
+                                         params["r_tiles_in_block"], params["K_tiles_in_block"],
+                                         params["N_tiles_in_block"], gate)
+            assert shape.vmem_bytes < compat.VMEM_LIMIT * compat.VMEM_HEADROOM
+
+
+def test_async_vmem_budget_includes_second_weight_slot():
+    # tests_test_speedup_migration.py.before:236-240
+    args = (513, 513, 257, 1025, torch.float32, 2, 2, 2, 2, True)
+    compat._fusion_shape(*args, async_dma=False)
+    with pytest.raises(ValueError, match="VMEM"):
+        compat._fusion_shape(*args, async_dma=True)
+
+
+def test_fusion_shape_padding():
+    s = compat._fusion_shape(4096, 2816, 1024, 14336, torch.bfloat16, 2, 2, 4, 1, True)
+    assert (s.M_block, s.r_block, s.K_block, s.N_block) == (512, 512, 512, 512)
+    assert (s.M_padded, s.r_padded, s.K_padded, s.N_padded) == (4096, 2816, 1024, 14336)
+
+
+# ---------------------------------------------------------------------------
+# model tables and ranks
+# ---------------------------------------------------------------------------
+
+def test_models_and_rank_for():
+    m = config.MODELS["llama-3.1-8b"]
+    assert (m.hidden_size, m.intermediate_size, m.num_layers) == (4096, 14336, 32)
+    assert m.rank_at_080 == 2560
+    assert config.rank_for(m, 0.9) == 2816
+    assert config.MODELS["llama-3.2-3b"].rank_at_080 == 1792
+    with pytest.raises(ValueError, match="compress-ratio"):
+        config.rank_for(m, 0.0)
+    for H, I, c in [(2048, 8192, 0.8), (4096, 14336, 0.9), (640, 640, 1.0), (896, 896, 1.0)]:
+        assert ops.low_rank_dim(H, I, c) == O.low_rank_dim(H, I, c)
+
+
+def test_gate_up_blocks_namedtuple():
+    b = config.GateUpBlocks(bs=128, bh=1024, br=512, bn=512)
+    assert b._asdict() == dict(bs=128, bh=1024, br=512, bn=512)
+
+
+# ---------------------------------------------------------------------------
+# seeded inputs (test_speedup.py:803-835)
+# ---------------------------------------------------------------------------
+
+def test_generator_order_and_scale():
+    shape = inputs.LayerShape(64, 96, 32)
+    ug, vg, uu, vu, ud, vd = inputs.make_factors(shape, seed=5)
+    rng = np.random.default_rng(5)
+    first = rng.normal(size=(64, 32)).astype(np.float32) / np.float32(8.0)
+    np.testing.assert_array_equal(uu, first)          # u_up is drawn first
+    assert ug.shape == (64, 32) and vg.shape == (32, 96) and ud.shape == (96, 32) and vd.shape == (32, 64)
+    big = inputs.make_factors(inputs.LayerShape(1024, 1024, 512), seed=0)
+    assert abs(big[0].std() - 1 / 32) < 1e-3            # N(0, 1/d_in)
+    assert abs(big[1].std() - 1 / np.sqrt(512)) < 1e-3  # N(0, 1/r)
+
+
+def test_stack_ranks_are_seeded_and_in_set():
+    a = inputs.stack_ranks(32, seed=3)
+    assert a == inputs.stack_ranks(32, seed=3)
+    assert len(a) == 32 and all(r in (2048, 2304, 2560, 2816, 3072) for pair in a for r in pair)
+    g = inputs.stack_gains(4, 128)
+    assert g.shape == (4, 128) and g.min() >= 0.9 and g.max() <= 1.1
+
+
+def test_quantizer_matches_oracle_codec():
+    from svdmlp import fp8
+
+    w = (np.random.default_rng(2).normal(size=(256, 64)) / 16).astype(np.float32)
+    q = fp8.quantize_per_channel(torch.from_numpy(w))
+    q_ref, s_ref = O.quantize_per_channel(w, axis=0)
+    np.testing.assert_allclose(q.scale.numpy(), s_ref, rtol=1e-6)
+    np.testing.assert_array_equal(q.data.view(torch.uint8).numpy(), q_ref)
