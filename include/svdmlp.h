@@ -104,6 +104,20 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
                    int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
                    int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
 
+/*
+ * Per-stage GPU timing (no counterpart in the reference, whose timing is host
+ * wall clock around block_until_ready, test_speedup.py:739-749).  While
+ * enabled, every stage launch of the calls above is bracketed by hipEvents
+ * on the caller's stream.  svdmlp_profile_read waits for the recorded events,
+ * writes per-stage total milliseconds and launch counts for the first n
+ * stages, clears the totals and returns the number of stages (or a negative
+ * status).  svdmlp_stage_name names stage i ("" when out of range).
+ * svdmlp_profile_enable returns the number of stages.
+ */
+int svdmlp_profile_enable(int enable);
+int svdmlp_profile_read(double* total_ms, int64_t* launches, int n);
+const char* svdmlp_stage_name(int stage);
+
 #ifdef __cplusplus
 }
 #endif

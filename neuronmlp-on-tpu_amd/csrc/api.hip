@@ -14,9 +14,14 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
+#include <vector>
+
+#include <cstdlib>
 
 #include "dispatch.hpp"
+#include "gemm_big.hpp"
 #include "svdmlp.h"
 
 using namespace svdmlp;
@@ -45,6 +50,83 @@ int check(hipError_t e, const char* what, const char* why = nullptr) {
   return SVDMLP_EHIP;
 }
 
+// ---------------------------------------------------------------------------
+// Optional per-stage GPU timing: hipEvents recorded on the caller's stream
+// around each stage launch while enabled (svdmlp_profile_enable).
+// ---------------------------------------------------------------------------
+enum Stage : int {
+  ST_ZERO = 0,
+  ST_GU_XU,
+  ST_GU_XUV,
+  ST_D_XU,
+  ST_D_XUV,
+  ST_DEC_GU_XU,
+  ST_DEC_GU_XUV,
+  ST_DEC_D_XU,
+  ST_DEC_D_XUV,
+  ST_FINALIZE,
+  ST_GU_XUV_G,
+  ST_COUNT
+};
+const char* const kStageNames[ST_COUNT] = {
+    "zero_fill",        "gate_up_xu",       "gate_up_xuv_swiglu", "down_xu",           "down_xuv",
+    "decode_gate_up_xu", "decode_gate_up_xuv", "decode_down_xu",   "decode_down_xuv", "finalize",
+    "gate_up_xuv_g"};
+
+struct Profiler {
+  std::mutex mu;
+  bool on = false;
+  struct Rec {
+    int stage;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> pending;
+  std::vector<hipEvent_t> pool;
+  double total_ms[ST_COUNT] = {};
+  int64_t count[ST_COUNT] = {};
+
+  hipEvent_t get() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+Profiler g_prof;
+
+// Brackets one stage launch with events when profiling is enabled.
+struct StageScope {
+  int stage;
+  hipStream_t st;
+  hipEvent_t a = nullptr, b = nullptr;
+  StageScope(int s, hipStream_t stream) : stage(s), st(stream) {
+    std::lock_guard<std::mutex> g(g_prof.mu);
+    if (!g_prof.on) return;
+    a = g_prof.get();
+    b = g_prof.get();
+    if (!a || !b || hipEventRecord(a, st) != hipSuccess) {
+      if (a) g_prof.pool.push_back(a);
+      if (b) g_prof.pool.push_back(b);
+      a = b = nullptr;
+    }
+  }
+  ~StageScope() {
+    if (!a) return;
+    const bool ok = hipEventRecord(b, st) == hipSuccess;
+    std::lock_guard<std::mutex> g(g_prof.mu);
+    if (ok) {
+      g_prof.pending.push_back({stage, a, b});
+    } else {
+      g_prof.pool.push_back(a);
+      g_prof.pool.push_back(b);
+    }
+  }
+};
+
 size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
 
 struct Ws {
@@ -53,8 +135,11 @@ struct Ws {
   size_t gu32;     // [2][T][big] fp32 gate/up sums (decode)
   size_t h;        // [T][big] h of the fused layer (4 bytes/elem worst case)
   size_t y32;      // [T][big] fp32 output accumulator (decode)
+  size_t part;     // [splits][batch][T][N] fp32 split-K partial slices (prefill)
   size_t total;
 };
+
+int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch);
 
 Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   const int64_t big = std::max(d, ff);
@@ -70,7 +155,17 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   w.h = off;
   off += a256(T * big * 4);
   w.y32 = off;
-  off += dec ? a256(T * big * 4) : 0;
+  off += a256(T * big * 4);
+  // split-K partial slices of the large-tile stages: X.U (gate/up, batch 2),
+  // h.Ud, XU.V (both output widths), sized by the same planner the launches use
+  int64_t part = 0;
+  const int64_t stages[][4] = {{d, r, 2, 8}, {ff, r, 1, 8}, {r, d, 1, 8}, {r, ff, 1, 8}, {r, d, 1, 4}, {r, ff, 1, 4}};
+  for (const auto& st : stages) {
+    const int sp = plan_splits(T, st[0], st[1], (int)st[3], (int)st[2]);
+    if (sp > 1) part = std::max(part, (int64_t)sp * st[2] * T * st[1] * 4);
+  }
+  w.part = off;
+  off += a256(part);
   w.total = off;
   return w;
 }
@@ -132,6 +227,7 @@ int prefill_xu(const Common& c, const Operand& a, bool a_kc, const void* const* 
   GemmDesc d{c.f32, c.f32 ? SRC_F32 : SRC_BF16, srcb_of(c.wt), a_kc, u_lin, 1, EPI_STORE, false, c.f32, vec};
   float* xu32 = reinterpret_cast<float*>(ws + L.xu32) + (int64_t)xu_slot * T * r;
   if (splits > 1) {
+    StageScope z(ST_ZERO, c.st);
     int rc = check(launch_fill_zero(xu32, (int64_t)batch * T * r, c.st), "zero rank-r accumulator");
     if (rc) return rc;
     d.epi = EPI_ATOMIC;
@@ -149,6 +245,7 @@ int prefill_xu(const Common& c, const Operand& a, bool a_kc, const void* const* 
   }
   *xu_bstride = p.out_bstride;
   const char* why = nullptr;
+  StageScope ss(batch == 2 ? ST_GU_XU : ST_D_XU, c.st);
   return check(gemm_launch(d, p, splits, batch, c.st, &why), "XU stage", why);
 }
 
@@ -174,6 +271,7 @@ int prefill_swiglu(const Common& c, int a_src, const void* xu, int64_t xu_bstrid
   p.k_split = r;
   GemmDesc d{c.f32, a_src, srcb_of(c.wt), true, v_lin, 2, EPI_SWIGLU, out_t, c.f32, vec};
   const char* why = nullptr;
+  StageScope ss(ST_GU_XUV, c.st);
   return check(gemm_launch(d, p, 1, 1, c.st, &why), "gate/up XUV stage", why);
 }
 
@@ -194,7 +292,169 @@ int prefill_v(const Common& c, int a_src, const void* xu, const void* v, const f
   p.k_split = r;
   GemmDesc d{c.f32, a_src, srcb_of(c.wt), true, v_lin, 1, EPI_STORE, false, c.f32, vec};
   const char* why = nullptr;
+  StageScope ss(ST_D_XUV, c.st);
   return check(gemm_launch(d, p, 1, 1, c.st, &why), "XUV stage", why);
+}
+
+// ---------------------------------------------------------------------------
+// Large-tile prefill path (bf16 activations and factors, aligned shapes)
+// ---------------------------------------------------------------------------
+
+// Tile choices; SVDMLP_TUNE="s1=44,s4=88,split=256" overrides them (read once).
+struct Tune {
+  int s1 = 8;         // X.U stages: block tile 256 x 32*s1
+  int s4 = 4;         // XU.V of the down half: 256 x 32*s4, or 0 = 256x256 split-K
+  int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 7 when ff % 224 == 0)
+  int split = 256;    // split-K target block count
+  bool big = true;    // large-tile path enabled
+};
+
+const Tune& tune() {
+  static const Tune t = [] {
+    Tune r;
+    const char* e = getenv("SVDMLP_TUNE");
+    if (!e) return r;
+    std::string str(e);
+    size_t pos = 0;
+    while (pos < str.size()) {
+      size_t end = str.find(',', pos);
+      if (end == std::string::npos) end = str.size();
+      const std::string kv = str.substr(pos, end - pos);
+      const size_t eq = kv.find('=');
+      if (eq != std::string::npos) {
+        const std::string k = kv.substr(0, eq);
+        const int v = atoi(kv.c_str() + eq + 1);
+        if (k == "s1") r.s1 = v;
+        if (k == "s4") r.s4 = v;
+        if (k == "s2fn") r.s2fn = v;
+        if (k == "split") r.split = v;
+        if (k == "big") r.big = v != 0;
+      }
+      pos = end + 1;
+    }
+    return r;
+  }();
+  return t;
+}
+
+bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes) {
+  if (c.f32 || c.wt != SVDMLP_BF16 || !vec || !tune().big) return false;
+  for (int64_t b : bytes)
+    if (b >= ((int64_t)1 << 31)) return false;
+  return true;
+}
+
+int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
+             const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
+             int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
+             bool out_f32 = false, int64_t out_sstride = 0) {
+  BigParams p{};
+  p.a[0] = a0;
+  p.a[1] = a1 ? a1 : a0;
+  p.b[0] = b0;
+  p.b[1] = b1 ? b1 : b0;
+  p.a_bytes[0] = p.a_bytes[1] = (uint32_t)a_bytes;
+  p.b_bytes[0] = p.b_bytes[1] = (uint32_t)b_bytes;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.out = out;
+  p.ldo = ldo;
+  p.out_bstride = out_bstride;
+  p.out_sstride = out_sstride;
+  p.gmem = gmem;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.mtiles = (M + 255) / 256;
+  p.ntiles = (N + 32 * fn - 1) / (32 * fn);
+  p.k_split = k_split;
+  const int splits = (K + k_split - 1) / k_split;
+  const BigDesc d{fn, b_kc, epi, out_f32};
+  const char* why = nullptr;
+  StageScope ss(stage, c.st);
+  return check(launch_big(d, p, splits, batch, c.st, &why), "large-tile GEMM", why);
+}
+
+int pick_splits(int tiles, int K) {
+  const int target = tune().split;
+  if (4 * tiles >= 3 * target) return 1;
+  const int s = (target + tiles - 1) / tiles;
+  return std::max(1, std::min(s, K / 256));
+}
+
+}  // namespace
+
+namespace {
+
+// K elements per split for the large-tile stages (a multiple of the 64-k
+// stage); the number of splits launched is ceil(K / k_split), and the same
+// count sizes the workspace and the reduction.
+int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch) {
+  const int64_t tiles = ((T + 255) / 256) * ((N + 32 * fn - 1) / (32 * fn)) * batch;
+  const int s = pick_splits((int)std::min<int64_t>(tiles, 1 << 20), (int)K);
+  const int64_t ks = ((K + s - 1) / s + 63) / 64 * 64;
+  return (int)ks;
+}
+
+int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
+  const int64_t ks = plan_ksplit(T, K, N, fn, batch);
+  return (int)((K + ks - 1) / ks);
+}
+
+// XU_b = A . U_b (b < batch) into bf16 ws.xu_bf16, batch stride T*r.  With
+// too few output tiles for the chip, K is split: each split writes an fp32
+// slice (plain stores) and one pass sums the slices in order into bf16.
+int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
+           int T, int K, int r, int batch, char* ws, const Ws& L) {
+  const int fn = tune().s1;
+  const int ks = plan_ksplit(T, K, r, fn, batch);
+  const int splits = (K + ks - 1) / ks;
+  uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
+  const int64_t u_bytes = (int64_t)K * r * 2;
+  const void* u1 = batch > 1 ? u[1] : u[0];
+  if (splits == 1)
+    return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, u_lin ? K : r, u_bytes, u_lin, T, r, K, batch, fn,
+                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  const int64_t slice = (int64_t)batch * T * r;
+  int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, u_lin ? K : r, u_bytes, u_lin, T, r, K, batch, fn,
+                    BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice);
+  if (rc) return rc;
+  StageScope fin(ST_FINALIZE, c.st);
+  return check(launch_reduce_bf16(part, splits, slice, xu, slice, c.st), "split-K reduce");
+}
+
+// out = SiLU(XUg . Vg) * (XUu . Vu): a g pass (bf16 g to the workspace) and a
+// u pass whose epilogue applies SiLU(g) * u.
+int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, const void* vg, const void* vu,
+               bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out) {
+  int fn = tune().s2fn;
+  if (fn == 0) fn = (ff % 224 == 0) ? 7 : 8;
+  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * ff * 2;
+  int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r,
+                    1, fn, BEPI_STORE, r, gbuf, ff, 0, nullptr);
+  if (rc) return rc;
+  return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r, 1,
+                  fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf);
+}
+
+// y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
+int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T, int r, int dout, char* ws,
+          const Ws& L, void* y) {
+  const int fn = tune().s4 > 0 ? tune().s4 : 8;
+  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * dout * 2;
+  const int ks = tune().s4 > 0 && tune().s4 != 8 ? r : plan_ksplit(T, r, dout, fn, 1);
+  const int splits = (r + ks - 1) / ks;
+  if (splits == 1)
+    return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, v_lin ? r : dout, v_bytes, v_lin, T, dout, r, 1,
+                    fn, BEPI_STORE, r, y, dout, 0, nullptr);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  const int64_t slice = (int64_t)T * dout;
+  int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, v_lin ? r : dout, v_bytes, v_lin, T, dout, r,
+                    1, fn, BEPI_STORE, ks, part, dout, 0, nullptr, true, slice);
+  if (rc) return rc;
+  StageScope fin(ST_FINALIZE, c.st);
+  return check(launch_reduce_bf16(part, splits, slice, static_cast<uint16_t*>(y), slice, c.st), "split-K reduce");
 }
 
 // ---------------------------------------------------------------------------
@@ -203,8 +463,9 @@ int prefill_v(const Common& c, int a_src, const void* xu, const void* v, const f
 
 int decode_mt(int64_t T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
 
-int decode_stage(const Common& c, int T, int K, int nseg, const Operand* a, int srca, const void* const* w,
-                 const float* const* sw, bool w_lin, const int* N, float* const* out, const char* what) {
+int decode_stage(const Common& c, int stage, int T, int K, int nseg, const Operand* a, int srca,
+                 const void* const* w, const float* const* sw, bool w_lin, const int* N, float* const* out,
+                 const char* what) {
   DecodeParams p{};
   p.nseg = nseg;
   p.T = T;
@@ -229,6 +490,7 @@ int decode_stage(const Common& c, int T, int K, int nseg, const Operand* a, int 
   const int splits = (int)(((int64_t)K + ks - 1) / ks);
   DecodeDesc d{decode_mt(T), srca, srcb_of(c.wt), w_lin};
   const char* why = nullptr;
+  StageScope ss(stage, c.st);
   return check(launch_decode(d, p, tiles * splits, c.st, &why), what, why);
 }
 
@@ -256,6 +518,44 @@ extern "C" {
 int svdmlp_version(void) { return SVDMLP_VERSION; }
 
 const char* svdmlp_last_error(void) { return g_err.c_str(); }
+
+int svdmlp_profile_enable(int enable) {
+  std::lock_guard<std::mutex> g(g_prof.mu);
+  g_prof.on = enable != 0;
+  return ST_COUNT;
+}
+
+const char* svdmlp_stage_name(int stage) {
+  return (stage >= 0 && stage < ST_COUNT) ? kStageNames[stage] : "";
+}
+
+int svdmlp_profile_read(double* total_ms, int64_t* launches, int n) {
+  std::lock_guard<std::mutex> g(g_prof.mu);
+  int rc = SVDMLP_OK;
+  for (auto& r : g_prof.pending) {
+    float ms = 0.f;
+    hipError_t e = hipEventSynchronize(r.b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
+    if (e != hipSuccess) {
+      rc = check(e, "profile read");
+    } else {
+      g_prof.total_ms[r.stage] += ms;
+      g_prof.count[r.stage] += 1;
+    }
+    g_prof.pool.push_back(r.a);
+    g_prof.pool.push_back(r.b);
+  }
+  g_prof.pending.clear();
+  for (int i = 0; i < n && i < ST_COUNT; ++i) {
+    if (total_ms) total_ms[i] = g_prof.total_ms[i];
+    if (launches) launches[i] = g_prof.count[i];
+  }
+  for (int i = 0; i < ST_COUNT; ++i) {
+    g_prof.total_ms[i] = 0.0;
+    g_prof.count[i] = 0;
+  }
+  return rc == SVDMLP_OK ? ST_COUNT : rc;
+}
 
 size_t svdmlp_workspace_bytes(int64_t T, int64_t d, int64_t ff, int64_t r, int32_t w_dtype) {
   (void)w_dtype;
@@ -289,7 +589,10 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
     float* xu32 = reinterpret_cast<float*>(ws + L.xu32);
     float* g32 = reinterpret_cast<float*>(ws + L.gu32);
     float* u32 = g32 + T * ff;
-    rc = check(launch_fill_zero(xu32, (int64_t)(L.h - L.xu32) / 4, c.st), "zero accumulators");
+    {
+      StageScope z(ST_ZERO, c.st);
+      rc = check(launch_fill_zero(xu32, (int64_t)(L.h - L.xu32) / 4, c.st), "zero accumulators");
+    }
     if (rc) return rc;
     const Operand ax{x, nullptr, d};
     const Operand a1[2] = {ax, ax};
@@ -297,17 +600,26 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
     const float* s1[2] = {s_ug, s_uu};
     const int n1[2] = {(int)r, (int)r};
     float* o1[2] = {xu32, xu32 + T * r};
-    rc = decode_stage(c, T, d, 2, a1, SRC_BF16, w1, fp8 ? s1 : nullptr, u_lin, n1, o1, "decode X.U");
+    rc = decode_stage(c, ST_DEC_GU_XU, T, d, 2, a1, SRC_BF16, w1, fp8 ? s1 : nullptr, u_lin, n1, o1, "decode X.U");
     if (rc) return rc;
     const Operand a2[2] = {Operand{xu32, nullptr, r}, Operand{xu32 + T * r, nullptr, r}};
     const void* w2[2] = {vg, vu};
     const float* s2[2] = {s_vg, s_vu};
     const int n2[2] = {(int)ff, (int)ff};
     float* o2[2] = {g32, u32};
-    rc = decode_stage(c, T, r, 2, a2, SRC_F32, w2, fp8 ? s2 : nullptr, v_lin, n2, o2, "decode XU.V");
+    rc = decode_stage(c, ST_DEC_GU_XUV, T, r, 2, a2, SRC_F32, w2, fp8 ? s2 : nullptr, v_lin, n2, o2, "decode XU.V");
     if (rc) return rc;
+    StageScope fin(ST_FINALIZE, c.st);
     return check(launch_finalize(g32, u32, ff, static_cast<uint16_t*>(h), out_t ? T : ff, T, ff, true, out_t, c.st),
                  "SwiGLU finalize");
+  }
+
+  if (!out_t && big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2})) {
+    const void* us[2] = {ug, uu};
+    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L))) return rc;
+    const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
+    uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.h);
+    return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h);
   }
 
   const Operand ax{x, nullptr, d};
@@ -346,25 +658,35 @@ int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, co
   if (!x_t && decode_ok(c, T, {din, dout, r}, vec)) {
     float* xd32 = reinterpret_cast<float*>(ws + L.xu32) + 2 * T * r;
     float* y32 = reinterpret_cast<float*>(ws + L.y32);
-    rc = check(launch_fill_zero(xd32, T * r, c.st), "zero accumulators");
-    if (!rc) rc = check(launch_fill_zero(y32, T * dout, c.st), "zero accumulators");
+    {
+      StageScope z(ST_ZERO, c.st);
+      rc = check(launch_fill_zero(xd32, T * r, c.st), "zero accumulators");
+      if (!rc) rc = check(launch_fill_zero(y32, T * dout, c.st), "zero accumulators");
+    }
     if (rc) return rc;
     const Operand a1[1] = {Operand{x, nullptr, din}};
     const void* w1[1] = {u};
     const float* s1[1] = {s_u};
     const int n1[1] = {(int)r};
     float* o1[1] = {xd32};
-    rc = decode_stage(c, T, din, 1, a1, SRC_BF16, w1, fp8 ? s1 : nullptr, u_lin, n1, o1, "decode X.U");
+    rc = decode_stage(c, ST_DEC_D_XU, T, din, 1, a1, SRC_BF16, w1, fp8 ? s1 : nullptr, u_lin, n1, o1, "decode X.U");
     if (rc) return rc;
     const Operand a2[1] = {Operand{xd32, nullptr, r}};
     const void* w2[1] = {v};
     const float* s2[1] = {s_v};
     const int n2[1] = {(int)dout};
     float* o2[1] = {y32};
-    rc = decode_stage(c, T, r, 1, a2, SRC_F32, w2, fp8 ? s2 : nullptr, v_lin, n2, o2, "decode XU.V");
+    rc = decode_stage(c, ST_DEC_D_XUV, T, r, 1, a2, SRC_F32, w2, fp8 ? s2 : nullptr, v_lin, n2, o2, "decode XU.V");
     if (rc) return rc;
+    StageScope fin(ST_FINALIZE, c.st);
     return check(launch_finalize(y32, nullptr, dout, static_cast<uint16_t*>(y), dout, T, dout, false, false, c.st),
                  "output finalize");
+  }
+
+  if (!x_t && big_ok(c, vec, {T * din * 2, din * r * 2, r * dout * 2, T * dout * 2})) {
+    const void* us[1] = {u};
+    if ((rc = big_xu(c, ST_D_XU, x, din, T * din * 2, us, u_lin, T, din, r, 1, ws, L))) return rc;
+    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), v, v_lin, T, r, dout, ws, L, y);
   }
 
   const Operand ax{x, nullptr, x_t ? T : din};
@@ -416,7 +738,10 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
     float* g32 = reinterpret_cast<float*>(ws + L.gu32);
     float* u32 = g32 + T * ff;
     float* y32 = reinterpret_cast<float*>(ws + L.y32);
-    rc = check(launch_fill_zero(xu32, (int64_t)(L.total - L.xu32) / 4, c.st), "zero accumulators");
+    {
+      StageScope z(ST_ZERO, c.st);
+      rc = check(launch_fill_zero(xu32, (int64_t)(L.total - L.xu32) / 4, c.st), "zero accumulators");
+    }
     if (rc) return rc;
     const Operand ax{x, nullptr, d};
     {
@@ -425,7 +750,7 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
       const float* s[2] = {S[0], S[2]};
       const int n[2] = {(int)r_gu, (int)r_gu};
       float* o[2] = {xg, xuu};
-      if ((rc = decode_stage(c, T, d, 2, a, SRC_BF16, w, s, u_lin, n, o, "decode X.U"))) return rc;
+      if ((rc = decode_stage(c, ST_DEC_GU_XU, T, d, 2, a, SRC_BF16, w, s, u_lin, n, o, "decode X.U"))) return rc;
     }
     {
       const Operand a[2] = {Operand{xg, nullptr, r_gu}, Operand{xuu, nullptr, r_gu}};
@@ -433,7 +758,7 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
       const float* s[2] = {S[1], S[3]};
       const int n[2] = {(int)ff, (int)ff};
       float* o[2] = {g32, u32};
-      if ((rc = decode_stage(c, T, r_gu, 2, a, SRC_F32, w, s, v_lin, n, o, "decode XU.V"))) return rc;
+      if ((rc = decode_stage(c, ST_DEC_GU_XUV, T, r_gu, 2, a, SRC_F32, w, s, v_lin, n, o, "decode XU.V"))) return rc;
     }
     {
       const Operand a[1] = {Operand{g32, u32, ff}};
@@ -441,7 +766,7 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
       const float* s[1] = {S[4]};
       const int n[1] = {(int)r_d};
       float* o[1] = {xd};
-      if ((rc = decode_stage(c, T, ff, 1, a, SRC_SWIGLU, w, s, u_lin, n, o, "decode h.Ud"))) return rc;
+      if ((rc = decode_stage(c, ST_DEC_D_XU, T, ff, 1, a, SRC_SWIGLU, w, s, u_lin, n, o, "decode h.Ud"))) return rc;
     }
     {
       const Operand a[1] = {Operand{xd, nullptr, r_d}};
@@ -449,13 +774,26 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
       const float* s[1] = {S[5]};
       const int n[1] = {(int)d};
       float* o[1] = {y32};
-      if ((rc = decode_stage(c, T, r_d, 1, a, SRC_F32, w, s, v_lin, n, o, "decode XUd.Vd"))) return rc;
+      if ((rc = decode_stage(c, ST_DEC_D_XUV, T, r_d, 1, a, SRC_F32, w, s, v_lin, n, o, "decode XUd.Vd"))) return rc;
     }
+    StageScope fin(ST_FINALIZE, c.st);
     return check(launch_finalize(y32, nullptr, d, static_cast<uint16_t*>(y), d, T, d, false, false, c.st),
                  "output finalize");
   }
 
   // Prefill: h stays in the workspace between the two halves.
+  if (big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2, ff * r * 2})) {
+    const void* us[2] = {ug, uu};
+    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L))) return rc;
+    const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
+    uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
+    uint16_t* gbuf = hbuf + T * ff;
+    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf))) return rc;
+    const void* ud1[1] = {ud};
+    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L))) return rc;
+    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y);
+  }
+
   const Operand ax{x, nullptr, d};
   const void* us[2] = {ug, uu};
   const float* sus[2] = {S[0], S[2]};

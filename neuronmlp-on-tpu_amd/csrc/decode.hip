@@ -56,6 +56,60 @@ __global__ void fill_zero_kernel(float* p, int64_t n) {
   }
 }
 
+// out[i] = bf16(in[i]), eight elements per thread and step.
+__global__ void cvt_bf16_kernel(const float* in, uint16_t* out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x * 8;
+  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; i < n; i += stride) {
+    if (i + 7 < n) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(in + i);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(in + i + 4);
+      *reinterpret_cast<u32x4*>(out + i) = u32x4{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w),
+                                                 pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)};
+    } else {
+      for (int64_t t = i; t < n; ++t) out[t] = (uint16_t)f32_to_bf16_bits(in[t]);
+    }
+  }
+}
+
+hipError_t launch_cvt_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int blocks = (int)std::min<int64_t>((n / 8 + 255) / 256 + 1, 2048);
+  hipLaunchKernelGGL(cvt_bf16_kernel, dim3(blocks), dim3(256), 0, st, in, out, n);
+  return hipGetLastError();
+}
+
+// out[i] = bf16(sum over split-K slices), eight elements per thread and step;
+// slices are summed in order, so the result is deterministic.
+__global__ void reduce_bf16_kernel(const float* in, int slices, int64_t stride, uint16_t* out, int64_t n) {
+  const int64_t step = (int64_t)gridDim.x * blockDim.x * 8;
+  for (int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8; i < n; i += step) {
+    if (i + 7 < n) {
+      f32x4 a = *reinterpret_cast<const f32x4*>(in + i);
+      f32x4 b = *reinterpret_cast<const f32x4*>(in + i + 4);
+      for (int s = 1; s < slices; ++s) {
+        a += *reinterpret_cast<const f32x4*>(in + s * stride + i);
+        b += *reinterpret_cast<const f32x4*>(in + s * stride + i + 4);
+      }
+      *reinterpret_cast<u32x4*>(out + i) = u32x4{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w),
+                                                 pack_bf16x2(b.x, b.y), pack_bf16x2(b.z, b.w)};
+    } else {
+      for (int64_t t = i; t < n; ++t) {
+        float v = in[t];
+        for (int s = 1; s < slices; ++s) v += in[s * stride + t];
+        out[t] = (uint16_t)f32_to_bf16_bits(v);
+      }
+    }
+  }
+}
+
+hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint16_t* out, int64_t n,
+                              hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  const int blocks = (int)std::min<int64_t>((n / 8 + 255) / 256 + 1, 4096);
+  hipLaunchKernelGGL(reduce_bf16_kernel, dim3(blocks), dim3(256), 0, st, in, slices, stride, out, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st) {
   if (n <= 0) return hipSuccess;
   const int64_t vec = (n + 3) / 4;

@@ -27,6 +27,15 @@ struct DecodeDesc {
   bool b_kc;     // Linear-layout weights
 };
 
+struct BigDesc {
+  int fn;        // block tile = 256 x 32*fn (8 waves, each 64 x 16*fn)
+  bool b_kc;     // Linear-layout B
+  int epi;       // BigEpi
+  bool out_f32;  // fp32 output (split-K partial slices)
+};
+
+struct BigParams;
+
 // Block tile of the prefill GEMM (rows x cols of C per 256-thread block).
 constexpr int kGemmBM = 128;
 constexpr int kGemmBN = 128;
@@ -37,9 +46,15 @@ hipError_t launch_gemm_fp8(const GemmDesc& d, const GemmParams& p, int splits, i
                            const char** why);
 hipError_t launch_gemm_f32(const GemmDesc& d, const GemmParams& p, int splits, int batch, hipStream_t st,
                            const char** why);
+hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st,
+                      const char** why);
 hipError_t launch_decode(const DecodeDesc& d, const DecodeParams& p, int blocks, hipStream_t st,
                          const char** why);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
+hipError_t launch_cvt_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st);
+// out[i] = bf16(sum_s in[s * stride + i]) for s < slices.
+hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint16_t* out, int64_t n,
+                              hipStream_t st);
 hipError_t launch_finalize(const float* g, const float* u, int64_t ldi, uint16_t* out, int64_t ldo, int rows,
                            int cols, bool swiglu, bool out_t, hipStream_t st);
 

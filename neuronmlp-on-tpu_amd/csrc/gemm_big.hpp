@@ -1,0 +1,281 @@
+// Large-tile bf16 MFMA GEMM for the prefill shapes (the hot kernel).
+//
+//   C[M x N] (+)= A[M x K] . B[K x N]
+//
+// Block: 512 threads = 8 waves (2 per SIMD) in a 4 (M) x 2 (N) grid; each
+// wave owns a 64 x (16*FN) tile of 16x16 MFMA blocks
+// (v_mfma_f32_16x16x32_bf16, fp32 accumulate), so the block tile is
+// 256 x 32*FN (256 x 224 or 256 x 256).  While one wave of a SIMD waits on
+// LDS, its sibling issues MFMAs.
+//
+// LDS, two stages of 64 k:
+//  * A (K contiguous): one 128-byte row per m, 16-byte chunks XOR-swizzled
+//    by row; an MFMA fragment is one ds_read_b128.
+//  * B in the reference's natural (in, out) layout (N contiguous): stored
+//    as it lies in HBM, one 512-byte row per k, its 32-byte units
+//    XOR-swizzled by (k & 3) | ((k >> 3) & 1) << 2.  A fragment (16 columns
+//    x 8 k) is two ds_read_b64_tr_b16: in each 16-lane group, lane i
+//    receives element i % 4 of the 8-byte pieces addressed by lanes
+//    i/4 + 4j, so pointing lane s at row k + s/4, columns n + 4*(s % 4)
+//    delivers column n + i, rows k..k+3 -- the MFMA operand layout -- with
+//    no transpose pass anywhere.
+//  * B in PyTorch Linear layout (K contiguous): same as A.
+// Global -> LDS is direct (buffer_load ... lds): each lane fetches the
+// 16-byte unit that belongs at its LDS slot under the swizzle, so no
+// registers hold staged tiles.  Out-of-range lanes use an offset past the
+// buffer end and fetch zeros.  The swizzle of a lane's slot does not change
+// along K, so each lane keeps one base offset per operand.
+// Pipeline: the DMA of stage k+1 is in flight while stage k is multiplied;
+// one barrier per stage.
+#pragma once
+
+#include "gemm.hpp"
+
+namespace svdmlp {
+
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define SVDMLP_LDS __attribute__((address_space(3)))
+
+constexpr uint32_t kOOB = 0x80000000u;  // offset past any buffer: reads return 0
+
+// Raw buffer descriptor (base, stride 0, num_records = bytes) in SGPRs.
+__device__ __forceinline__ i32x4 make_rsrc_sgpr(const void* p, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)p;
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+  r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = 0x00020000;
+  return r;
+}
+
+// LDS byte address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((const SVDMLP_LDS char*)p);
+}
+
+// 16 bytes per lane from global (buffer offset `voff`, past-the-end -> 0)
+// straight into LDS at lds_base + 16 * lane.  Volatile inline asm without a
+// memory clobber: the compiler neither serialises it against LDS traffic it
+// cannot prove disjoint nor waits on it; ordering comes from the program
+// order of volatile asm around s_barrier, and completion is awaited
+// explicitly (wait_dma) before the barrier that publishes the stage.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc));
+}
+
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ u32x2 lds_read_tr(const char* p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((SVDMLP_LDS bf16x4*)(p)));
+}
+
+// 32-byte unit swizzle of a natural-layout B row k.
+__device__ __forceinline__ int bnat_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+
+enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2 };
+
+struct BigParams {
+  const void* a[2];  // per batch entry (blockIdx.z)
+  const void* b[2];
+  uint32_t a_bytes[2], b_bytes[2];
+  int64_t lda, ldb;  // elements
+  void* out;
+  int64_t ldo;
+  int64_t out_bstride;   // elements between batch outputs
+  int64_t out_sstride;   // elements between split-K partial slices (fp32 output)
+  const uint16_t* gmem;  // BEPI_SWIGLU_MEM: bf16 gate values, same layout as out
+  int M, N, K;
+  int mtiles, ntiles;
+  int k_split;
+};
+
+constexpr int kBigThreads = 512;
+
+template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_>
+struct BigCfg {
+  static constexpr int FM = 4, FN = FN_;  // per wave: 64 x 16*FN
+  static constexpr bool B_KC = B_KC_;
+  static constexpr int EPI = EPI_;
+  static constexpr bool OUT_F32 = OUT_F32_;
+  static constexpr int BM = 256, BN = 32 * FN, BK = 64;
+  static constexpr int A_BYTES = BM * 128;
+  static constexpr int B_PITCH = 512;
+  static constexpr int B_BYTES = B_KC ? BN * 128 : BK * B_PITCH;
+  static constexpr int STAGE = A_BYTES + B_BYTES;
+  static constexpr int A_UNITS = A_BYTES / 1024 / 8;  // 1 KB DMA instructions per wave
+  static constexpr int B_BLOCKS = B_BYTES / 1024;
+  static constexpr int B_UNITS = (B_BLOCKS + 7) / 8;
+  static_assert(A_BYTES % 8192 == 0 && B_BYTES % 1024 == 0, "tiles must split into 1 KB blocks");
+  static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
+  static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+};
+
+template <class C>
+__global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
+  constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN, BK = C::BK;
+  // One array per stage (distinct objects for the compiler's alias analysis).
+  __shared__ __attribute__((aligned(16))) char lds0[C::STAGE];
+  __shared__ __attribute__((aligned(16))) char lds1[C::STAGE];
+
+  const int ntile_total = p.mtiles * p.ntiles;
+  const int tile = xcd_remap(blockIdx.x, ntile_total);
+  const int m0 = (tile % p.mtiles) * BM;
+  const int n0 = (tile / p.mtiles) * BN;
+  const int zb = blockIdx.z;
+  const int kbeg = blockIdx.y * p.k_split;
+  const int kend = min(p.K, kbeg + p.k_split);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int wm0 = (wave >> 1) * (BM / 4);
+  const int wn0 = (wave & 1) * (BN / 2);
+
+  const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
+  const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
+  const uint32_t lda2 = (uint32_t)p.lda * 2u, ldb2 = (uint32_t)p.ldb * 2u;
+
+  // ---- per-lane DMA geometry (constant along K) ----
+  // A: instruction i of this wave fills LDS rows 8*(wave + 8i) + lane/8;
+  // the slot's logical chunk is (lane & 7) ^ swz(row), independent of i.
+  const int a_row0 = 8 * wave + (lane >> 3);
+  const int a_chunk = (lane & 7) ^ lds_swz(a_row0);
+  const uint32_t a_base = (uint32_t)(m0 + a_row0) * lda2 + (uint32_t)(a_chunk * 16);
+  // B natural: instruction i fills LDS k-row 2*(wave + 8i) + lane/32,
+  // slot lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
+  // B linear: like A with rows n.
+  int b_row0, b_col;
+  uint32_t b_base;
+  if constexpr (C::B_KC) {
+    b_row0 = 8 * wave + (lane >> 3);
+    b_col = ((lane & 7) ^ lds_swz(b_row0)) * 8;  // k offset within the stage
+    b_base = (uint32_t)(n0 + b_row0) * ldb2 + (uint32_t)(b_col * 2);
+  } else {
+    b_row0 = 2 * wave + (lane >> 5);
+    const int q = lane & 31;
+    b_col = 16 * ((q >> 1) ^ bnat_swz(b_row0)) + 8 * (q & 1);
+    b_base = (uint32_t)b_row0 * ldb2 + (uint32_t)((n0 + b_col) * 2);
+  }
+
+  auto load_tile = [&](int kt, char* stage) {
+    const int k0 = kbeg + kt * BK;
+    const uint32_t la = lds_addr(stage);
+    const uint32_t lb = la + C::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < C::A_UNITS; ++i) {
+      const bool ok = (m0 + a_row0 + 64 * i < p.M) && (k0 + a_chunk * 8 < kend);
+      const uint32_t off = a_base + (uint32_t)(64 * i) * lda2 + (uint32_t)(k0 * 2);
+      dma16(ra, ok ? off : kOOB, la + (wave + 8 * i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < C::B_UNITS; ++i) {
+      bool ok;
+      uint32_t off;
+      if constexpr (C::B_KC) {
+        ok = (n0 + b_row0 + 64 * i < p.N) && (k0 + b_col < kend);
+        off = b_base + (uint32_t)(64 * i) * ldb2 + (uint32_t)(k0 * 2);
+      } else {
+        ok = (k0 + b_row0 + 16 * i < kend) && (b_col < BN) && (n0 + b_col < p.N);
+        off = b_base + (uint32_t)(k0 + 16 * i) * ldb2;
+      }
+      if (C::B_BLOCKS % 8 == 0 || wave + 8 * i < C::B_BLOCKS)  // wave-uniform
+        dma16(rb, ok ? off : kOOB, lb + (wave + 8 * i) * 1024);
+    }
+  };
+
+  // ---- fragments ----
+  auto read_frags = [&](const char* stage, int ks, u32x4* fa, u32x4* fb) {
+    const char* la = stage;
+    const char* lb = la + C::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) fa[i] = lds_read_chunk(la, wm0 + 16 * i + lr, 4 * ks + lg);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (C::B_KC) {
+        fb[j] = lds_read_chunk(lb, wn0 + 16 * j + lr, 4 * ks + lg);
+      } else {
+        const int nb = wn0 + 16 * j;  // multiple of 16 -> 32-byte unit nb/16
+        const int k_lo = 32 * ks + 8 * lg + (lr >> 2);
+        const int k_hi = k_lo + 4;
+        const char* plo = lb + k_lo * C::B_PITCH + (((nb >> 4) ^ bnat_swz(k_lo)) << 5) + ((lr & 3) << 3);
+        const char* phi = lb + k_hi * C::B_PITCH + (((nb >> 4) ^ bnat_swz(k_hi)) << 5) + ((lr & 3) << 3);
+        const u32x2 lo = lds_read_tr(plo);
+        const u32x2 hi = lds_read_tr(phi);
+        fb[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
+      }
+    }
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto stage_step = [&](int kt, char* cur, char* nxt) {
+    load_tile(kt + 1, nxt);  // zeros past kend
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 fa[FM], fb[FN];
+      read_frags(cur, ks, fa, fb);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(fb[j], fa[i], acc[i][j], __bf16{});
+    }
+    wait_dma();  // own DMA into nxt landed
+    __syncthreads();
+  };
+
+  if (nk > 0) {
+    load_tile(0, lds0);
+    wait_dma();
+    __syncthreads();
+  }
+  for (int kt = 0; kt < nk; kt += 2) {
+    stage_step(kt, lds0, lds1);
+    if (kt + 1 < nk) stage_step(kt + 1, lds1, lds0);
+  }
+
+  // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
+  const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
+  char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)blockIdx.y * p.out_sstride) * esz;
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm0 + 16 * i + lr;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn0 + 16 * j + 4 * lg;
+      if (n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+      const f32x4 v = acc[i][j];
+      const int64_t o = (int64_t)m * p.ldo + n;
+      if constexpr (C::EPI == BEPI_ATOMIC) {
+        float* op = reinterpret_cast<float*>(outp) + o;
+        unsafeAtomicAdd(op + 0, v.x);
+        unsafeAtomicAdd(op + 1, v.y);
+        unsafeAtomicAdd(op + 2, v.z);
+        unsafeAtomicAdd(op + 3, v.w);
+      } else if constexpr (C::OUT_F32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + o) = v;
+      } else if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
+        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + o);
+        const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
+        const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) =
+            u32x2{pack_bf16x2(silu_f32(g0) * v.x, silu_f32(g1) * v.y),
+                  pack_bf16x2(silu_f32(g2) * v.z, silu_f32(g3) * v.w)};
+      } else {
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) =
+            u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+      }
+    }
+  }
+}
+
+}  // namespace svdmlp

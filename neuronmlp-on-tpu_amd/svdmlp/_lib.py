@@ -36,6 +36,9 @@ EXPORTED = (
     "svdmlp_gate_up",
     "svdmlp_xuv",
     "svdmlp_svd_mlp",
+    "svdmlp_profile_enable",
+    "svdmlp_profile_read",
+    "svdmlp_stage_name",
 )
 
 _lock = threading.Lock()
@@ -69,6 +72,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.svdmlp_xuv.argtypes = [_vp] * 3 + [_vp] * 2 + [_vp] + [_i64] * 4 + [_i32, _i32, _u32, _vp, _sz, _vp]
     lib.svdmlp_svd_mlp.restype = ctypes.c_int
     lib.svdmlp_svd_mlp.argtypes = [_vp] * 7 + [_vp, _vp] + [_i64] * 5 + [_i32, _i32, _u32, _vp, _sz, _vp]
+    lib.svdmlp_profile_enable.restype = ctypes.c_int
+    lib.svdmlp_profile_enable.argtypes = [ctypes.c_int]
+    lib.svdmlp_profile_read.restype = ctypes.c_int
+    lib.svdmlp_profile_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int64),
+                                        ctypes.c_int]
+    lib.svdmlp_stage_name.restype = ctypes.c_char_p
+    lib.svdmlp_stage_name.argtypes = [ctypes.c_int]
 
 
 def _mapped_hip_runtimes() -> set[str]:
@@ -131,3 +141,29 @@ def version() -> int:
 
 def workspace_bytes(T: int, d: int, ff: int, r: int, w_dtype: int) -> int:
     return int(load().svdmlp_workspace_bytes(T, d, ff, r, w_dtype))
+
+
+class StageProfile:
+    """Per-stage GPU time of the library's launches (hipEvents on the
+    caller's stream).  ``with StageProfile() as prof: ...`` then
+    ``prof.result`` maps stage name -> (total_ms, launches)."""
+
+    def __init__(self):
+        self.result: dict[str, tuple[float, int]] = {}
+
+    def __enter__(self):
+        lib = load()
+        lib.svdmlp_profile_read(None, None, 0)  # drop anything stale
+        lib.svdmlp_profile_enable(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib = load()
+        n = lib.svdmlp_profile_enable(0)
+        ms = (ctypes.c_double * n)()
+        cnt = (ctypes.c_int64 * n)()
+        rc = lib.svdmlp_profile_read(ms, cnt, n)
+        if rc < 0:
+            check(rc)
+        self.result = {lib.svdmlp_stage_name(i).decode(): (ms[i], cnt[i]) for i in range(n) if cnt[i]}
+        return False

@@ -178,6 +178,25 @@ def test_8b_decode(gpu, layer8b, T):
     assert _rel(_np(y), O.fused_xuv_ref(h_ref, f[4], f[5], "bfloat16")) < BF16_TOL
 
 
+@pytest.mark.parametrize("T", [65, 128, 200, 256, 300, 512, 777])
+def test_prefill_token_counts(gpu, T):
+    """Token counts change the tile count, hence the split-K plan (and the
+    partial-slice reduction) of every large-tile stage."""
+    shape = inputs.LayerShape(1024, 2048, 512, 384)
+    x, f = inputs.make_layer(shape, T=T, seed=T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    got = _np(ops.svd_mlp(*t))
+    assert np.isfinite(got).all()
+    err = _rel(got, O.svd_mlp_ref(xb, *fb, dtype="bfloat16"))
+    assert err < BF16_TOL, err
+    h = _np(ops.fused_gate_up(*t[:5]))
+    assert _rel(h, O.fused_gate_up_ref(xb, *fb[:4], dtype="bfloat16")) < BF16_TOL
+    hb = inputs.as_float32(h, torch.bfloat16)
+    y = _np(ops.fused_xuv(_to(hb, torch.bfloat16, gpu), t[5], t[6]))
+    assert _rel(y, O.fused_xuv_ref(hb, fb[4], fb[5], "bfloat16")) < BF16_TOL
+
+
 def test_decode_and_prefill_paths_agree(gpu, layer8b):
     """T=64 runs the decode kernels, T=128 the tiled GEMMs; the first 64 rows
     of the two must agree with each other and with the oracle."""
