@@ -8,9 +8,10 @@ in HBM.  Weights rotate over several synthetic layers so that consecutive
 steps do not re-read factors out of the 256 MB Infinity Cache.
 
 The JSON line also carries:
-  roofline      the dominant kernel (gate/up XUV + SwiGLU) timed live with
-                hipEvents on the launch stream: algorithmic FLOP per launch /
-                average launch duration vs the 2.5 PFLOP/s bf16 MFMA peak
+  roofline      the dominant kernel (the GEMM stage with the most time per
+                layer) timed live with hipEvents on the launch stream:
+                algorithmic FLOP per launch / average launch duration vs the
+                2.5 PFLOP/s bf16 MFMA peak
   decode        T = 1, 8, 32, 64 decode layers: us/layer
                 and GB/s of compulsory bytes vs the 8 TB/s HBM peak
   cpu_baseline  the numpy oracle (oracle/reference_cpu.py) timed on this
@@ -54,10 +55,13 @@ def _args(argv=None):
     p.add_argument("--only", choices=("prefill", "decode"), default=None,
                    help="run one part only (for profiler runs)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--weights-layout", choices=("natural", "linear"), default="natural",
+                   help="natural (in, out) factors as kernels/reference.py takes them, or PyTorch Linear "
+                        "(out, in) storage passed as transposed views (test_speedup.py nki_mm)")
     return p.parse_args(argv)
 
 
-def _layer_weights(torch, dev, seed):
+def _layer_weights(torch, dev, seed, linear=False):
     """Synthetic factors of one layer: U ~ N(0, 1/d_in), V ~ N(0, 1/r), bf16,
     drawn on the device from a seeded generator (reference recipe
     test_speedup.py:803-808, device RNG instead of numpy)."""
@@ -65,12 +69,31 @@ def _layer_weights(torch, dev, seed):
     g.manual_seed(seed)
 
     def rnd(rows, cols):
-        return (torch.randn(rows, cols, generator=g, device=dev, dtype=torch.float32)
-                / math.sqrt(rows)).to(torch.bfloat16)
+        w = (torch.randn(rows, cols, generator=g, device=dev, dtype=torch.float32)
+             / math.sqrt(rows)).to(torch.bfloat16)
+        return w.t().contiguous().t() if linear else w
 
     uu, vu, ug, vg = rnd(D, R), rnd(R, FF), rnd(D, R), rnd(R, FF)
     ud, vd = rnd(FF, R), rnd(R, D)
     return ug, vg, uu, vu, ud, vd  # gate-first, kernels/reference.py order
+
+
+def _stage_work(T):
+    """Per-launch algorithmic FLOP, compulsory HBM bytes (bf16 operands read
+    once, the stage's bf16 result written once) and a description of each
+    GEMM stage of the prefill layer, keyed by the library's stage names."""
+    return {
+        "gate_up_xu": (2.0 * T * D * 2 * R, 2 * (T * D + 2 * D * R + 2 * T * R),
+                       "big_gemm_kernel X.[Ug|Uu] (split-K fp32 slices)"),
+        "gate_up_xuv_g": (2.0 * T * R * FF, 2 * (T * R + R * FF + T * FF),
+                          "big_gemm_kernel XUg.Vg -> bf16 g"),
+        "gate_up_xuv_swiglu": (2.0 * T * R * FF, 2 * (T * R + R * FF + 2 * T * FF),
+                               "big_gemm_kernel XUu.Vu, SiLU(g)*u epilogue"),
+        "down_xu": (2.0 * T * FF * R, 2 * (T * FF + FF * R + T * R),
+                    "big_gemm_kernel h.Ud (split-K fp32 slices)"),
+        "down_xuv": (2.0 * T * R * D, 2 * (T * R + R * D + T * D),
+                     "big_gemm_kernel XUd.Vd (split-K fp32 slices)"),
+    }
 
 
 def _time_steps(torch, fn, steps, warmup, stream):
@@ -139,7 +162,8 @@ def main(argv=None) -> int:
     svdmlp.load()
     stream = torch.cuda.current_stream(dev)
     T = args.tokens
-    layers = [_layer_weights(torch, dev, args.seed + i) for i in range(args.layers)]
+    linear = args.weights_layout == "linear"
+    layers = [_layer_weights(torch, dev, args.seed + i, linear) for i in range(args.layers)]
     gx = torch.Generator(device=dev)
     gx.manual_seed(args.seed + 1000)
     x = torch.randn(T, D, generator=gx, device=dev, dtype=torch.float32).to(torch.bfloat16)
@@ -158,9 +182,13 @@ def main(argv=None) -> int:
         with _lib.StageProfile() as prof:
             ms_prof, _ = _time_steps(torch, step, args.steps, 0, stream)
         stages = {k: v[0] / v[1] for k, v in prof.result.items()}
-        dom_ms = stages.get("gate_up_xuv_swiglu")
-        dom_flops = 2.0 * T * 2 * R * FF
-        dom_bytes = 2 * (2 * R * FF + 2 * T * R + T * FF)  # Vg, Vu, XU (gate, up), h
+        # Each GEMM stage is one kernel launch; the roofline line is for the
+        # one with the most time per layer.
+        stage_work = _stage_work(T)
+        gemm_stages = {k: v for k, v in stages.items() if k in stage_work}
+        dom = max(gemm_stages, key=gemm_stages.get) if gemm_stages else None
+        dom_ms = gemm_stages.get(dom)
+        dom_flops, dom_bytes, dom_desc = stage_work.get(dom, (None, None, None))
         achieved = dom_flops / (dom_ms * 1e-3) / 1e12 if dom_ms else None
         tflops = flops / (ms * 1e-3) / 1e12
         record.update({
@@ -179,10 +207,11 @@ def main(argv=None) -> int:
             "dtype": "bf16",
             "data": "synthetic (seeded device RNG; U~N(0,1/d_in), V~N(0,1/r), X~N(0,1))",
             "config": {"workload": "LLaMA3-8B SVD-MLP layer, prefill", "T": T, "d": D, "ff": FF, "r": R,
-                       "layers_rotated": len(layers), "flop_per_step": flops},
+                       "layers_rotated": len(layers), "flop_per_step": flops,
+                       "weights_layout": args.weights_layout},
             "wall_s_timed": round(wall, 4),
             "roofline": {
-                "kernel": "gate_up_xuv_swiglu (gemm_kernel, 2 branches, SwiGLU epilogue)",
+                "kernel": f"{dom}: {dom_desc}" if dom else None,
                 "bound": "mfma",
                 "achieved": round(achieved, 2) if achieved else None,
                 "peak": PEAK_BF16_TFLOPS,

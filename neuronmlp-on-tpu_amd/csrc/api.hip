@@ -303,7 +303,7 @@ int prefill_v(const Common& c, int a_src, const void* xu, const void* v, const f
 // Tile choices; SVDMLP_TUNE="s1=44,s4=88,split=256" overrides them (read once).
 struct Tune {
   int s1 = 8;         // X.U stages: block tile 256 x 32*s1
-  int s4 = 4;         // XU.V of the down half: 256 x 32*s4, or 0 = 256x256 split-K
+  int s4 = 8;         // XU.V of the down half: 256 x 32*s4 (8: split-K over r)
   int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 7 when ff % 224 == 0)
   int split = 256;    // split-K target block count
   bool big = true;    // large-tile path enabled

@@ -8,9 +8,14 @@
 // 256 x 32*FN (256 x 224 or 256 x 256).  While one wave of a SIMD waits on
 // LDS, its sibling issues MFMAs.
 //
-// LDS, two stages of 64 k:
-//  * A (K contiguous): one 128-byte row per m, 16-byte chunks XOR-swizzled
-//    by row; an MFMA fragment is one ds_read_b128.
+// LDS holds 4 stages of 32 k (one MFMA k-step each).  The DMA of a stage
+// is issued four steps before its MFMAs, its fragments are read into
+// registers one step before, and both are interleaved one instruction per
+// MFMA with the current step's MFMAs (sched_barrier-pinned), so a wave
+// never holds its MFMAs behind a burst of memory instructions:
+//  * A (K contiguous): one 64-byte row per m (four 16-byte chunks), chunk
+//    XOR-swizzled by (row >> 2) & 3; an MFMA fragment is one ds_read_b128
+//    and each 16-lane group of a read touches 16 distinct bank slots.
 //  * B in the reference's natural (in, out) layout (N contiguous): stored
 //    as it lies in HBM, one 512-byte row per k, its 32-byte units
 //    XOR-swizzled by (k & 3) | ((k >> 3) & 1) << 2.  A fragment (16 columns
@@ -24,9 +29,9 @@
 // 16-byte unit that belongs at its LDS slot under the swizzle, so no
 // registers hold staged tiles.  Out-of-range lanes use an offset past the
 // buffer end and fetch zeros.  The swizzle of a lane's slot does not change
-// along K, so each lane keeps one base offset per operand.
-// Pipeline: the DMA of stage k+1 is in flight while stage k is multiplied;
-// one barrier per stage.
+// along K, so each lane keeps one base offset per operand.  Every wave
+// issues exactly four 1 KB DMA instructions per stage, so "all but the two
+// youngest stages landed" is the constant wait vmcnt(8).
 #pragma once
 
 #include "gemm.hpp"
@@ -61,13 +66,28 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // cannot prove disjoint nor waits on it; ordering comes from the program
 // order of volatile asm around s_barrier, and completion is awaited
 // explicitly (wait_dma) before the barrier that publishes the stage.
+// GFX9 needs one wait state between an SALU write of M0 and an LDS DMA that
+// reads it (s_nop 0); the compiler's hazard pass does not look inside asm.
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(lds_base), "v"(voff), "s"(rsrc));
 }
 
-__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+  static_assert(N == 0 || N == 4 || N == 8, "vmcnt literal");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+}
+
+// A-tile chunk swizzle for 64-byte rows.
+__device__ __forceinline__ int a_swz(int row) { return (row >> 2) & 3; }
+
+__device__ __forceinline__ u32x4 lds_read_a(const char* base, int row, int chunk) {
+  return *reinterpret_cast<const u32x4*>(base + row * 64 + ((chunk ^ a_swz(row)) << 4));
+}
 
 __device__ __forceinline__ u32x2 lds_read_tr(const char* p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((SVDMLP_LDS bf16x4*)(p)));
@@ -101,17 +121,18 @@ struct BigCfg {
   static constexpr bool B_KC = B_KC_;
   static constexpr int EPI = EPI_;
   static constexpr bool OUT_F32 = OUT_F32_;
-  static constexpr int BM = 256, BN = 32 * FN, BK = 64;
-  static constexpr int A_BYTES = BM * 128;
+  static constexpr int BM = 256, BN = 32 * FN, BK = 32;  // BK per stage
+  static constexpr int STAGES = 4;
+  static constexpr int A_BYTES = BM * 64;                      // 16 KB
   static constexpr int B_PITCH = 512;
-  static constexpr int B_BYTES = B_KC ? BN * 128 : BK * B_PITCH;
+  static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (Linear: rows >= BN read zeros)
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int A_UNITS = A_BYTES / 1024 / 8;  // 1 KB DMA instructions per wave
-  static constexpr int B_BLOCKS = B_BYTES / 1024;
-  static constexpr int B_UNITS = (B_BLOCKS + 7) / 8;
-  static_assert(A_BYTES % 8192 == 0 && B_BYTES % 1024 == 0, "tiles must split into 1 KB blocks");
+  static constexpr int A_UNITS = A_BYTES / 1024 / 8;  // 2 DMA instructions per wave
+  static constexpr int B_UNITS = B_BYTES / 1024 / 8;  // 2
+  static_assert(A_UNITS == 2 && B_UNITS == 2, "four DMA instructions per wave and stage");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
-  static_assert(2 * STAGE <= 160 * 1024, "LDS budget");
+  static_assert(B_KC ? BN <= 256 : true, "Linear-layout B tile holds at most 256 rows");
+  static_assert(STAGES * STAGE <= 160 * 1024, "LDS budget");
 };
 
 template <class C>
@@ -120,6 +141,8 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   // One array per stage (distinct objects for the compiler's alias analysis).
   __shared__ __attribute__((aligned(16))) char lds0[C::STAGE];
   __shared__ __attribute__((aligned(16))) char lds1[C::STAGE];
+  __shared__ __attribute__((aligned(16))) char lds2[C::STAGE];
+  __shared__ __attribute__((aligned(16))) char lds3[C::STAGE];
 
   const int ntile_total = p.mtiles * p.ntiles;
   const int tile = xcd_remap(blockIdx.x, ntile_total);
@@ -141,19 +164,19 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   const uint32_t lda2 = (uint32_t)p.lda * 2u, ldb2 = (uint32_t)p.ldb * 2u;
 
   // ---- per-lane DMA geometry (constant along K) ----
-  // A: instruction i of this wave fills LDS rows 8*(wave + 8i) + lane/8;
-  // the slot's logical chunk is (lane & 7) ^ swz(row), independent of i.
-  const int a_row0 = 8 * wave + (lane >> 3);
-  const int a_chunk = (lane & 7) ^ lds_swz(a_row0);
+  // A: instruction i of this wave fills LDS rows 16*(wave + 8i) + lane/4;
+  // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row) = (lane%4) ^ (lane/16).
+  const int a_row0 = 16 * wave + (lane >> 2);
+  const int a_chunk = (lane & 3) ^ a_swz(a_row0);
   const uint32_t a_base = (uint32_t)(m0 + a_row0) * lda2 + (uint32_t)(a_chunk * 16);
-  // B natural: instruction i fills LDS k-row 2*(wave + 8i) + lane/32,
-  // slot lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
+  // B natural: instruction i fills LDS k-row 2*(wave + 8i) + lane/32, slot
+  // lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
   // B linear: like A with rows n.
   int b_row0, b_col;
   uint32_t b_base;
   if constexpr (C::B_KC) {
-    b_row0 = 8 * wave + (lane >> 3);
-    b_col = ((lane & 7) ^ lds_swz(b_row0)) * 8;  // k offset within the stage
+    b_row0 = 16 * wave + (lane >> 2);
+    b_col = ((lane & 3) ^ a_swz(b_row0)) * 8;  // k offset within the stage
     b_base = (uint32_t)(n0 + b_row0) * ldb2 + (uint32_t)(b_col * 2);
   } else {
     b_row0 = 2 * wave + (lane >> 5);
@@ -162,85 +185,137 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
     b_base = (uint32_t)b_row0 * ldb2 + (uint32_t)((n0 + b_col) * 2);
   }
 
-  auto load_tile = [&](int kt, char* stage) {
+  // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS buffer `stage`.
+  auto dma_one = [&](int kt, char* stage, int d) {
     const int k0 = kbeg + kt * BK;
     const uint32_t la = lds_addr(stage);
-    const uint32_t lb = la + C::A_BYTES;
-#pragma unroll
-    for (int i = 0; i < C::A_UNITS; ++i) {
-      const bool ok = (m0 + a_row0 + 64 * i < p.M) && (k0 + a_chunk * 8 < kend);
-      const uint32_t off = a_base + (uint32_t)(64 * i) * lda2 + (uint32_t)(k0 * 2);
+    if (d < C::A_UNITS) {
+      const int i = d;
+      const bool ok = (m0 + a_row0 + 128 * i < p.M) && (k0 + a_chunk * 8 < kend);
+      const uint32_t off = a_base + (uint32_t)(128 * i) * lda2 + (uint32_t)(k0 * 2);
       dma16(ra, ok ? off : kOOB, la + (wave + 8 * i) * 1024);
-    }
-#pragma unroll
-    for (int i = 0; i < C::B_UNITS; ++i) {
+    } else {
+      const int i = d - C::A_UNITS;
       bool ok;
       uint32_t off;
       if constexpr (C::B_KC) {
-        ok = (n0 + b_row0 + 64 * i < p.N) && (k0 + b_col < kend);
-        off = b_base + (uint32_t)(64 * i) * ldb2 + (uint32_t)(k0 * 2);
+        const int row = b_row0 + 128 * i;
+        ok = (row < BN) && (n0 + row < p.N) && (k0 + b_col < kend);
+        off = b_base + (uint32_t)(128 * i) * ldb2 + (uint32_t)(k0 * 2);
       } else {
         ok = (k0 + b_row0 + 16 * i < kend) && (b_col < BN) && (n0 + b_col < p.N);
         off = b_base + (uint32_t)(k0 + 16 * i) * ldb2;
       }
-      if (C::B_BLOCKS % 8 == 0 || wave + 8 * i < C::B_BLOCKS)  // wave-uniform
-        dma16(rb, ok ? off : kOOB, lb + (wave + 8 * i) * 1024);
+      dma16(rb, ok ? off : kOOB, la + C::A_BYTES + (wave + 8 * i) * 1024);
     }
   };
-
-  // ---- fragments ----
-  auto read_frags = [&](const char* stage, int ks, u32x4* fa, u32x4* fb) {
-    const char* la = stage;
-    const char* lb = la + C::A_BYTES;
+  constexpr int NDMA = C::A_UNITS + C::B_UNITS;
+  auto load_tile = [&](int kt, char* stage) {
 #pragma unroll
-    for (int i = 0; i < FM; ++i) fa[i] = lds_read_chunk(la, wm0 + 16 * i + lr, 4 * ks + lg);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      if constexpr (C::B_KC) {
-        fb[j] = lds_read_chunk(lb, wn0 + 16 * j + lr, 4 * ks + lg);
-      } else {
-        const int nb = wn0 + 16 * j;  // multiple of 16 -> 32-byte unit nb/16
-        const int k_lo = 32 * ks + 8 * lg + (lr >> 2);
-        const int k_hi = k_lo + 4;
-        const char* plo = lb + k_lo * C::B_PITCH + (((nb >> 4) ^ bnat_swz(k_lo)) << 5) + ((lr & 3) << 3);
-        const char* phi = lb + k_hi * C::B_PITCH + (((nb >> 4) ^ bnat_swz(k_hi)) << 5) + ((lr & 3) << 3);
-        const u32x2 lo = lds_read_tr(plo);
-        const u32x2 hi = lds_read_tr(phi);
-        fb[j] = u32x4{lo.x, lo.y, hi.x, hi.y};
-      }
-    }
+    for (int d = 0; d < NDMA; ++d) dma_one(kt, stage, d);
   };
 
+  // ---- fragments of one stage (one 32-k MFMA step) ----
+  // Per-lane LDS offsets, constant over stages: A rows wm0 + 16i + lr share
+  // one swizzle, so fragment i is a_off + 1 KB * i; B (natural) fragment j
+  // reads k rows 8*lg + lr/4 (+4 for the upper half, same swizzle, +2 KB).
+  const int a_off = (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
+  int b_off[FN];
+  if constexpr (C::B_KC) {
+    const int row0 = wn0 + lr;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) b_off[j] = C::A_BYTES + (row0 + 16 * j) * 64 + ((lg ^ a_swz(row0)) << 4);
+  } else {
+    const int k_lo = 8 * lg + (lr >> 2);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      b_off[j] = C::A_BYTES + k_lo * C::B_PITCH + ((((wn0 >> 4) + j) ^ bnat_swz(k_lo)) << 5) + ((lr & 3) << 3);
+  }
   f32x4 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto stage_step = [&](int kt, char* cur, char* nxt) {
-    load_tile(kt + 1, nxt);  // zeros past kend
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      u32x4 fa[FM], fb[FN];
-      read_frags(cur, ks, fa, fb);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_chunk(fb[j], fa[i], acc[i][j], __bf16{});
+  // Fragment registers: A as one 16-byte read per 16-row block; B as two
+  // 8-byte halves (k rows 0-3 and 4-7 of each lane's 8) so that natural and
+  // Linear layouts share one schedule (a Linear fragment is one 16-byte
+  // read split across the pair).
+  struct Frags {
+    u32x4 a[FM];
+    u32x2 b[2 * FN];
+  };
+  // Read number r of a stage's fragments: A blocks first, then B.
+  auto read_one = [&](const char* stage, int r, Frags& f) {
+    if (r < FM) {
+      f.a[r] = *reinterpret_cast<const u32x4*>(stage + a_off + 1024 * r);
+    } else if constexpr (C::B_KC) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + b_off[r - FM]);
+      f.b[2 * (r - FM)] = u32x2{v.x, v.y};
+      f.b[2 * (r - FM) + 1] = u32x2{v.z, v.w};
+    } else {
+      const int j = (r - FM) >> 1, hi = (r - FM) & 1;
+      f.b[2 * j + hi] = lds_read_tr(stage + b_off[j] + hi * 4 * C::B_PITCH);
     }
-    wait_dma();  // own DMA into nxt landed
+  };
+  constexpr int NREAD = FM + (C::B_KC ? FN : 2 * FN);
+  auto read_frags = [&](const char* stage, Frags& f) {
+#pragma unroll
+    for (int r = 0; r < NREAD; ++r) read_one(stage, r, f);
+  };
+  auto mfma_one = [&](int m, const Frags& f) {
+    const int i = m / FN, j = m % FN;
+    const u32x2 lo = f.b[2 * j], hi = f.b[2 * j + 1];
+    acc[i][j] = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, f.a[i], acc[i][j], __bf16{});
+  };
+
+  // Stage kt sits in buffer kt % 4.  Step kt runs the MFMAs of stage kt
+  // (fragments already in registers, read in step kt-1) and, interleaved
+  // one per MFMA so that no wave holds its MFMAs behind a burst of memory
+  // instructions:
+  //  * the fragment reads of stage kt+1;
+  //  * the DMA of stage kt+4 into buffer kt % 4, free since every wave's
+  //    reads of stage kt completed before the barrier that ended step kt-1.
+  // Then it waits until stage kt+2 landed (stages kt+3 and kt+4 may still be
+  // in flight: 8 DMA instructions) and meets the other waves at the barrier.
+  // DMAs past kend fetch zeros and keep the per-wave count constant.  The
+  // sched_barriers pin this instruction order.
+  Frags f0, f1;
+  constexpr int NMFMA = FM * FN;
+  static_assert(NREAD <= NMFMA && NDMA == 4, "one fragment read per MFMA slot");
+  auto step = [&](int kt, const char* next, char* own, const Frags& cur, Frags& nxt) {
+#pragma unroll
+    for (int m = 0; m < NMFMA; ++m) {
+      if (m < NREAD) read_one(next, m, nxt);
+#pragma unroll
+      for (int d = 0; d < NDMA; ++d)
+        if (m == d * NMFMA / NDMA + 1) dma_one(kt + 4, own, d);
+      mfma_one(m, cur);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_dma<8>();
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   if (nk > 0) {
     load_tile(0, lds0);
-    wait_dma();
+    load_tile(1, lds1);
+    load_tile(2, lds2);
+    load_tile(3, lds3);
+    wait_dma<8>();  // stages 0 and 1 landed
     __syncthreads();
+    read_frags(lds0, f0);
+    __syncthreads();  // every wave holds stage 0 before step 0 refills its buffer
+    __builtin_amdgcn_sched_barrier(0);
   }
-  for (int kt = 0; kt < nk; kt += 2) {
-    stage_step(kt, lds0, lds1);
-    if (kt + 1 < nk) stage_step(kt + 1, lds1, lds0);
+  for (int kt = 0; kt < nk; kt += 4) {
+    step(kt, lds1, lds0, f0, f1);
+    if (kt + 1 < nk) step(kt + 1, lds2, lds1, f1, f0);
+    if (kt + 2 < nk) step(kt + 2, lds3, lds2, f0, f1);
+    if (kt + 3 < nk) step(kt + 3, lds0, lds3, f1, f0);
   }
+  wait_dma<0>();  // drain DMAs of stages past the end before the block exits
 
   // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
   const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
