@@ -305,7 +305,7 @@ struct Tune {
   int s1 = 8;         // X.U stages: block tile 256 x 32*s1
   int s4 = 8;         // XU.V of the down half: 256 x 32*s4 (8: split-K over r)
   int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 7 when ff % 224 == 0)
-  int split = 256;    // split-K target block count
+  int split = 256;    // CUs assumed by the split-K planner
   bool big = true;    // large-tile path enabled
 };
 
@@ -375,25 +375,41 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   return check(launch_big(d, p, splits, batch, c.st, &why), "large-tile GEMM", why);
 }
 
-int pick_splits(int tiles, int K) {
-  const int target = tune().split;
-  if (4 * tiles >= 3 * target) return 1;
-  const int s = (target + tiles - 1) / tiles;
-  return std::max(1, std::min(s, K / 256));
-}
-
 }  // namespace
 
 namespace {
 
-// K elements per split for the large-tile stages (a multiple of the 64-k
+// K elements per split for the large-tile stages (a multiple of the 32-k
 // stage); the number of splits launched is ceil(K / k_split), and the same
-// count sizes the workspace and the reduction.
+// count sizes the workspace and the reduction.  The split count minimises a
+// cost model in shader cycles, with one 512-thread block per CU and the
+// MI355X's 256 CUs (a fixed count, so that the workspace size does not
+// depend on the device queried):
+//   rounds * (k-steps per split * cycles per step + fixed cost per block)
+//   + per fp32 slice: writing it and reading it back in the reduction.
+// The constants are measured on MI355X: a 32-k step costs ~41 cycles per
+// MFMA of the wave tile (64 x 32*fn), prologue + epilogue ~20k cycles, and
+// a slice byte ~0.00045 cycles each way (~4 TB/s at ~1.8 GHz).
 int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch) {
+  const int64_t cus = tune().split;
   const int64_t tiles = ((T + 255) / 256) * ((N + 32 * fn - 1) / (32 * fn)) * batch;
-  const int s = pick_splits((int)std::min<int64_t>(tiles, 1 << 20), (int)K);
-  const int64_t ks = ((K + s - 1) / s + 63) / 64 * 64;
-  return (int)ks;
+  const double c_step = 41.0 * 4 * fn, c_block = 20000.0;
+  const double c_slice = 0.0009 * (double)batch * (double)T * (double)N * 4.0;
+  int64_t best_ks = K;
+  double best = -1.0;
+  const int64_t max_s = std::max<int64_t>(1, std::min<int64_t>(64, K / 128));
+  for (int64_t s = 1; s <= max_s; ++s) {
+    const int64_t ks = ((K + s - 1) / s + 31) / 32 * 32;
+    const int64_t splits = (K + ks - 1) / ks;
+    const int64_t rounds = (tiles * splits + cus - 1) / cus;
+    const double cost = (double)rounds * ((double)(ks / 32) * c_step + c_block) +
+                        (splits > 1 ? (double)splits * c_slice : 0.0);
+    if (best < 0 || cost < best) {
+      best = cost;
+      best_ks = ks;
+    }
+  }
+  return (int)std::min<int64_t>(best_ks, K);
 }
 
 int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
