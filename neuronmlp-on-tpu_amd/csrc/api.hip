@@ -337,10 +337,14 @@ const Tune& tune() {
   return t;
 }
 
-bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes) {
+// The large-tile kernel takes bf16 operands below 2 GB each (32-bit buffer
+// offsets) and contraction lengths that are whole 32-k stages.
+bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes, std::initializer_list<int64_t> ks) {
   if (c.f32 || c.wt != SVDMLP_BF16 || !vec || !tune().big) return false;
   for (int64_t b : bytes)
     if (b >= ((int64_t)1 << 31)) return false;
+  for (int64_t k : ks)
+    if (k % 32 != 0) return false;
   return true;
 }
 
@@ -630,7 +634,7 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
                  "SwiGLU finalize");
   }
 
-  if (!out_t && big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2})) {
+  if (!out_t && big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2}, {d, r})) {
     const void* us[2] = {ug, uu};
     if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
@@ -699,7 +703,7 @@ int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, co
                  "output finalize");
   }
 
-  if (!x_t && big_ok(c, vec, {T * din * 2, din * r * 2, r * dout * 2, T * dout * 2})) {
+  if (!x_t && big_ok(c, vec, {T * din * 2, din * r * 2, r * dout * 2, T * dout * 2}, {din, r})) {
     const void* us[1] = {u};
     if ((rc = big_xu(c, ST_D_XU, x, din, T * din * 2, us, u_lin, T, din, r, 1, ws, L))) return rc;
     return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), v, v_lin, T, r, dout, ws, L, y);
@@ -798,7 +802,7 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
   }
 
   // Prefill: h stays in the workspace between the two halves.
-  if (big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2, ff * r * 2})) {
+  if (big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2, ff * r * 2}, {d, r_gu, ff, r_d})) {
     const void* us[2] = {ug, uu};
     if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);

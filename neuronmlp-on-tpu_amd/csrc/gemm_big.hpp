@@ -14,8 +14,8 @@
 // MFMA with the current step's MFMAs (sched_barrier-pinned), so a wave
 // never holds its MFMAs behind a burst of memory instructions:
 //  * A (K contiguous): one 64-byte row per m (four 16-byte chunks), chunk
-//    XOR-swizzled by (row >> 2) & 3; an MFMA fragment is one ds_read_b128
-//    and each 16-lane group of a read touches 16 distinct bank slots.
+//    XOR-swizzled by (row >> 1) & 3; an MFMA fragment is one ds_read_b128
+//    and each 8-lane group of a read touches all 32 banks once.
 //  * B in the reference's natural (in, out) layout (N contiguous): stored
 //    as it lies in HBM, one 512-byte row per k, its 32-byte units
 //    XOR-swizzled by (k & 3) | ((k >> 3) & 1) << 2.  A fragment (16 columns
@@ -60,18 +60,18 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)((const SVDMLP_LDS char*)p);
 }
 
-// 16 bytes per lane from global (buffer offset `voff`, past-the-end -> 0)
-// straight into LDS at lds_base + 16 * lane.  Volatile inline asm without a
+// 16 bytes per lane from global (buffer offset `voff` + scalar `soff`,
+// past-the-end -> 0) straight into LDS at lds_base + 16 * lane.  Volatile inline asm without a
 // memory clobber: the compiler neither serialises it against LDS traffic it
 // cannot prove disjoint nor waits on it; ordering comes from the program
 // order of volatile asm around s_barrier, and completion is awaited
 // explicitly (wait_dma) before the barrier that publishes the stage.
 // GFX9 needs one wait state between an SALU write of M0 and an LDS DMA that
 // reads it (s_nop 0); the compiler's hazard pass does not look inside asm.
-__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(lds_base), "v"(voff), "s"(rsrc));
+               : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff));
 }
 
 template <int N>
@@ -82,19 +82,24 @@ __device__ __forceinline__ void wait_dma() {
   if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 
-// A-tile chunk swizzle for 64-byte rows.
-__device__ __forceinline__ int a_swz(int row) { return (row >> 2) & 3; }
+// A-tile chunk swizzle for 64-byte rows.  A ds_read_b128 serves 8 lanes
+// (128 bytes, all 32 banks) per cycle; lanes 8q..8q+7 read the same logical
+// chunk of 8 consecutive rows.  Rows r and r+2 lie 128 bytes apart (same
+// banks), so the XOR must differ between them: (row >> 1) & 3 places the 8
+// rows on 8 distinct 16-byte bank groups.
+__device__ __forceinline__ int a_swz(int row) { return (row >> 1) & 3; }
 
-__device__ __forceinline__ u32x4 lds_read_a(const char* base, int row, int chunk) {
-  return *reinterpret_cast<const u32x4*>(base + row * 64 + ((chunk ^ a_swz(row)) << 4));
-}
 
-__device__ __forceinline__ u32x2 lds_read_tr(const char* p) {
+typedef const SVDMLP_LDS char* lds_cptr;  // 32-bit LDS address
+
+__device__ __forceinline__ u32x2 lds_read_tr(lds_cptr p) {
   return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((SVDMLP_LDS bf16x4*)(p)));
 }
 
+__device__ __forceinline__ u32x4 lds_read_b128(lds_cptr p) { return *reinterpret_cast<const SVDMLP_LDS u32x4*>(p); }
+
 // 32-byte unit swizzle of a natural-layout B row k.
-__device__ __forceinline__ int bnat_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+__device__ __forceinline__ int bnat_swz(int k) { return k & 3; }
 
 enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2 };
 
@@ -138,18 +143,27 @@ struct BigCfg {
 template <class C>
 __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN, BK = C::BK;
-  // One array per stage (distinct objects for the compiler's alias analysis).
-  __shared__ __attribute__((aligned(16))) char lds0[C::STAGE];
-  __shared__ __attribute__((aligned(16))) char lds1[C::STAGE];
-  __shared__ __attribute__((aligned(16))) char lds2[C::STAGE];
-  __shared__ __attribute__((aligned(16))) char lds3[C::STAGE];
+  constexpr int NS = C::STAGES;
+  // LDS: the A tiles of the 4 stages in the first 64 KB, the B tiles in the
+  // next 64 KB, so that every fragment read of any stage is one base
+  // register plus a 16-bit immediate offset.
+  constexpr int B_REGION = NS * C::A_BYTES;
+  __shared__ __attribute__((aligned(1024))) char lds[NS * (C::A_BYTES + C::B_BYTES)];
 
-  const int ntile_total = p.mtiles * p.ntiles;
-  const int tile = xcd_remap(blockIdx.x, ntile_total);
-  const int m0 = (tile % p.mtiles) * BM;
-  const int n0 = (tile / p.mtiles) * BN;
-  const int zb = blockIdx.z;
-  const int kbeg = blockIdx.y * p.k_split;
+  // Blocks are dispatched round-robin over the 8 XCDs (each with its own
+  // L2).  Remap the linear block id so that each XCD holds a contiguous run
+  // of work ordered m-tile fastest, then n-tile, then K split, then batch
+  // entry: the blocks of one XCD then share K-range slices of A (same m) and
+  // B (same n) in its L2.
+  const int nblk = gridDim.x * gridDim.y * gridDim.z;
+  int vb = xcd_remap(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), nblk);
+  const int m0 = (vb % p.mtiles) * BM;
+  vb /= p.mtiles;
+  const int n0 = (vb % p.ntiles) * BN;
+  vb /= p.ntiles;
+  const int split = vb % gridDim.y;
+  const int zb = vb / gridDim.y;
+  const int kbeg = split * p.k_split;
   const int kend = min(p.K, kbeg + p.k_split);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
@@ -162,75 +176,86 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
   const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
   const uint32_t lda2 = (uint32_t)p.lda * 2u, ldb2 = (uint32_t)p.ldb * 2u;
+  const uint32_t lbase = lds_addr(lds);
 
   // ---- per-lane DMA geometry (constant along K) ----
+  // The lane's byte offset without the stage's k (which goes into the
+  // instruction's scalar offset), or kOOB for rows / columns outside the
+  // matrix.  K and the split length are whole 32-k stages, so a stage lies
+  // either below kend or wholly past it; stages past it (the pipeline's
+  // run-out) use a descriptor with no records and fetch zeros.
   // A: instruction i of this wave fills LDS rows 16*(wave + 8i) + lane/4;
-  // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row) = (lane%4) ^ (lane/16).
+  // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row).
+  const i32x4 r_none = make_rsrc_sgpr(p.a[zb], 0);
   const int a_row0 = 16 * wave + (lane >> 2);
-  const int a_chunk = (lane & 3) ^ a_swz(a_row0);
-  const uint32_t a_base = (uint32_t)(m0 + a_row0) * lda2 + (uint32_t)(a_chunk * 16);
+  const int a_kk = 8 * ((lane & 3) ^ a_swz(a_row0));  // k within the stage
+  uint32_t a_voff[C::A_UNITS];
+#pragma unroll
+  for (int i = 0; i < C::A_UNITS; ++i) {
+    const int row = m0 + a_row0 + 128 * i;
+    a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
+  }
   // B natural: instruction i fills LDS k-row 2*(wave + 8i) + lane/32, slot
   // lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
-  // B linear: like A with rows n.
-  int b_row0, b_col;
-  uint32_t b_base;
+  // B Linear: like A with rows n.
+  uint32_t b_voff[C::B_UNITS];
   if constexpr (C::B_KC) {
-    b_row0 = 16 * wave + (lane >> 2);
-    b_col = ((lane & 3) ^ a_swz(b_row0)) * 8;  // k offset within the stage
-    b_base = (uint32_t)(n0 + b_row0) * ldb2 + (uint32_t)(b_col * 2);
+    const int row0 = 16 * wave + (lane >> 2);
+    const int kk = 8 * ((lane & 3) ^ a_swz(row0));
+#pragma unroll
+    for (int i = 0; i < C::B_UNITS; ++i) {
+      const int row = row0 + 128 * i;
+      b_voff[i] = (row < BN && n0 + row < p.N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
+    }
   } else {
-    b_row0 = 2 * wave + (lane >> 5);
+    const int kk = 2 * wave + (lane >> 5);
     const int q = lane & 31;
-    b_col = 16 * ((q >> 1) ^ bnat_swz(b_row0)) + 8 * (q & 1);
-    b_base = (uint32_t)b_row0 * ldb2 + (uint32_t)((n0 + b_col) * 2);
+    const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
+#pragma unroll
+    for (int i = 0; i < C::B_UNITS; ++i)
+      b_voff[i] = (col < BN && n0 + col < p.N) ? (uint32_t)(kk + 16 * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
   }
 
-  // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS buffer `stage`.
-  auto dma_one = [&](int kt, char* stage, int d) {
+  // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
+  auto dma_one = [&](int kt, int s, int d) {
     const int k0 = kbeg + kt * BK;
-    const uint32_t la = lds_addr(stage);
+    const bool live = k0 < kend;  // uniform
     if (d < C::A_UNITS) {
-      const int i = d;
-      const bool ok = (m0 + a_row0 + 128 * i < p.M) && (k0 + a_chunk * 8 < kend);
-      const uint32_t off = a_base + (uint32_t)(128 * i) * lda2 + (uint32_t)(k0 * 2);
-      dma16(ra, ok ? off : kOOB, la + (wave + 8 * i) * 1024);
+      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u, lbase + s * C::A_BYTES + (wave + 8 * d) * 1024);
     } else {
       const int i = d - C::A_UNITS;
-      bool ok;
-      uint32_t off;
-      if constexpr (C::B_KC) {
-        const int row = b_row0 + 128 * i;
-        ok = (row < BN) && (n0 + row < p.N) && (k0 + b_col < kend);
-        off = b_base + (uint32_t)(128 * i) * ldb2 + (uint32_t)(k0 * 2);
-      } else {
-        ok = (k0 + b_row0 + 16 * i < kend) && (b_col < BN) && (n0 + b_col < p.N);
-        off = b_base + (uint32_t)(k0 + 16 * i) * ldb2;
-      }
-      dma16(rb, ok ? off : kOOB, la + C::A_BYTES + (wave + 8 * i) * 1024);
+      const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (uint32_t)k0 * ldb2;
+      dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + 8 * i) * 1024);
     }
   };
   constexpr int NDMA = C::A_UNITS + C::B_UNITS;
-  auto load_tile = [&](int kt, char* stage) {
-#pragma unroll
-    for (int d = 0; d < NDMA; ++d) dma_one(kt, stage, d);
-  };
 
-  // ---- fragments of one stage (one 32-k MFMA step) ----
-  // Per-lane LDS offsets, constant over stages: A rows wm0 + 16i + lr share
-  // one swizzle, so fragment i is a_off + 1 KB * i; B (natural) fragment j
-  // reads k rows 8*lg + lr/4 (+4 for the upper half, same swizzle, +2 KB).
-  const int a_off = (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
-  int b_off[FN];
+  // ---- fragment read addresses (constant over stages) ----
+  // A: rows wm0 + 16i + lr share one swizzle; fragment i of stage s is at
+  // a_rd + s * A_BYTES + 1 KB * i.
+  const lds_cptr l0 = (lds_cptr)lds;
+  const lds_cptr a_rd = l0 + (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
+  // B natural: the lane reads k rows k_lo = 8*lg + lr/4 (and k_lo + 4 for
+  // the upper half, same swizzle) in 32-byte unit U = wn0/16 + j for
+  // fragment j, stored at unit U ^ (k_lo & 3).  Only the low two bits of U
+  // are swizzled, so with t = j % 4 the unit of fragment j is that of
+  // fragment t plus 4 * (j / 4): fragment j of stage s is at
+  // b_rd[j % 4] + 128 * (j / 4) + s * B_BYTES (+ 2 KB for the upper half).
+  // B Linear: like A, fragment j of stage s at b_rd[0] + s * B_BYTES + 1 KB * j.
+  lds_cptr b_rd[4];
   if constexpr (C::B_KC) {
     const int row0 = wn0 + lr;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) b_off[j] = C::A_BYTES + (row0 + 16 * j) * 64 + ((lg ^ a_swz(row0)) << 4);
+    b_rd[0] = l0 + B_REGION + row0 * 64 + ((lg ^ a_swz(row0)) << 4);
+    b_rd[1] = b_rd[2] = b_rd[3] = b_rd[0];
   } else {
     const int k_lo = 8 * lg + (lr >> 2);
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      b_off[j] = C::A_BYTES + k_lo * C::B_PITCH + ((((wn0 >> 4) + j) ^ bnat_swz(k_lo)) << 5) + ((lr & 3) << 3);
+    for (int t = 0; t < 4; ++t) {
+      const int u = (wn0 >> 4) + t;
+      b_rd[t] = l0 + B_REGION + k_lo * C::B_PITCH + (((u & ~3) | ((u & 3) ^ bnat_swz(k_lo))) << 5) + ((lr & 3) << 3);
+    }
   }
+
   f32x4 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -245,36 +270,32 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
     u32x4 a[FM];
     u32x2 b[2 * FN];
   };
-  // Read number r of a stage's fragments: A blocks first, then B.
-  auto read_one = [&](const char* stage, int r, Frags& f) {
+  // Read number r of stage slot s's fragments: A blocks first, then B.
+  auto read_one = [&](int s, int r, Frags& f) {
     if (r < FM) {
-      f.a[r] = *reinterpret_cast<const u32x4*>(stage + a_off + 1024 * r);
+      f.a[r] = lds_read_b128(a_rd + s * C::A_BYTES + 1024 * r);
     } else if constexpr (C::B_KC) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(stage + b_off[r - FM]);
+      const u32x4 v = lds_read_b128(b_rd[0] + s * C::B_BYTES + 1024 * (r - FM));
       f.b[2 * (r - FM)] = u32x2{v.x, v.y};
       f.b[2 * (r - FM) + 1] = u32x2{v.z, v.w};
     } else {
       const int j = (r - FM) >> 1, hi = (r - FM) & 1;
-      f.b[2 * j + hi] = lds_read_tr(stage + b_off[j] + hi * 4 * C::B_PITCH);
+      f.b[2 * j + hi] = lds_read_tr(b_rd[j & 3] + 128 * (j >> 2) + s * C::B_BYTES + hi * 4 * C::B_PITCH);
     }
   };
   constexpr int NREAD = FM + (C::B_KC ? FN : 2 * FN);
-  auto read_frags = [&](const char* stage, Frags& f) {
-#pragma unroll
-    for (int r = 0; r < NREAD; ++r) read_one(stage, r, f);
-  };
   auto mfma_one = [&](int m, const Frags& f) {
     const int i = m / FN, j = m % FN;
     const u32x2 lo = f.b[2 * j], hi = f.b[2 * j + 1];
     acc[i][j] = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, f.a[i], acc[i][j], __bf16{});
   };
 
-  // Stage kt sits in buffer kt % 4.  Step kt runs the MFMAs of stage kt
+  // Stage kt sits in slot kt % 4.  Step kt runs the MFMAs of stage kt
   // (fragments already in registers, read in step kt-1) and, interleaved
   // one per MFMA so that no wave holds its MFMAs behind a burst of memory
   // instructions:
   //  * the fragment reads of stage kt+1;
-  //  * the DMA of stage kt+4 into buffer kt % 4, free since every wave's
+  //  * the DMA of stage kt+4 into slot kt % 4, free since every wave's
   //    reads of stage kt completed before the barrier that ended step kt-1.
   // Then it waits until stage kt+2 landed (stages kt+3 and kt+4 may still be
   // in flight: 8 DMA instructions) and meets the other waves at the barrier.
@@ -283,13 +304,13 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   Frags f0, f1;
   constexpr int NMFMA = FM * FN;
   static_assert(NREAD <= NMFMA && NDMA == 4, "one fragment read per MFMA slot");
-  auto step = [&](int kt, const char* next, char* own, const Frags& cur, Frags& nxt) {
+  auto step = [&](int kt, int s, const Frags& cur, Frags& nxt) {
 #pragma unroll
     for (int m = 0; m < NMFMA; ++m) {
-      if (m < NREAD) read_one(next, m, nxt);
+      if (m < NREAD) read_one((s + 1) % NS, m, nxt);
 #pragma unroll
       for (int d = 0; d < NDMA; ++d)
-        if (m == d * NMFMA / NDMA + 1) dma_one(kt + 4, own, d);
+        if (m == d * NMFMA / NDMA + 1) dma_one(kt + NS, s, d);
       mfma_one(m, cur);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -299,27 +320,28 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   };
 
   if (nk > 0) {
-    load_tile(0, lds0);
-    load_tile(1, lds1);
-    load_tile(2, lds2);
-    load_tile(3, lds3);
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int d = 0; d < NDMA; ++d) dma_one(s, s, d);
     wait_dma<8>();  // stages 0 and 1 landed
     __syncthreads();
-    read_frags(lds0, f0);
-    __syncthreads();  // every wave holds stage 0 before step 0 refills its buffer
+#pragma unroll
+    for (int r = 0; r < NREAD; ++r) read_one(0, r, f0);
+    __syncthreads();  // every wave holds stage 0 before step 0 refills its slot
     __builtin_amdgcn_sched_barrier(0);
   }
   for (int kt = 0; kt < nk; kt += 4) {
-    step(kt, lds1, lds0, f0, f1);
-    if (kt + 1 < nk) step(kt + 1, lds2, lds1, f1, f0);
-    if (kt + 2 < nk) step(kt + 2, lds3, lds2, f0, f1);
-    if (kt + 3 < nk) step(kt + 3, lds0, lds3, f1, f0);
+    step(kt, 0, f0, f1);
+    if (kt + 1 < nk) step(kt + 1, 1, f1, f0);
+    if (kt + 2 < nk) step(kt + 2, 2, f0, f1);
+    if (kt + 3 < nk) step(kt + 3, 3, f1, f0);
   }
   wait_dma<0>();  // drain DMAs of stages past the end before the block exits
 
   // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
   const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
-  char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)blockIdx.y * p.out_sstride) * esz;
+  char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm0 + 16 * i + lr;
