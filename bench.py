@@ -55,6 +55,9 @@ def _args(argv=None):
     p.add_argument("--only", choices=("prefill", "decode"), default=None,
                    help="run one part only (for profiler runs)")
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--copy-check", type=int, default=0, metavar="MIB",
+                   help="before the steps, copy a MIB-sized buffer 3 times (a plain copy kernel of known size "
+                        "for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     p.add_argument("--weights-layout", choices=("natural", "linear"), default="natural",
                    help="natural (in, out) factors as kernels/reference.py takes them, or PyTorch Linear "
                         "(out, in) storage passed as transposed views (test_speedup.py nki_mm)")
@@ -94,6 +97,23 @@ def _stage_work(T):
         "down_xuv": (2.0 * T * R * D, 2 * (T * R + R * D + T * D),
                      "big_gemm_kernel XUd.Vd (split-K fp32 slices)"),
     }
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_8b_T1024_traffic.md"
+
+
+def _profiled_traffic(stage):
+    """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel of known size),
+    or None when the summary has no line for it."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == stage:
+                return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def _time_steps(torch, fn, steps, warmup, stream):
@@ -168,6 +188,14 @@ def main(argv=None) -> int:
     gx.manual_seed(args.seed + 1000)
     x = torch.randn(T, D, generator=gx, device=dev, dtype=torch.float32).to(torch.bfloat16)
     flops = 2.0 * T * 3 * R * (D + FF)
+    if args.copy_check > 0:
+        n = args.copy_check << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     factor_bytes = 2 * (2 * R * (D + FF) + R * (FF + D))
     record: dict = {}
 
@@ -217,7 +245,9 @@ def main(argv=None) -> int:
                 "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4) if achieved else None,
-                "traffic": None,
+                "traffic": _profiled_traffic(dom) if (T, args.weights_layout) == (1024, "natural") else None,
+                "traffic_source": "profiles/prefill_8b_T1024_traffic.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                                  "per dispatch, calibrated on a 256 MiB copy",
                 "algorithmic_flop_per_launch": dom_flops,
                 "algorithmic_bytes_per_launch": dom_bytes,
                 "avg_launch_us": round(dom_ms * 1e3, 2) if dom_ms else None,

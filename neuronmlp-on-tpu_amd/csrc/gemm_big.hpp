@@ -68,7 +68,18 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // explicitly (wait_dma) before the barrier that publishes the stage.
 // GFX9 needs one wait state between an SALU write of M0 and an LDS DMA that
 // reads it (s_nop 0); the compiler's hazard pass does not look inside asm.
+// The descriptor, scalar offset and LDS base are wave-uniform by
+// construction; readfirstlane keeps them in SGPRs whatever the compiler's
+// uniformity analysis concludes.
+__device__ __forceinline__ i32x4 uniform4(i32x4 v) {
+  return i32x4{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+               __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+}
+
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+  rsrc = uniform4(rsrc);
+  soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)soff);
+  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_base);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
                : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff));
