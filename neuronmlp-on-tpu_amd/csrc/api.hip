@@ -21,6 +21,7 @@
 #include <cstdlib>
 
 #include "dispatch.hpp"
+#include "decode_layer.hpp"
 #include "gemm_big.hpp"
 #include "svdmlp.h"
 
@@ -66,12 +67,13 @@ enum Stage : int {
   ST_DEC_D_XUV,
   ST_FINALIZE,
   ST_GU_XUV_G,
+  ST_DEC_LAYER,
   ST_COUNT
 };
 const char* const kStageNames[ST_COUNT] = {
     "zero_fill",        "gate_up_xu",       "gate_up_xuv_swiglu", "down_xu",           "down_xuv",
     "decode_gate_up_xu", "decode_gate_up_xuv", "decode_down_xu",   "decode_down_xuv", "finalize",
-    "gate_up_xuv_g"};
+    "gate_up_xuv_g",    "decode_layer"};
 
 struct Profiler {
   std::mutex mu;
@@ -130,6 +132,7 @@ struct StageScope {
 size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
 
 struct Ws {
+  size_t sync;     // 4 KB of grid-barrier words (zero before first use)
   size_t xu_bf16;  // [2][T][r] bf16 (gate, up) rank-r intermediate
   size_t xu32;     // [3][T][r] fp32 (gate, up, down) split-K accumulators
   size_t gu32;     // [2][T][big] fp32 gate/up sums (decode)
@@ -146,6 +149,9 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   const bool dec = T <= kDecodeMaxT;
   Ws w;
   size_t off = 0;
+  w.sync = off;
+  off += 4096;
+  static_assert(kDlSyncBytes <= 4096, "barrier words fit the sync area");
   w.xu_bf16 = off;
   off += a256(2 * T * r * 2);
   w.xu32 = off;
@@ -307,6 +313,8 @@ struct Tune {
   int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 7 when ff % 224 == 0)
   int split = 256;    // CUs assumed by the split-K planner
   bool big = true;    // large-tile path enabled
+  bool dlayer = true; // persistent decode layer enabled
+  int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
 };
 
 const Tune& tune() {
@@ -329,6 +337,8 @@ const Tune& tune() {
         if (k == "s2fn") r.s2fn = v;
         if (k == "split") r.split = v;
         if (k == "big") r.big = v != 0;
+        if (k == "dlayer") r.dlayer = v != 0;
+        if (k == "dlmin") r.dlmin = v;
       }
       pos = end + 1;
     }
@@ -519,6 +529,68 @@ bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, 
   for (int64_t v : dims)
     if (v % 8) return false;
   return true;
+}
+
+// The persistent decode layer takes bf16 activations and factors in natural
+// layout, T <= 64, ranks and d multiples of 128 and ff a multiple of 64 (its
+// tiles), every operand below 2 GB (32-bit buffer offsets).
+// Below kDlMinT tokens the per-stage decode kernels are faster (measured on
+// MI355X, 8B shape: T=1 77 us vs 88 us; T=8 120 vs 95; T=64 539 vs 250).
+constexpr int64_t kDlMinT = 4;
+
+bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
+                     bool vec) {
+  if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T > kDecodeMaxT || !tune().dlayer) return false;
+  if (T < std::min<int64_t>(kDlMinT, tune().dlmin)) return false;
+  if (d % 128 || r_gu % 128 || r_d % 128 || ff % 64) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  for (int64_t bytes : {T * d * 2, d * r_gu * 2, r_gu * ff * 2, ff * r_d * 2, r_d * d * 2, T * ff * 2, 2 * T * r_gu * 4})
+    if (bytes >= lim) return false;
+  return decode_layer_grid(decode_layer_mt((int)T)) > 0;
+}
+
+// Split-K plan of one decode-layer phase: `tiles` 128-column tiles over K;
+// as many splits as keep tiles * splits within the grid, K per split a
+// multiple of 32.  Returns the K per split; *units = tiles * splits.
+int dl_plan(int64_t K, int64_t tiles, int grid, int* units) {
+  const int64_t s = std::max<int64_t>(1, grid / std::max<int64_t>(1, tiles));
+  int64_t ks = ((K + s - 1) / s + 31) / 32 * 32;
+  ks = std::min(ks, K);
+  *units = (int)(tiles * ((K + ks - 1) / ks));
+  return (int)ks;
+}
+
+int decode_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                 const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
+                 char* ws, const Ws& L) {
+  const int mt = decode_layer_mt((int)T);
+  const int grid = decode_layer_grid(mt);
+  DecLayerParams p{};
+  p.x = x;
+  p.ug = ug;
+  p.vg = vg;
+  p.uu = uu;
+  p.vu = vu;
+  p.ud = ud;
+  p.vd = vd;
+  p.y = y;
+  p.xu32 = reinterpret_cast<float*>(ws + L.xu32);
+  p.xd32 = p.xu32 + 2 * T * r_gu;
+  p.h = reinterpret_cast<uint16_t*>(ws + L.h);
+  p.y32 = reinterpret_cast<float*>(ws + L.y32);
+  p.sync = reinterpret_cast<uint64_t*>(ws + L.sync);
+  p.T = (int)T;
+  p.d = (int)d;
+  p.ff = (int)ff;
+  p.r_gu = (int)r_gu;
+  p.r_d = (int)r_d;
+  p.ks1 = dl_plan(d, 2 * r_gu / 128, grid, &p.units1);
+  p.units2 = (int)(ff / 64);
+  p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
+  p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
+  const char* why = nullptr;
+  StageScope ss(ST_DEC_LAYER, c.st);
+  return check(launch_decode_layer(p, mt, grid, c.st, &why), "decode layer", why);
 }
 
 int validate_dims(int64_t T, int64_t a, int64_t b, int64_t r) {
@@ -749,6 +821,9 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
   const float* S[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (fp8)
     for (int i = 0; i < 6; ++i) S[i] = scales[i];
+
+  if (decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec))
+    return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L);
 
   if (decode_ok(c, T, {d, ff, r_gu, r_d}, vec)) {
     float* xu32 = reinterpret_cast<float*>(ws + L.xu32);

@@ -1,0 +1,62 @@
+// Launcher of the persistent decode-layer kernel.  Grid = CU count with one
+// block per CU (its LDS takes most of a CU), so on an otherwise idle device
+// every block is resident at once.  A plain launch is used: a cooperative
+// launch guarantees residency but costs ~20 us per launch on this stack
+// (~2.3 us for a plain one).  If other work holds CUs, late blocks only delay
+// the barriers; the bounded barrier spin turns a true deadlock into a flagged
+// error instead of a hang.
+#include "decode_layer.hpp"
+#include "dispatch.hpp"
+
+namespace svdmlp {
+
+namespace {
+
+template <int MT>
+hipError_t coop(const DecLayerParams& p, int grid, hipStream_t st) {
+  hipLaunchKernelGGL(decode_layer_kernel<MT>, dim3(grid), dim3(kDlThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int MT>
+int blocks_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&decode_layer_kernel<MT>),
+                                                   kDlThreads, 0) != hipSuccess)
+    return 0;
+  return n;
+}
+
+}  // namespace
+
+int decode_layer_mt(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
+
+int decode_layer_grid(int mt) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  const int per = mt == 1 ? blocks_per_cu<1>() : (mt == 2 ? blocks_per_cu<2>() : blocks_per_cu<4>());
+  return per >= 1 ? cus : 0;
+}
+
+hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why) {
+  if (grid <= 0) {
+    *why = "decode layer: the kernel cannot be resident on this device";
+    return hipErrorInvalidValue;
+  }
+  hipError_t e;
+  if (mt == 1)
+    e = coop<1>(p, grid, st);
+  else if (mt == 2)
+    e = coop<2>(p, grid, st);
+  else if (mt == 4)
+    e = coop<4>(p, grid, st);
+  else {
+    *why = "decode layer: no instance for this token count";
+    return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess) *why = "decode layer: launch failed";
+  return e;
+}
+
+}  // namespace svdmlp

@@ -1,0 +1,535 @@
+// The whole SVD-MLP layer at decode shapes (T <= 64 tokens) in one
+// persistent, cooperatively launched kernel.
+//
+// At these shapes the layer is a stream of 311 MB of bf16 factors (LLaMA3-8B,
+// r = 2816) against a few KB of activations, so the design goal is to keep
+// HBM busy from the first byte to the last:
+//  * one block per CU (grid = CU count; the LDS footprint keeps it to one);
+//  * weights go global -> LDS by direct DMA through a ring of 4 to 6 stages
+//    of one or two 32-k chunks (by token count: the activation tile shares
+//    the ring).  A chunk is 32 k x 128 columns, stored as two 64-column
+//    sub-tiles of 128-byte rows whose 32-byte units are XOR-swizzled by
+//    k & 3, and read with the transposing ds_read_b64_tr_b16, so no
+//    register transpose exists;
+//  * the activation rows (zero-padded to 16 * MT) follow in the same ring;
+//  * the layer runs as phases separated by grid barriers:
+//      0  zero the fp32 accumulators
+//      1  XU_g, XU_u += X . [Ug | Uu]               (split-K, fp32 atomics)
+//      2  h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu))    (a block owns 64 columns
+//         of both branches over the whole rank: no split, no atomics)
+//      3  XU_d += h . Ud                             (split-K, fp32 atomics)
+//      4  y32 += XU_d . Vd                           (split-K, fp32 atomics)
+//      5  y = bf16(y32)
+//    The fp32 rank sums XU and XU_d are rounded to bf16 where they are read
+//    (the reference rounds the rank-r intermediate to the activation dtype);
+//  * before waiting at a barrier, every block already issues the weight DMAs
+//    of its first stages of the next phase (weights do not depend on the
+//    barrier), so barrier latency overlaps the weight stream.
+// Data crosses phases only through device-coherent accesses: fp32 atomics,
+// device-scope (sc1) stores of h and of the zero fill, and device-scope
+// loads (the activation DMAs, the final read of y32).  Each wave waits for
+// its own writes (vmcnt(0)) before its block arrives at a barrier, so the
+// barriers need no cache write-back or invalidation (with agent-scope fences
+// a barrier costs ~9 us, without ~2 us).
+// Grid barriers are two-level: blocks arrive on one of 16 group counters,
+// the last of a group arrives on a root counter, and the last root arrival
+// advances a generation word that every block polls (a single counter for
+// all blocks serialises 256 device-scope atomics, ~15 us).  The 64-bit
+// counters only ever grow: a launch reads the generation at its start and
+// waits for start + k at barrier k, and group / root completion is taken
+// modulo the group size, so no reset is needed as long as every launch on a
+// workspace uses the same grid.  Polls are bounded; on timeout a flag is set
+// and the kernel runs to its end.
+#pragma once
+
+#include "gemm_big.hpp"
+
+namespace svdmlp {
+
+struct DecLayerParams {
+  const void* x;  // (T, d) bf16
+  const void* ug;
+  const void* vg;
+  const void* uu;
+  const void* vu;
+  const void* ud;
+  const void* vd;
+  void* y;         // (T, d) bf16
+  float* xu32;     // (2, T, r_gu) gate/up rank sums
+  uint16_t* h;     // (T, ff) bf16
+  float* xd32;     // (T, r_d)
+  float* y32;      // (T, d)
+  uint64_t* sync;  // barrier words, one per 128-byte line (kDlSync*)
+  int T, d, ff, r_gu, r_d;
+  int ks1, ks3, ks4;                   // K per split, phases 1, 3, 4 (multiples of 32)
+  int units1, units2, units3, units4;  // tiles x splits
+};
+
+constexpr int kDlThreads = 512;
+constexpr int kDlWStage = 8192;    // 32 k x 128 columns bf16
+constexpr uint32_t kDlSpinLimit = 1u << 22;
+// Barrier words in the workspace's sync area, one 128-byte line each (in
+// uint64 units): kDlGroups group counters, then root, generation, timeout.
+constexpr int kDlGroups = 16;
+constexpr int kDlLine = 16;
+constexpr int kDlRoot = kDlGroups * kDlLine;
+constexpr int kDlGen = kDlRoot + kDlLine;
+constexpr int kDlFlag = kDlGen + kDlLine;
+constexpr int kDlSyncBytes = (kDlFlag + kDlLine) * 8;
+
+// Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
+// weight bytes per block barrier) and the ring holds NS stages, as far as
+// the activation tile, which shares the ring, leaves room.
+template <int MT>
+struct DlDepth {
+  static constexpr int KC = MT == 4 ? 1 : 2;
+  static constexpr int NS = MT == 2 ? 4 : 6;
+};
+
+template <int N>
+__device__ __forceinline__ void dl_wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Block barrier that publishes LDS writes (ds, and DMA after the issuing
+// wave's vmcnt wait) without a global-memory fence.
+__device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Grid barrier k of this launch (gen0: generation at launch start).  Every
+// wave has completed its own global writes (vmcnt(0)) before calling.
+__device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k) {
+  dl_block_sync();
+  if (threadIdx.x == 0) {
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t g = b % kDlGroups;
+    const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
+    const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
+    const uint64_t a = __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((a + 1) % gsize == 0) {
+      const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((r + 1) % ngroups == 0)
+        __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    uint32_t polls = 0;
+    while ((int64_t)(__hip_atomic_load(&sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - gen0 - k) < 0) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++polls >= kDlSpinLimit) {
+        __hip_atomic_fetch_or(&sync[kDlFlag], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  dl_block_sync();
+}
+
+// Device-scope 8-byte store / load (sc1): coherent across XCDs without cache
+// maintenance.
+__device__ __forceinline__ void dl_store8(void* p, u32x2 v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u32x2 dl_load8(const void* p) {
+  return __builtin_bit_cast(u32x2, __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ void dl_atomic_add(float* p, float v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One unit of a phase: an output tile of 16*MT rows x 128 columns over the
+// k range [kb, ke).  DUAL: sub-tile 0 is branch g (A = a0, B = b0), sub-tile
+// 1 branch u (A = a1, B = b1), both over columns n0..n0+63; otherwise both
+// sub-tiles read B = b0 (columns n0..n0+127) against A = a0.
+struct DlUnit {
+  const void* a0;
+  const void* a1;
+  int64_t lda;  // elements
+  const void* b0;
+  const void* b1;
+  int64_t ldb;  // elements
+  uint32_t a_bytes, b_bytes;
+  int n0, kb, ke;
+  float* out;  // atomic target (row-major, ldo)
+  int64_t ldo;
+};
+
+// Compile-time shape of a unit: AF32 = fp32 activations (rank sums).
+template <int MT, bool AF32, bool DUAL>
+struct DlShape {
+  static constexpr int A_ROW = AF32 ? 128 : 64;            // bytes per 32-k activation row
+  static constexpr int A_SUB = 16 * MT * A_ROW;             // one branch of one stage
+  static constexpr int NA = (DUAL ? 2 : 1) * A_SUB / 1024;  // 1 KB DMA instructions per stage
+  static constexpr int CNT_A = (NA + 7) / 8;                // per wave per chunk (padded with dummies)
+  static constexpr int KC = DlDepth<MT>::KC;
+  static constexpr int P = KC * (1 + CNT_A);                // DMA instructions per wave per stage
+};
+
+template <int MT>
+struct DlLds {
+  static constexpr int NS = DlDepth<MT>::NS;
+  static constexpr int KC = DlDepth<MT>::KC;
+  static constexpr int A_CHUNK = MT * 16 * 128 * 2;  // one 32-k chunk: fp32, two branches (the largest case)
+  static constexpr int W_SLOT = KC * kDlWStage;
+  static constexpr int A_SLOT = KC * A_CHUNK;
+  static constexpr int W_OFF = 0;
+  static constexpr int A_OFF = NS * W_SLOT;
+  static constexpr int DUMMY_OFF = A_OFF + NS * A_SLOT;
+  static constexpr int BYTES = DUMMY_OFF + 1024;
+  static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+struct DlCtx {
+  uint32_t lbase;  // LDS byte address of the block's array
+  lds_cptr l0;
+  int wave, lane, lr, lg, T;
+};
+
+// Weight DMA of stage j into ring slot `slot` (one instruction per wave):
+// rows 8*(wave%4)..+7 of sub-tile wave/4; lane L takes row 8*(wave%4) + L/8,
+// physical chunk L%8 of 32-byte unit pu = (L%8)/2, which holds logical unit
+// pu ^ (row & 3).
+template <int MT, bool DUAL>
+__device__ __forceinline__ void dl_dma_w(const DlCtx& c, const DlUnit& U, int j, int slot) {
+  using L = DlLds<MT>;
+  const int sub = c.wave >> 2;
+  const int row = 8 * (c.wave & 3) + (c.lane >> 3);
+  const int col = (DUAL ? 0 : 64 * sub) + 16 * (((c.lane & 7) >> 1) ^ (row & 3)) + 8 * (c.lane & 1);
+  const void* bp = (DUAL && sub) ? U.b1 : U.b0;
+  const uint32_t voff = (uint32_t)row * (uint32_t)U.ldb * 2u + (uint32_t)(U.n0 + col) * 2u;
+#pragma unroll
+  for (int kc = 0; kc < L::KC; ++kc) {
+    const int k0 = U.kb + 32 * (L::KC * j + kc);
+    const bool live = k0 < U.ke;
+    const i32x4 rs = make_rsrc_sgpr(bp, live ? U.b_bytes : 0u);
+    dma16(rs, voff, live ? (uint32_t)k0 * (uint32_t)U.ldb * 2u : 0u,
+          c.lbase + L::W_OFF + slot * L::W_SLOT + kc * kDlWStage + sub * 4096 + (c.wave & 3) * 1024);
+  }
+}
+
+// Activation DMAs of stage j into ring slot `slot` (CNT_A per wave).
+// bf16: instruction q holds rows 16q..16q+15 (64 bytes each, 16-byte chunk
+// XOR a_swz(row)); fp32: instruction q holds rows 8q..8q+7 (128 bytes each,
+// chunk XOR (row & 7)) of branch q / (NA/2) when DUAL.  Instructions past NA
+// are dummies (no records) into a scratch slot, keeping the per-wave count.
+template <int MT, bool AF32, bool DUAL>
+__device__ __forceinline__ void dl_dma_a(const DlCtx& c, const DlUnit& U, int j, int slot) {
+  using S = DlShape<MT, AF32, DUAL>;
+  using L = DlLds<MT>;
+#pragma unroll
+  for (int kc = 0; kc < L::KC; ++kc) {
+    const int k0 = U.kb + 32 * (L::KC * j + kc);
+    const bool live = k0 < U.ke;
+#pragma unroll
+    for (int ci = 0; ci < S::CNT_A; ++ci) {
+      const int q = c.wave + 8 * ci;
+      if (q < S::NA) {
+        constexpr int PER = DUAL ? S::NA / 2 : S::NA;
+        const int br = DUAL ? q / PER : 0, qq = q % PER;
+        const void* ap = br ? U.a1 : U.a0;
+        const i32x4 rs = make_rsrc_sgpr(ap, live ? U.a_bytes : 0u);
+        int row, lchunk;
+        uint32_t voff;
+        if constexpr (AF32) {
+          row = 8 * qq + (c.lane >> 3);
+          lchunk = (c.lane & 7) ^ (row & 7);
+          voff = row < c.T ? (uint32_t)row * (uint32_t)U.lda * 4u + (uint32_t)lchunk * 16u : kOOB;
+        } else {
+          row = 16 * qq + (c.lane >> 2);
+          lchunk = (c.lane & 3) ^ a_swz(row);
+          voff = row < c.T ? (uint32_t)row * (uint32_t)U.lda * 2u + (uint32_t)lchunk * 16u : kOOB;
+        }
+        const uint32_t soff = live ? (uint32_t)k0 * (AF32 ? 4u : 2u) : 0u;
+        dma16_dev(rs, voff, soff, c.lbase + L::A_OFF + slot * L::A_SLOT + kc * L::A_CHUNK + br * S::A_SUB + qq * 1024);
+      } else {
+        dma16_dev(make_rsrc_sgpr(U.a0, 0u), kOOB, 0u, c.lbase + L::DUMMY_OFF);
+      }
+    }
+  }
+}
+
+// vmcnt wait for stage j in the first NS-2 steps (KC chunks per stage,
+// CNT_A activation DMAs per chunk): the activation DMAs of stages
+// j+1..NS-2 and the j steps' (W, A) DMAs were issued after it:
+// (NS-2) * KC * CNT_A + j * KC in all (B + J * STEP).
+template <int B, int STEP, int J, int NMAX>
+__device__ __forceinline__ void dl_wait_head(int j) {
+  if constexpr (J < NMAX) {
+    if (j == J) {
+      dl_wait_vm<B + J * STEP>();
+      return;
+    }
+    dl_wait_head<B, STEP, J + 1, NMAX>(j);
+  }
+}
+
+// Runs one unit: returns the accumulators (lane: D[n = 4*lg + t][m = lr] of
+// each 16-row block mt).  `prefetched`: waves 1..7 already issued their
+// weight DMAs of stages 0..NS-2 (before the grid barrier); wave 0 issues
+// its own here, ahead of the activation DMAs, keeping every wave's order
+// W(0..NS-2), A(0..NS-2), then (W, A) per step.
+template <int MT, bool AF32, bool DUAL>
+__device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool prefetched, f32x4 (&acc)[MT]) {
+  using S = DlShape<MT, AF32, DUAL>;
+  using L = DlLds<MT>;
+  constexpr int NS = L::NS, KC = L::KC;
+  const int nk = (U.ke - U.kb + 32 * KC - 1) / (32 * KC);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (!prefetched || c.wave == 0)
+    for (int s = 0; s < NS - 1; ++s) dl_dma_w<MT, DUAL>(c, U, s, s);
+  for (int s = 0; s < NS - 1; ++s) dl_dma_a<MT, AF32, DUAL>(c, U, s, s);
+
+  // fragment addresses within a slot
+  const int sub = c.wave >> 2, lu = c.wave & 3;
+  const int k_lo = 8 * c.lg + (c.lr >> 2);
+  const int b_off = L::W_OFF + sub * 4096 + k_lo * 128 + ((lu ^ (k_lo & 3)) << 5) + ((c.lr & 3) << 3);
+  const int abr = DUAL ? sub : 0;
+
+  for (int j = 0; j < nk; ++j) {
+    if (j < NS - 2)
+      dl_wait_head<(NS - 2) * KC * S::CNT_A, KC, 0, NS - 2>(j);
+    else
+      dl_wait_vm<(NS - 2) * S::P>();
+    dl_block_sync();
+    const int sn = j + NS - 1, slot_n = sn % NS;
+    dl_dma_w<MT, DUAL>(c, U, sn, slot_n);
+    dl_dma_a<MT, AF32, DUAL>(c, U, sn, slot_n);
+
+    const int slot = j % NS;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const lds_cptr wb = c.l0 + slot * L::W_SLOT + kc * kDlWStage + b_off;
+      const u32x2 lo = lds_read_tr(wb), hi = lds_read_tr(wb + 512);
+      const u32x4 fb = u32x4{lo.x, lo.y, hi.x, hi.y};
+      const lds_cptr ab = c.l0 + L::A_OFF + slot * L::A_SLOT + kc * L::A_CHUNK + abr * S::A_SUB;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = 16 * mt + c.lr;
+        u32x4 fa;
+        if constexpr (AF32) {
+          const lds_cptr rp = ab + row * 128;
+          const int x = row & 7;
+          const u32x4 v0 = lds_read_b128(rp + (((2 * c.lg) ^ x) << 4));
+          const u32x4 v1 = lds_read_b128(rp + (((2 * c.lg + 1) ^ x) << 4));
+          fa = u32x4{pack_bf16x2(__uint_as_float(v0.x), __uint_as_float(v0.y)),
+                     pack_bf16x2(__uint_as_float(v0.z), __uint_as_float(v0.w)),
+                     pack_bf16x2(__uint_as_float(v1.x), __uint_as_float(v1.y)),
+                     pack_bf16x2(__uint_as_float(v1.z), __uint_as_float(v1.w))};
+        } else {
+          fa = lds_read_b128(ab + row * 64 + ((c.lg ^ a_swz(row)) << 4));
+        }
+        acc[mt] = mfma_chunk(fb, fa, acc[mt], __bf16{});
+      }
+    }
+  }
+  dl_wait_vm<0>();  // drain run-out DMAs before the ring is reused
+  dl_block_sync();
+}
+
+// fp32 atomics of a unit's accumulators into U.out.
+template <int MT, bool DUAL>
+__device__ __forceinline__ void dl_atomic_out(const DlCtx& c, const DlUnit& U, const f32x4 (&acc)[MT]) {
+  const int n = U.n0 + (DUAL ? 0 : 64 * (c.wave >> 2)) + 16 * (c.wave & 3) + 4 * c.lg;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + c.lr;
+    if (m < c.T) {
+      float* o = U.out + (int64_t)m * U.ldo + n;
+      dl_atomic_add(o + 0, acc[mt].x);
+      dl_atomic_add(o + 1, acc[mt].y);
+      dl_atomic_add(o + 2, acc[mt].z);
+      dl_atomic_add(o + 3, acc[mt].w);
+    }
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerParams p) {
+  using L = DlLds<MT>;
+  __shared__ __attribute__((aligned(1024))) char lds[L::BYTES];
+  DlCtx c;
+  c.lbase = lds_addr(lds);
+  c.l0 = (lds_cptr)lds;
+  c.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  c.lane = threadIdx.x & 63;
+  c.lr = c.lane & 15;
+  c.lg = c.lane >> 4;
+  c.T = p.T;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int T = p.T;
+  constexpr int NS = L::NS;
+  uint32_t nbar = 0;
+  // Generation at launch start: it cannot advance before every block has
+  // arrived at barrier 1, which each block does only after this read.
+  const uint64_t gen0 = __hip_atomic_load(&p.sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  auto unit_of = [&](int phase, int u, DlUnit& U) {
+    if (phase == 1) {
+      const int per = p.r_gu / 128, nt = 2 * per;
+      const int tile = u % nt, split = u / nt, br = tile / per;
+      U.a0 = U.a1 = p.x;
+      U.lda = p.d;
+      U.a_bytes = (uint32_t)((int64_t)T * p.d * 2);
+      U.b0 = U.b1 = br ? p.uu : p.ug;
+      U.ldb = p.r_gu;
+      U.b_bytes = (uint32_t)((int64_t)p.d * p.r_gu * 2);
+      U.n0 = (tile % per) * 128;
+      U.kb = split * p.ks1;
+      U.ke = min(p.d, U.kb + p.ks1);
+      U.out = p.xu32 + (int64_t)br * T * p.r_gu;
+      U.ldo = p.r_gu;
+    } else if (phase == 2) {
+      U.a0 = p.xu32;
+      U.a1 = p.xu32 + (int64_t)T * p.r_gu;
+      U.lda = p.r_gu;
+      U.a_bytes = (uint32_t)((int64_t)T * p.r_gu * 4);
+      U.b0 = p.vg;
+      U.b1 = p.vu;
+      U.ldb = p.ff;
+      U.b_bytes = (uint32_t)((int64_t)p.r_gu * p.ff * 2);
+      U.n0 = u * 64;
+      U.kb = 0;
+      U.ke = p.r_gu;
+      U.out = nullptr;
+      U.ldo = p.ff;
+    } else if (phase == 3) {
+      const int nt = p.r_d / 128;
+      const int tile = u % nt, split = u / nt;
+      U.a0 = U.a1 = p.h;
+      U.lda = p.ff;
+      U.a_bytes = (uint32_t)((int64_t)T * p.ff * 2);
+      U.b0 = U.b1 = p.ud;
+      U.ldb = p.r_d;
+      U.b_bytes = (uint32_t)((int64_t)p.ff * p.r_d * 2);
+      U.n0 = tile * 128;
+      U.kb = split * p.ks3;
+      U.ke = min(p.ff, U.kb + p.ks3);
+      U.out = p.xd32;
+      U.ldo = p.r_d;
+    } else {
+      const int nt = p.d / 128;
+      const int tile = u % nt, split = u / nt;
+      U.a0 = U.a1 = p.xd32;
+      U.lda = p.r_d;
+      U.a_bytes = (uint32_t)((int64_t)T * p.r_d * 4);
+      U.b0 = U.b1 = p.vd;
+      U.ldb = p.d;
+      U.b_bytes = (uint32_t)((int64_t)p.r_d * p.d * 2);
+      U.n0 = tile * 128;
+      U.kb = split * p.ks4;
+      U.ke = min(p.r_d, U.kb + p.ks4);
+      U.out = p.y32;
+      U.ldo = p.d;
+    }
+  };
+  const int units[5] = {0, p.units1, p.units2, p.units3, p.units4};
+  // Waves 1..7 issue the first weight stages of this block's first unit of
+  // `phase` (wave 0 issues its share after the barrier).
+  auto prefetch = [&](int phase) {
+    if (b < units[phase] && c.wave != 0) {
+      DlUnit U;
+      unit_of(phase, b, U);
+      for (int s = 0; s < NS - 1; ++s) {
+        if (phase == 2)
+          dl_dma_w<MT, true>(c, U, s, s);
+        else
+          dl_dma_w<MT, false>(c, U, s, s);
+      }
+    }
+  };
+
+  // ---- phase 0: zero the accumulators ----
+  {
+    const int64_t tid = (int64_t)b * kDlThreads + threadIdx.x, stride = (int64_t)G * kDlThreads;
+    const u32x2 z = {0u, 0u};
+    const int64_t n1 = (int64_t)2 * T * p.r_gu / 2, n2 = (int64_t)T * p.r_d / 2, n3 = (int64_t)T * p.d / 2;
+    for (int64_t i = tid; i < n1; i += stride) dl_store8(p.xu32 + 2 * i, z);
+    for (int64_t i = tid; i < n2; i += stride) dl_store8(p.xd32 + 2 * i, z);
+    for (int64_t i = tid; i < n3; i += stride) dl_store8(p.y32 + 2 * i, z);
+  }
+  dl_wait_vm<0>();
+  prefetch(1);
+  dl_grid_sync(p.sync, gen0, ++nbar);
+
+  // ---- phase 1: XU_g, XU_u += X . [Ug | Uu] ----
+  for (int u = b; u < units[1]; u += G) {
+    DlUnit U;
+    unit_of(1, u, U);
+    f32x4 acc[MT];
+    dl_run<MT, false, false>(c, U, u == b, acc);
+    dl_atomic_out<MT, false>(c, U, acc);
+  }
+  dl_wait_vm<0>();
+  prefetch(2);
+  dl_grid_sync(p.sync, gen0, ++nbar);
+
+  // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
+  for (int u = b; u < units[2]; u += G) {
+    DlUnit U;
+    unit_of(2, u, U);
+    f32x4 acc[MT];
+    dl_run<MT, true, true>(c, U, u == b, acc);
+    // waves 4..7 hold u, waves 0..3 g, for the same lanes' (m, n)
+    f32x4* xch = reinterpret_cast<f32x4*>(lds + L::A_OFF);
+    if (c.wave >= 4) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xch[((c.wave - 4) * MT + mt) * 64 + c.lane] = acc[mt];
+    }
+    dl_block_sync();
+    if (c.wave < 4) {
+      const int n = U.n0 + 16 * c.wave + 4 * c.lg;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = 16 * mt + c.lr;
+        const f32x4 uv = xch[(c.wave * MT + mt) * 64 + c.lane];
+        if (m < T) {
+          const f32x4 g = acc[mt];
+          dl_store8(p.h + (int64_t)m * p.ff + n, u32x2{pack_bf16x2(silu_f32(g.x) * uv.x, silu_f32(g.y) * uv.y),
+                                                        pack_bf16x2(silu_f32(g.z) * uv.z, silu_f32(g.w) * uv.w)});
+        }
+      }
+    }
+    dl_block_sync();
+  }
+  dl_wait_vm<0>();
+  prefetch(3);
+  dl_grid_sync(p.sync, gen0, ++nbar);
+
+  // ---- phase 3: XU_d += h . Ud ----
+  for (int u = b; u < units[3]; u += G) {
+    DlUnit U;
+    unit_of(3, u, U);
+    f32x4 acc[MT];
+    dl_run<MT, false, false>(c, U, u == b, acc);
+    dl_atomic_out<MT, false>(c, U, acc);
+  }
+  dl_wait_vm<0>();
+  prefetch(4);
+  dl_grid_sync(p.sync, gen0, ++nbar);
+
+  // ---- phase 4: y32 += XU_d . Vd ----
+  for (int u = b; u < units[4]; u += G) {
+    DlUnit U;
+    unit_of(4, u, U);
+    f32x4 acc[MT];
+    dl_run<MT, true, false>(c, U, u == b, acc);
+    dl_atomic_out<MT, false>(c, U, acc);
+  }
+  dl_wait_vm<0>();
+  dl_grid_sync(p.sync, gen0, ++nbar);
+
+  // ---- phase 5: y = bf16(y32) ----
+  {
+    const int64_t tid = (int64_t)b * kDlThreads + threadIdx.x, stride = (int64_t)G * kDlThreads;
+    const int64_t n = (int64_t)T * p.d / 2;
+    for (int64_t i = tid; i < n; i += stride) {
+      const u32x2 v = dl_load8(p.y32 + 2 * i);
+      reinterpret_cast<uint32_t*>(p.y)[i] = pack_bf16x2(__uint_as_float(v.x), __uint_as_float(v.y));
+    }
+  }
+
+}
+
+}  // namespace svdmlp

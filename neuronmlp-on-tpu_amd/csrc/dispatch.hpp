@@ -35,6 +35,7 @@ struct BigDesc {
 };
 
 struct BigParams;
+struct DecLayerParams;
 
 // Block tile of the prefill GEMM (rows x cols of C per 256-thread block).
 constexpr int kGemmBM = 128;
@@ -51,6 +52,11 @@ hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batc
 hipError_t launch_decode(const DecodeDesc& d, const DecodeParams& p, int blocks, hipStream_t st,
                          const char** why);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
+// Persistent decode layer (T <= 64): token tiles of 16 rows (1, 2 or 4),
+// grid = CU count when the kernel fits one block per CU, else 0.
+int decode_layer_mt(int T);
+int decode_layer_grid(int mt);
+hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why);
 hipError_t launch_cvt_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st);
 // out[i] = bf16(sum_s in[s * stride + i]) for s < slices.
 hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint16_t* out, int64_t n,

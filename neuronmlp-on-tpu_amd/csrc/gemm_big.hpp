@@ -85,6 +85,18 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, 
                : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff));
 }
 
+// As dma16, but a device-scope (sc1) load: it bypasses the non-coherent
+// caches, so it sees data that other XCDs wrote with device-scope stores or
+// atomics without any cache maintenance.
+__device__ __forceinline__ void dma16_dev(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+  rsrc = uniform4(rsrc);
+  soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)soff);
+  lds_base = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_base);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen sc1 lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff));
+}
+
 template <int N>
 __device__ __forceinline__ void wait_dma() {
   static_assert(N == 0 || N == 4 || N == 8, "vmcnt literal");

@@ -155,8 +155,12 @@ def _stream(dev: torch.device) -> int:
 
 
 def _workspace(dev, T, d, ff, r, w_code) -> torch.Tensor:
+    """Workspace of the C ABI's size; its first 4 KB (grid-barrier words of
+    the persistent decode kernel) start at zero, as the ABI requires."""
     nbytes = _lib.workspace_bytes(T, d, ff, r, w_code)
-    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+    ws = torch.empty(max(nbytes, 4096), dtype=torch.uint8, device=dev)
+    ws[:4096].zero_()
+    return ws
 
 
 # ---------------------------------------------------------------------------

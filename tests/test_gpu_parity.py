@@ -19,6 +19,7 @@ pytestmark = pytest.mark.gpu
 
 BF16_TOL = 1e-2
 FP8_TOL = 3e-2
+DECODE_LAYER_MIN_T = 4   # kDlMinT in csrc/api.hip
 
 
 def _to(a, dtype, dev):
@@ -195,6 +196,34 @@ def test_prefill_token_counts(gpu, T):
     hb = inputs.as_float32(h, torch.bfloat16)
     y = _np(ops.fused_xuv(_to(hb, torch.bfloat16, gpu), t[5], t[6]))
     assert _rel(y, O.fused_xuv_ref(hb, fb[4], fb[5], "bfloat16")) < BF16_TOL
+
+
+def _barrier_state(ws):
+    """(generation, timeout flag) of the decode kernel's barrier words."""
+    w = ws[:4096].view(torch.int64).cpu().tolist()
+    return w[272], w[288]
+
+
+@pytest.mark.parametrize("shape,Ts", [
+    (inputs.LayerShape(1024, 2048, 512), (1, 3, 17, 40, 64, 16)),      # every token-tile count, reused workspace
+    (inputs.LayerShape(1024, 32768, 256), (5, 33)),                     # 512 column tiles: two units per block
+])
+def test_decode_layer_workspace_reuse(gpu, shape, Ts):
+    """The persistent decode kernel (one cooperative launch, grid barriers
+    in the workspace's first 256 bytes) over one reused workspace: results
+    match the oracle, every call advances the barrier generation by its five
+    barriers and no barrier times out."""
+    x, f = inputs.make_layer(shape, T=max(Ts), seed=31)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ws = ops.svd_mlp_workspace(t[0], r=shape.r, ff=shape.ff)
+    gen = 0
+    for T in Ts:
+        y = _np(ops.svd_mlp(t[0][:T].contiguous(), *t[1:], workspace=ws))
+        err = _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16"))
+        assert err < BF16_TOL, (T, err)
+        gen += 5 if T >= DECODE_LAYER_MIN_T else 0   # fewer tokens take the per-stage kernels
+        assert _barrier_state(ws) == (gen, 0), T
 
 
 def test_decode_and_prefill_paths_agree(gpu, layer8b):
