@@ -109,6 +109,20 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
                    int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * One MLP block of the model: y = x + svd_mlp(RMSNorm(x) * norm_w), with
+ * RMSNorm in fp32 (x * rsqrt(mean(x^2) + eps), times the fp32 gain, rounded
+ * to the activation dtype) and the residual add rounded to the activation
+ * dtype.  norm_w holds d fp32 gains; y must not alias x.  Replaces the MLP
+ * half of bench/e2e_block.py:268-278 (_fused_svd_block) with LlamaRMSNorm,
+ * models/modeling_llama.py:253-262.
+ */
+int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
+                         const void* uu, const void* vu, const void* ud, const void* vd,
+                         const float* const* scales /* 6 or NULL */, void* y, int64_t T, int64_t d, int64_t ff,
+                         int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                         void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * Per-stage GPU timing (no counterpart in the reference, whose timing is host
  * wall clock around block_until_ready, test_speedup.py:739-749).  While
  * enabled, every stage launch of the calls above is bracketed by hipEvents

@@ -14,6 +14,8 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <array>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -139,10 +141,43 @@ struct Ws {
   size_t h;        // [T][big] h of the fused layer (4 bytes/elem worst case)
   size_t y32;      // [T][big] fp32 output accumulator (decode)
   size_t part;     // [splits][batch][T][N] fp32 split-K partial slices (prefill)
+  size_t norm;     // [T][d] RMSNorm output of the MLP block (4 bytes/elem worst case)
   size_t total;
 };
 
 int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch);
+
+// Bytes of split-K partial slices for any call with ranks <= r: the
+// large-tile stages X.U (gate/up, batch 2), h.Ud and XU.V (both output
+// widths), planned as the launches plan them.  The slice size is not
+// monotone in the rank (the split count changes with the tile count), so the
+// maximum over every rank up to r (multiples of 8, the large-tile path's
+// alignment) is taken; the result is cached per shape.
+int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
+  static std::mutex mu;
+  static std::map<std::array<int64_t, 4>, int64_t> memo;
+  const std::array<int64_t, 4> key{T, d, ff, r};
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = memo.find(key);
+    if (it != memo.end()) return it->second;
+  }
+  int64_t part = 0;
+  for (int64_t rr = std::min<int64_t>(r, 8); rr <= r; rr += (rr + 8 <= r ? 8 : std::max<int64_t>(1, r - rr))) {
+    // {K, N, batch, fn}: the rank is N of the X.U stages and K of the XU.V stages
+    const int64_t stages[][4] = {{d, rr, 2, 8}, {ff, rr, 1, 8}, {rr, d, 1, 8}, {rr, ff, 1, 8}, {rr, d, 1, 4},
+                                 {rr, ff, 1, 4}};
+    for (const auto& st : stages) {
+      const int sp = plan_splits(T, st[0], st[1], (int)st[3], (int)st[2]);
+      if (sp > 1) part = std::max(part, (int64_t)sp * st[2] * T * st[1] * 4);
+    }
+    if (rr == r) break;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (memo.size() > 4096) memo.clear();
+  memo[key] = part;
+  return part;
+}
 
 Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   const int64_t big = std::max(d, ff);
@@ -162,16 +197,11 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   off += a256(T * big * 4);
   w.y32 = off;
   off += a256(T * big * 4);
-  // split-K partial slices of the large-tile stages: X.U (gate/up, batch 2),
-  // h.Ud, XU.V (both output widths), sized by the same planner the launches use
-  int64_t part = 0;
-  const int64_t stages[][4] = {{d, r, 2, 8}, {ff, r, 1, 8}, {r, d, 1, 8}, {r, ff, 1, 8}, {r, d, 1, 4}, {r, ff, 1, 4}};
-  for (const auto& st : stages) {
-    const int sp = plan_splits(T, st[0], st[1], (int)st[3], (int)st[2]);
-    if (sp > 1) part = std::max(part, (int64_t)sp * st[2] * T * st[1] * 4);
-  }
+  const int64_t part = part_bytes(T, d, ff, r);
   w.part = off;
   off += a256(part);
+  w.norm = off;
+  off += a256(T * d * 4);
   w.total = off;
   return w;
 }
@@ -610,6 +640,30 @@ extern "C" {
 int svdmlp_version(void) { return SVDMLP_VERSION; }
 
 const char* svdmlp_last_error(void) { return g_err.c_str(); }
+
+int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
+                         const void* uu, const void* vu, const void* ud, const void* vd, const float* const* scales,
+                         void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
+                         int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
+  g_err.clear();
+  int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
+  if (rc) return rc;
+  if ((rc = check_types(act_dtype, w_dtype))) return rc;
+  if (!x || !norm_w || !y || !workspace) return fail("null pointer argument");
+  if (x == y) return fail("x and y must not alias (y receives the MLP output before the residual add)");
+  if (!(eps > 0.0f)) return fail("eps must be positive, got %g", (double)eps);
+  const int64_t r = std::max(r_gu, r_d);
+  const Ws L = ws_layout(T, d, ff, r);
+  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  const bool bf16 = act_dtype == SVDMLP_BF16;
+  hipStream_t st = (hipStream_t)stream;
+  void* h = static_cast<char*>(workspace) + L.norm;
+  if ((rc = check(launch_rmsnorm(x, norm_w, h, T, d, eps, bf16, st), "RMSNorm"))) return rc;
+  if ((rc = svdmlp_svd_mlp(h, ug, vg, uu, vu, ud, vd, scales, y, T, d, ff, r_gu, r_d, act_dtype, w_dtype, flags,
+                           workspace, ws_bytes, stream)))
+    return rc;
+  return check(launch_residual_add(x, y, T * d, bf16, st), "residual add");
+}
 
 int svdmlp_profile_enable(int enable) {
   std::lock_guard<std::mutex> g(g_prof.mu);

@@ -52,6 +52,10 @@ hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batc
 hipError_t launch_decode(const DecodeDesc& d, const DecodeParams& p, int blocks, hipStream_t st,
                          const char** why);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
+// MLP block prologue / epilogue: y = act(gain * rmsnorm(x)), y = act(x + y).
+hipError_t launch_rmsnorm(const void* x, const float* gain, void* y, int64_t T, int64_t d, float eps, bool bf16,
+                          hipStream_t st);
+hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hipStream_t st);
 // Persistent decode layer (T <= 64): token tiles of 16 rows (1, 2 or 4),
 // grid = CU count when the kernel fits one block per CU, else 0.
 int decode_layer_mt(int T);

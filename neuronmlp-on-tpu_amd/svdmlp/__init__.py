@@ -10,6 +10,7 @@ Host package over libsvdmlp.so (hand-written HIP kernels for gfx950):
 * :mod:`svdmlp.config`  -- model shapes, ranks and block parameters.
 * :mod:`svdmlp.inputs`  -- seeded synthetic inputs of the benchmark configs.
 * :mod:`svdmlp.fp8`     -- fp8 e4m3fn per-channel factor quantization.
+* :mod:`svdmlp.stack`   -- the N-layer MLP stack (RMSNorm, MLP, residual).
 """
 
 from ._lib import SvdMlpError, load, version, workspace_bytes  # noqa: F401
@@ -20,6 +21,7 @@ from .ops import (  # noqa: F401
     low_rank_dim,
     silu,
     svd_mlp,
+    svd_mlp_block,
     svd_mlp_workspace,
 )
 

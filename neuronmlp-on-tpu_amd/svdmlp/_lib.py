@@ -36,6 +36,7 @@ EXPORTED = (
     "svdmlp_gate_up",
     "svdmlp_xuv",
     "svdmlp_svd_mlp",
+    "svdmlp_svd_mlp_block",
     "svdmlp_profile_enable",
     "svdmlp_profile_read",
     "svdmlp_stage_name",
@@ -72,6 +73,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.svdmlp_xuv.argtypes = [_vp] * 3 + [_vp] * 2 + [_vp] + [_i64] * 4 + [_i32, _i32, _u32, _vp, _sz, _vp]
     lib.svdmlp_svd_mlp.restype = ctypes.c_int
     lib.svdmlp_svd_mlp.argtypes = [_vp] * 7 + [_vp, _vp] + [_i64] * 5 + [_i32, _i32, _u32, _vp, _sz, _vp]
+    lib.svdmlp_svd_mlp_block.restype = ctypes.c_int
+    lib.svdmlp_svd_mlp_block.argtypes = ([_vp, _vp, ctypes.c_float] + [_vp] * 6 + [_vp, _vp] + [_i64] * 5
+                                         + [_i32, _i32, _u32, _vp, _sz, _vp])
     lib.svdmlp_profile_enable.restype = ctypes.c_int
     lib.svdmlp_profile_enable.argtypes = [ctypes.c_int]
     lib.svdmlp_profile_read.restype = ctypes.c_int

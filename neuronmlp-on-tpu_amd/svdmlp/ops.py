@@ -223,12 +223,8 @@ def fused_xuv(x, u, v, *, x_transposed: bool = False) -> torch.Tensor:
     return out
 
 
-def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
-            out: torch.Tensor | None = None) -> torch.Tensor:
-    """Full SVD SwiGLU block, fused_xuv(fused_gate_up(x)) with h rounded to
-    x.dtype in between (kernels/reference.py:85-93).  Gate/up rank and down
-    rank may differ.  ``workspace``/``out`` may be supplied to avoid
-    per-call allocation (see :func:`svd_mlp_workspace`)."""
+def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out):
+    """Validation and argument marshalling shared by svd_mlp and svd_mlp_block."""
     validate_arrays(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
     T, d = _shape(x)
     if u_gate.shape[0] != d or v_gate.shape[0] != u_gate.shape[1]:
@@ -240,7 +236,6 @@ def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.T
         raise ValueError("X, U, V contraction dimensions do not match")
     r_d = int(u_down.shape[1])
     dev = _check_device(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
-    lib = _lib.load()
     x = _activation(x)
     fs = [_Factor(f) for f in (u_gate, v_gate, u_up, v_up, u_down, v_down)]
     us, vs = (fs[0], fs[2], fs[4]), (fs[1], fs[3], fs[5])
@@ -257,11 +252,51 @@ def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.T
         raise ValueError("out must be a contiguous (T, d) tensor of x.dtype on x.device")
     if workspace is None:
         workspace = svd_mlp_workspace(x, r=max(r_gu, r_d), ff=ff, w_code=w_code)
+    dims = (T, d, ff, r_gu, r_d)
+    return x, fs, flags, w_code, scale_arr, out, workspace, dims, dev
+
+
+def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Full SVD SwiGLU block, fused_xuv(fused_gate_up(x)) with h rounded to
+    x.dtype in between (kernels/reference.py:85-93).  Gate/up rank and down
+    rank may differ.  ``workspace``/``out`` may be supplied to avoid
+    per-call allocation (see :func:`svd_mlp_workspace`)."""
+    lib = _lib.load()
+    x, fs, flags, w_code, scale_arr, out, workspace, dims, dev = _prepare_layer(
+        x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
     with torch.cuda.device(dev):
         _lib.check(lib.svdmlp_svd_mlp(
             x.data_ptr(), *(f.ptr for f in fs),
             ctypes.addressof(scale_arr) if scale_arr is not None else None, out.data_ptr(),
-            T, d, ff, r_gu, r_d, _ACT_CODES[x.dtype], w_code, flags,
+            *dims, _ACT_CODES[x.dtype], w_code, flags,
+            workspace.data_ptr(), workspace.numel(), _stream(dev)))
+    return out
+
+
+def svd_mlp_block(x, norm_weight, u_gate, v_gate, u_up, v_up, u_down, v_down, *, eps: float = 1e-5,
+                  workspace: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One MLP block of the model, x + svd_mlp(RMSNorm(x) * norm_weight):
+    LlamaRMSNorm in fp32 (models/modeling_llama.py:253-262) and the residual
+    add of bench/e2e_block.py:268-278, both rounded to x.dtype.
+    ``norm_weight`` is the (d,) gain (any float dtype; used in fp32)."""
+    lib = _lib.load()
+    x, fs, flags, w_code, scale_arr, out, workspace, dims, dev = _prepare_layer(
+        x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
+    if out.data_ptr() == x.data_ptr():
+        raise ValueError("out must not alias x")
+    d = dims[1]
+    if norm_weight.dim() != 1 or norm_weight.shape[0] != d or norm_weight.device != dev:
+        raise ValueError(f"norm_weight must be a ({d},) tensor on x.device")
+    gain = norm_weight.to(torch.float32).contiguous()
+    eps = float(eps)
+    if not eps > 0:
+        raise ValueError(f"eps must be positive, got {eps}")
+    with torch.cuda.device(dev):
+        _lib.check(lib.svdmlp_svd_mlp_block(
+            x.data_ptr(), gain.data_ptr(), eps, *(f.ptr for f in fs),
+            ctypes.addressof(scale_arr) if scale_arr is not None else None, out.data_ptr(),
+            *dims, _ACT_CODES[x.dtype], w_code, flags,
             workspace.data_ptr(), workspace.numel(), _stream(dev)))
     return out
 

@@ -275,3 +275,42 @@ def test_fp8_factors(gpu, T):
     err = _rel(got, O.svd_mlp_ref(xb, *deq, dtype="bfloat16"))
     print(f"fp8 T={T} rel_l2={err:.3e}")
     assert err < FP8_TOL
+
+
+# ---------------------------------------------------------------------------
+# BASELINE config 4 (scaled): RMSNorm + MLP + residual blocks, non-uniform ranks
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T", [48, 300])
+def test_mlp_block(gpu, T):
+    """x + svd_mlp(RMSNorm(x) * gain) against the oracle's block
+    (decode-layer path at T=48, large-tile path at T=300)."""
+    shape = inputs.LayerShape(1024, 2048, 512, 384)
+    x, f = inputs.make_layer(shape, T=T, seed=41 + T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    gain = np.random.default_rng(T).uniform(0.9, 1.1, size=shape.d).astype(np.float32)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    y = _np(ops.svd_mlp_block(t[0], torch.from_numpy(gain).to(gpu), *t[1:], eps=1e-5))
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    # the residual dominates y: compare the MLP part as well
+    assert _rel(y, ref) < BF16_TOL
+    assert _rel(y - xb, ref - xb) < BF16_TOL
+
+
+def test_mlp_stack_nonuniform_ranks(gpu):
+    """Three blocks with independently drawn gate/up/down ranks (gate and up
+    zero-padded to a common rank) against the oracle, layer after layer."""
+    from svdmlp import stack
+
+    d, ff, T = 1024, 2048, 96
+    layers = stack.make_stack(3, d, ff, seed=5, device=gpu, choices=(256, 384, 512))
+    assert len({l.ranks for l in layers}) > 1
+    x = torch.from_numpy(_x(T, d, 17)).to(gpu).to(torch.bfloat16)
+    y = _np(stack.run_stack(x, layers, eps=1e-5))
+    ref = x.float().cpu().numpy()
+    for l in layers:
+        f = [a.float().cpu().numpy() for a in l.factors]
+        ref = O.mlp_block_ref(ref, l.gain.cpu().numpy(), f, eps=1e-5, dtype="bfloat16")
+    x0 = x.float().cpu().numpy()
+    assert _rel(y, ref) < BF16_TOL
+    assert _rel(y - x0, ref - x0) < BF16_TOL

@@ -174,3 +174,49 @@ def test_quantizer_matches_oracle_codec():
     q_ref, s_ref = O.quantize_per_channel(w, axis=0)
     np.testing.assert_allclose(q.scale.numpy(), s_ref, rtol=1e-6)
     np.testing.assert_array_equal(q.data.view(torch.uint8).numpy(), q_ref)
+
+
+# ---------------------------------------------------------------------------
+# MLP stack helpers
+# ---------------------------------------------------------------------------
+
+def test_stack_rank_draw_is_seeded_and_in_choices():
+    from svdmlp import stack
+
+    a = stack.draw_ranks(32, seed=7)
+    assert a == stack.draw_ranks(32, seed=7)
+    assert a != stack.draw_ranks(32, seed=8)
+    assert all(r in stack.RANK_CHOICES for row in a for r in row)
+    # gate, up and down are drawn independently: some layer has unequal ranks
+    assert any(len(set(row)) > 1 for row in a)
+
+
+def test_stack_rank_padding_is_exact():
+    """Zero-padding U columns / V rows leaves x.U.V unchanged (checked with
+    the oracle's float64-free fp32 math on CPU tensors)."""
+    import torch
+
+    from svdmlp import stack
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 16, generator=g)
+    u, v = torch.randn(16, 6, generator=g), torch.randn(6, 12, generator=g)
+    up, vp = stack.pad_rank(u, v, 10)
+    assert up.shape == (16, 10) and vp.shape == (10, 12)
+    assert torch.equal(up[:, 6:], torch.zeros(16, 4)) and torch.equal(vp[6:], torch.zeros(4, 12))
+    np.testing.assert_allclose(O.fused_xuv_ref(x.numpy(), up.numpy(), vp.numpy()),
+                               O.fused_xuv_ref(x.numpy(), u.numpy(), v.numpy()), rtol=1e-6, atol=1e-6)
+
+
+def test_stack_flops_uses_drawn_ranks():
+    from svdmlp import stack
+
+    class L:
+        def __init__(self, ranks):
+            self.ranks = ranks
+
+    layers = [L((2048, 3072, 2560)), L((2816, 2816, 2816))]
+    T, d, ff = 4096, 4096, 14336
+    want = sum(2 * T * ((rg + ru) * (d + ff) + rd * (ff + d)) for rg, ru, rd in (l.ranks for l in layers))
+    assert stack.stack_flops(T, d, ff, layers) == want
+    assert stack.stack_flops(T, d, ff, layers[1:]) == O.layer_flops(T, d, ff, 2816)
