@@ -379,8 +379,11 @@ const Tune& tune() {
 
 // The large-tile kernel takes bf16 operands below 2 GB each (32-bit buffer
 // offsets) and contraction lengths that are whole 32-k stages.
+int wbytes(const Common& c) { return c.wt == SVDMLP_FP8_E4M3 ? 1 : 2; }
+
 bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes, std::initializer_list<int64_t> ks) {
-  if (c.f32 || c.wt != SVDMLP_BF16 || !vec || !tune().big) return false;
+  if (c.f32 || !vec || !tune().big) return false;
+  if (c.wt != SVDMLP_BF16 && c.wt != SVDMLP_FP8_E4M3) return false;
   for (int64_t b : bytes)
     if (b >= ((int64_t)1 << 31)) return false;
   for (int64_t k : ks)
@@ -391,8 +394,12 @@ bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes, std
 int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
-             bool out_f32 = false, int64_t out_sstride = 0) {
+             bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr) {
   BigParams p{};
+  const bool fp8 = c.wt == SVDMLP_FP8_E4M3;
+  if (fp8 && (!s0 || b_kc)) return fail("fp8 large-tile GEMM needs natural-layout weights and scales");
+  p.scale[0] = s0;
+  p.scale[1] = s1 ? s1 : s0;
   p.a[0] = a0;
   p.a[1] = a1 ? a1 : a0;
   p.b[0] = b0;
@@ -413,7 +420,7 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   p.ntiles = (N + 32 * fn - 1) / (32 * fn);
   p.k_split = k_split;
   const int splits = (K + k_split - 1) / k_split;
-  const BigDesc d{fn, b_kc, epi, out_f32};
+  const BigDesc d{fn, b_kc, epi, out_f32, fp8};
   const char* why = nullptr;
   StageScope ss(stage, c.st);
   return check(launch_big(d, p, splits, batch, c.st, &why), "large-tile GEMM", why);
@@ -465,20 +472,22 @@ int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
 // too few output tiles for the chip, K is split: each split writes an fp32
 // slice (plain stores) and one pass sums the slices in order into bf16.
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
-           int T, int K, int r, int batch, char* ws, const Ws& L) {
+           int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr) {
   const int fn = tune().s1;
   const int ks = plan_ksplit(T, K, r, fn, batch);
   const int splits = (K + ks - 1) / ks;
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
-  const int64_t u_bytes = (int64_t)K * r * 2;
+  const int64_t u_bytes = (int64_t)K * r * wbytes(c);
   const void* u1 = batch > 1 ? u[1] : u[0];
+  const float* s0 = su ? su[0] : nullptr;
+  const float* s1 = su && batch > 1 ? su[1] : s0;
   if (splits == 1)
     return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, u_lin ? K : r, u_bytes, u_lin, T, r, K, batch, fn,
-                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr);
+                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1);
   float* part = reinterpret_cast<float*>(ws + L.part);
   const int64_t slice = (int64_t)batch * T * r;
   int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, u_lin ? K : r, u_bytes, u_lin, T, r, K, batch, fn,
-                    BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice);
+                    BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice, s0, s1);
   if (rc) return rc;
   StageScope fin(ST_FINALIZE, c.st);
   return check(launch_reduce_bf16(part, splits, slice, xu, slice, c.st), "split-K reduce");
@@ -487,31 +496,32 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
 // out = SiLU(XUg . Vg) * (XUu . Vu): a g pass (bf16 g to the workspace) and a
 // u pass whose epilogue applies SiLU(g) * u.
 int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, const void* vg, const void* vu,
-               bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out) {
+               bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, const float* s_vg = nullptr,
+               const float* s_vu = nullptr) {
   int fn = tune().s2fn;
   if (fn == 0) fn = (ff % 224 == 0) ? 7 : 8;
-  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * ff * 2;
+  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * ff * wbytes(c);
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r,
-                    1, fn, BEPI_STORE, r, gbuf, ff, 0, nullptr);
+                    1, fn, BEPI_STORE, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
   if (rc) return rc;
   return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r, 1,
-                  fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf);
+                  fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf, false, 0, s_vu);
 }
 
 // y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
 int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T, int r, int dout, char* ws,
-          const Ws& L, void* y) {
+          const Ws& L, void* y, const float* sv = nullptr) {
   const int fn = tune().s4 > 0 ? tune().s4 : 8;
-  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * dout * 2;
+  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * dout * wbytes(c);
   const int ks = tune().s4 > 0 && tune().s4 != 8 ? r : plan_ksplit(T, r, dout, fn, 1);
   const int splits = (r + ks - 1) / ks;
   if (splits == 1)
     return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, v_lin ? r : dout, v_bytes, v_lin, T, dout, r, 1,
-                    fn, BEPI_STORE, r, y, dout, 0, nullptr);
+                    fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv);
   float* part = reinterpret_cast<float*>(ws + L.part);
   const int64_t slice = (int64_t)T * dout;
   int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, v_lin ? r : dout, v_bytes, v_lin, T, dout, r,
-                    1, fn, BEPI_STORE, ks, part, dout, 0, nullptr, true, slice);
+                    1, fn, BEPI_STORE, ks, part, dout, 0, nullptr, true, slice, sv);
   if (rc) return rc;
   StageScope fin(ST_FINALIZE, c.st);
   return check(launch_reduce_bf16(part, splits, slice, static_cast<uint16_t*>(y), slice, c.st), "split-K reduce");
@@ -762,10 +772,11 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
 
   if (!out_t && big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2}, {d, r})) {
     const void* us[2] = {ug, uu};
-    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L))) return rc;
+    const float* sus[2] = {s_ug, s_uu};
+    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L, fp8 ? sus : nullptr))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.h);
-    return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h);
+    return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h, fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr);
   }
 
   const Operand ax{x, nullptr, d};
@@ -831,8 +842,11 @@ int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, co
 
   if (!x_t && big_ok(c, vec, {T * din * 2, din * r * 2, r * dout * 2, T * dout * 2}, {din, r})) {
     const void* us[1] = {u};
-    if ((rc = big_xu(c, ST_D_XU, x, din, T * din * 2, us, u_lin, T, din, r, 1, ws, L))) return rc;
-    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), v, v_lin, T, r, dout, ws, L, y);
+    const float* sus[1] = {s_u};
+    if ((rc = big_xu(c, ST_D_XU, x, din, T * din * 2, us, u_lin, T, din, r, 1, ws, L, fp8 ? sus : nullptr)))
+      return rc;
+    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), v, v_lin, T, r, dout, ws, L, y,
+                 fp8 ? s_v : nullptr);
   }
 
   const Operand ax{x, nullptr, x_t ? T : din};
@@ -933,14 +947,16 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
   // Prefill: h stays in the workspace between the two halves.
   if (big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2, ff * r * 2}, {d, r_gu, ff, r_d})) {
     const void* us[2] = {ug, uu};
-    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L))) return rc;
+    const float* sus[2] = {S[0], S[2]};
+    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L, sus))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
     uint16_t* gbuf = hbuf + T * ff;
-    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf))) return rc;
+    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf, S[1], S[3]))) return rc;
     const void* ud1[1] = {ud};
-    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L))) return rc;
-    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y);
+    const float* sud[1] = {S[4]};
+    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud))) return rc;
+    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5]);
   }
 
   const Operand ax{x, nullptr, d};

@@ -32,6 +32,7 @@ struct BigDesc {
   bool b_kc;     // Linear-layout B
   int epi;       // BigEpi
   bool out_f32;  // fp32 output (split-K partial slices)
+  bool fp8 = false;  // fp8 e4m3fn B (natural layout) with per-column scales
 };
 
 struct BigParams;

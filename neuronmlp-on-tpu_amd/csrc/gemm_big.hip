@@ -6,9 +6,9 @@ namespace svdmlp {
 
 namespace {
 
-template <int FN, bool BK, int EPI, bool F32 = false>
+template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false>
 hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
-  using C = BigCfg<FN, BK, EPI, F32>;
+  using C = BigCfg<FN, BK, EPI, F32, F8>;
   dim3 grid(p.mtiles * p.ntiles, splits, batch);
   hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(kBigThreads), 0, st, p);
   return hipGetLastError();
@@ -16,6 +16,7 @@ hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
 
 template <int FN, int EPI, bool F32 = false>
 hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st) {
+  if (d.fp8) return go<FN, false, EPI, F32, true>(p, splits, batch, st);  // fp8 B: natural layout only
   return d.b_kc ? go<FN, true, EPI, F32>(p, splits, batch, st) : go<FN, false, EPI, F32>(p, splits, batch, st);
 }
 

@@ -99,8 +99,9 @@ __device__ __forceinline__ void dma16_dev(i32x4 rsrc, uint32_t voff, uint32_t so
 
 template <int N>
 __device__ __forceinline__ void wait_dma() {
-  static_assert(N == 0 || N == 4 || N == 8, "vmcnt literal");
+  static_assert(N == 0 || N == 4 || N == 6 || N == 8, "vmcnt literal");
   if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
   if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
   if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
@@ -121,6 +122,27 @@ __device__ __forceinline__ u32x2 lds_read_tr(lds_cptr p) {
 
 __device__ __forceinline__ u32x4 lds_read_b128(lds_cptr p) { return *reinterpret_cast<const SVDMLP_LDS u32x4*>(p); }
 
+typedef int i32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
+// ds_read_b64_tr_b8: in each 16-lane group, lane i receives byte i % 8 of the
+// 8-byte pieces addressed by lanes 2j + i/8 (j = 0..7).  Pointing lane s at
+// k-row k + s/2, bytes n + 8*(s % 2) gives lane i column n + i, rows
+// k..k+7: the fp8 MFMA operand, 8 consecutive k of one column.
+__device__ __forceinline__ u32x2 lds_read_tr8(lds_cptr p) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((SVDMLP_LDS i32x2v*)(p)));
+}
+
+// 8 fp8 e4m3fn values (k order, bytes of v.x then v.y) widened exactly to 8
+// bf16 packed in pairs (every e4m3 value, subnormals and NaN included, is a
+// bf16 value; the hardware conversion with scale 1 is exact).
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 v) {
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, true))};
+}
+
 // 32-byte unit swizzle of a natural-layout B row k.
 __device__ __forceinline__ int bnat_swz(int k) { return k & 3; }
 
@@ -136,6 +158,7 @@ struct BigParams {
   int64_t out_bstride;   // elements between batch outputs
   int64_t out_sstride;   // elements between split-K partial slices (fp32 output)
   const uint16_t* gmem;  // BEPI_SWIGLU_MEM: bf16 gate values, same layout as out
+  const float* scale[2]; // fp8 B: one fp32 scale per output column, per batch entry
   int M, N, K;
   int mtiles, ntiles;
   int k_split;
@@ -143,21 +166,25 @@ struct BigParams {
 
 constexpr int kBigThreads = 512;
 
-template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_>
+template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false>
 struct BigCfg {
   static constexpr int FM = 4, FN = FN_;  // per wave: 64 x 16*FN
   static constexpr bool B_KC = B_KC_;
   static constexpr int EPI = EPI_;
   static constexpr bool OUT_F32 = OUT_F32_;
+  // fp8 e4m3fn B in natural layout: 1-byte elements staged as they lie in
+  // HBM, widened to bf16 after the transposing LDS read.
+  static constexpr bool FP8_B = FP8_B_;
   static constexpr int BM = 256, BN = 32 * FN, BK = 32;  // BK per stage
   static constexpr int STAGES = 4;
   static constexpr int A_BYTES = BM * 64;                      // 16 KB
-  static constexpr int B_PITCH = 512;
-  static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (Linear: rows >= BN read zeros)
+  static constexpr int B_PITCH = FP8_B ? 256 : 512;
+  static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (fp8: 8 KB; Linear: rows >= BN read zeros)
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_UNITS = A_BYTES / 1024 / 8;  // 2 DMA instructions per wave
-  static constexpr int B_UNITS = B_BYTES / 1024 / 8;  // 2
-  static_assert(A_UNITS == 2 && B_UNITS == 2, "four DMA instructions per wave and stage");
+  static constexpr int B_UNITS = B_BYTES / 1024 / 8;  // 2 (fp8: 1)
+  static_assert(A_UNITS == 2 && B_UNITS == (FP8_B ? 1 : 2), "DMA instructions per wave and stage");
+  static_assert(!(FP8_B && B_KC), "fp8 B is read in natural layout only");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
   static_assert(B_KC ? BN <= 256 : true, "Linear-layout B tile holds at most 256 rows");
   static_assert(STAGES * STAGE <= 160 * 1024, "LDS budget");
@@ -230,6 +257,13 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
       const int row = row0 + 128 * i;
       b_voff[i] = (row < BN && n0 + row < p.N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
     }
+  } else if constexpr (C::FP8_B) {
+    // fp8 natural: the wave's one instruction fills k-rows 4*wave + lane/16
+    // (256 bytes each); slot lane%16 holds logical 16-byte chunk
+    // (lane%16) ^ (row & 7), i.e. columns 16 * that chunk .. +15.
+    const int kk = 4 * wave + (lane >> 4);
+    const int col = 16 * ((lane & 15) ^ (kk & 7));
+    b_voff[0] = (col < BN && n0 + col < p.N) ? (uint32_t)kk * (uint32_t)p.ldb + (uint32_t)(n0 + col) : kOOB;
   } else {
     const int kk = 2 * wave + (lane >> 5);
     const int q = lane & 31;
@@ -247,7 +281,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
       dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u, lbase + s * C::A_BYTES + (wave + 8 * d) * 1024);
     } else {
       const int i = d - C::A_UNITS;
-      const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (uint32_t)k0 * ldb2;
+      const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)p.ldb : (uint32_t)k0 * ldb2);
       dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + 8 * i) * 1024);
     }
   };
@@ -278,6 +312,18 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
       b_rd[t] = l0 + B_REGION + k_lo * C::B_PITCH + (((u & ~3) | ((u & 3) ^ bnat_swz(k_lo))) << 5) + ((lr & 3) << 3);
     }
   }
+  // fp8 B: lane s = lr of group lg points at k-row 8*lg + lr/2, bytes
+  // 8*(lr & 1) of 16-byte chunk c = wn0/16 + j (fragment j's 16 columns),
+  // stored at chunk (c & ~7) | ((c & 7) ^ (row & 7)); one base per fragment.
+  lds_cptr b8[C::FP8_B ? FN : 1];
+  if constexpr (C::FP8_B) {
+    const int row = 8 * lg + (lr >> 1);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int cc = (wn0 >> 4) + j;
+      b8[j] = l0 + B_REGION + row * C::B_PITCH + (((cc & ~7) | ((cc & 7) ^ (row & 7))) << 4) + ((lr & 1) << 3);
+    }
+  }
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -297,6 +343,8 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   auto read_one = [&](int s, int r, Frags& f) {
     if (r < FM) {
       f.a[r] = lds_read_b128(a_rd + s * C::A_BYTES + 1024 * r);
+    } else if constexpr (C::FP8_B) {
+      f.b[r - FM] = lds_read_tr8(b8[r - FM] + s * C::B_BYTES);
     } else if constexpr (C::B_KC) {
       const u32x4 v = lds_read_b128(b_rd[0] + s * C::B_BYTES + 1024 * (r - FM));
       f.b[2 * (r - FM)] = u32x2{v.x, v.y};
@@ -306,11 +354,19 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
       f.b[2 * j + hi] = lds_read_tr(b_rd[j & 3] + 128 * (j >> 2) + s * C::B_BYTES + hi * 4 * C::B_PITCH);
     }
   };
-  constexpr int NREAD = FM + (C::B_KC ? FN : 2 * FN);
+  constexpr int NREAD = FM + ((C::B_KC || C::FP8_B) ? FN : 2 * FN);
+  // fp8 B: fragment j widened to bf16 once per step (fbw[j]), interleaved
+  // with the first FN MFMAs, which are the first to use them.
+  u32x4 fbw[C::FP8_B ? FN : 1];
   auto mfma_one = [&](int m, const Frags& f) {
     const int i = m / FN, j = m % FN;
-    const u32x2 lo = f.b[2 * j], hi = f.b[2 * j + 1];
-    acc[i][j] = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, f.a[i], acc[i][j], __bf16{});
+    if constexpr (C::FP8_B) {
+      if (m < FN) fbw[j] = fp8x8_to_bf16x8(f.b[j]);
+      acc[i][j] = mfma_chunk(fbw[j], f.a[i], acc[i][j], __bf16{});
+    } else {
+      const u32x2 lo = f.b[2 * j], hi = f.b[2 * j + 1];
+      acc[i][j] = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, f.a[i], acc[i][j], __bf16{});
+    }
   };
 
   // Stage kt sits in slot kt % 4.  Step kt runs the MFMAs of stage kt
@@ -326,7 +382,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   // sched_barriers pin this instruction order.
   Frags f0, f1;
   constexpr int NMFMA = FM * FN;
-  static_assert(NREAD <= NMFMA && NDMA == 4, "one fragment read per MFMA slot");
+  static_assert(NREAD <= NMFMA && (NDMA == 4 || NDMA == 3), "one fragment read per MFMA slot");
   auto step = [&](int kt, int s, const Frags& cur, Frags& nxt) {
 #pragma unroll
     for (int m = 0; m < NMFMA; ++m) {
@@ -337,7 +393,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
       mfma_one(m, cur);
       __builtin_amdgcn_sched_barrier(0);
     }
-    wait_dma<8>();
+    wait_dma<2 * NDMA>();
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -347,7 +403,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int d = 0; d < NDMA; ++d) dma_one(s, s, d);
-    wait_dma<8>();  // stages 0 and 1 landed
+    wait_dma<2 * NDMA>();  // stages 0 and 1 landed
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < NREAD; ++r) read_one(0, r, f0);
@@ -373,7 +429,8 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn0 + 16 * j + 4 * lg;
       if (n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
-      const f32x4 v = acc[i][j];
+      f32x4 v = acc[i][j];
+      if constexpr (C::FP8_B) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
       const int64_t o = (int64_t)m * p.ldo + n;
       if constexpr (C::EPI == BEPI_ATOMIC) {
         float* op = reinterpret_cast<float*>(outp) + o;

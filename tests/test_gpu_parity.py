@@ -263,18 +263,44 @@ def test_replay_is_stable(gpu, layer8b):
 # BASELINE config 5 (scaled down): fp8 e4m3 factors, bf16 activations
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("T", [8, 256])
-def test_fp8_factors(gpu, T):
-    shape = inputs.LayerShape(1024, 2048, 512)
-    x, f = inputs.make_layer(shape, T=T, seed=9)
+def _fp8_layer(shape, T, seed, gpu):
+    x, f = inputs.make_layer(shape, T=T, seed=seed)
     xb = inputs.as_float32(x, torch.bfloat16)
     q = [fp8.quantize_per_channel(torch.from_numpy(a)) for a in f]
     deq = [O.e4m3_decode(qq.data.view(torch.uint8).numpy()) * qq.scale.numpy() for qq in q]
     qg = [ops.QuantizedFactor(qq.data.to(gpu), qq.scale.to(gpu)) for qq in q]
+    return xb, deq, qg
+
+
+# T=8: decode path; T=256: large-tile path with split-K; T=300: ragged M.
+# The second shape has N edges that cut the 224/256-wide tiles and d not a
+# multiple of the tile width (large-tile path, partial B tiles).
+@pytest.mark.parametrize("T,shape", [
+    (8, inputs.LayerShape(1024, 2048, 512)),
+    (256, inputs.LayerShape(1024, 2048, 512)),
+    (300, inputs.LayerShape(1024, 2048, 512)),
+    (640, inputs.LayerShape(1056, 1120, 416, 288)),
+])
+def test_fp8_factors(gpu, T, shape):
+    xb, deq, qg = _fp8_layer(shape, T, 9 + T, gpu)
     got = _np(ops.svd_mlp(_to(xb, torch.bfloat16, gpu), *qg))
     err = _rel(got, O.svd_mlp_ref(xb, *deq, dtype="bfloat16"))
-    print(f"fp8 T={T} rel_l2={err:.3e}")
+    print(f"fp8 T={T} {shape} rel_l2={err:.3e}")
     assert err < FP8_TOL
+
+
+@pytest.mark.parametrize("T", [16, 512])
+def test_fp8_gate_up_and_xuv_entries(gpu, T):
+    """The two halves as separate entry points with fp8 factors."""
+    shape = inputs.LayerShape(1024, 2048, 512)
+    xb, deq, qg = _fp8_layer(shape, T, 70 + T, gpu)
+    xt = _to(xb, torch.bfloat16, gpu)
+    h = ops.fused_gate_up(xt, *qg[:4])
+    ref_h = O.fused_gate_up_ref(xb, *deq[:4], dtype="bfloat16")
+    assert _rel(_np(h), ref_h) < FP8_TOL
+    hb = inputs.as_float32(_np(h), torch.bfloat16)
+    y = ops.fused_xuv(_to(hb, torch.bfloat16, gpu), *qg[4:])
+    assert _rel(_np(y), O.fused_xuv_ref(hb, *deq[4:], dtype="bfloat16")) < FP8_TOL
 
 
 # ---------------------------------------------------------------------------
