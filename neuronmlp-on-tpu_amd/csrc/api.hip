@@ -23,6 +23,7 @@
 #include <cstdlib>
 
 #include "dispatch.hpp"
+#include "decode_gemv.hpp"
 #include "decode_layer.hpp"
 #include "gemm_big.hpp"
 #include "svdmlp.h"
@@ -70,12 +71,13 @@ enum Stage : int {
   ST_FINALIZE,
   ST_GU_XUV_G,
   ST_DEC_LAYER,
+  ST_DEC_GEMV,
   ST_COUNT
 };
 const char* const kStageNames[ST_COUNT] = {
     "zero_fill",        "gate_up_xu",       "gate_up_xuv_swiglu", "down_xu",           "down_xuv",
     "decode_gate_up_xu", "decode_gate_up_xuv", "decode_down_xu",   "decode_down_xuv", "finalize",
-    "gate_up_xuv_g",    "decode_layer"};
+    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer"};
 
 struct Profiler {
   std::mutex mu;
@@ -345,6 +347,8 @@ struct Tune {
   bool big = true;    // large-tile path enabled
   bool dlayer = true; // persistent decode layer enabled
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
+  int gvmax = 4;       // highest T for the streaming-GEMV decode layer (0: off)
+  int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
 };
 
 const Tune& tune() {
@@ -369,6 +373,8 @@ const Tune& tune() {
         if (k == "big") r.big = v != 0;
         if (k == "dlayer") r.dlayer = v != 0;
         if (k == "dlmin") r.dlmin = v;
+        if (k == "gvmax") r.gvmax = v;
+        if (k == "gvrw") r.gvrw = v;
       }
       pos = end + 1;
     }
@@ -633,6 +639,56 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   return check(launch_decode_layer(p, mt, grid, c.st, &why), "decode layer", why);
 }
 
+// Streaming-GEMV layer (1 <= T <= min(kGvMaxT, gvmax)): bf16, natural
+// layout, every K a multiple of the 16-row group, each factor below 2 GB and
+// each block's activation rows within the kernel's LDS slice.
+bool gemv_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
+                   bool vec) {
+  const int rw = tune().gvrw == 1 ? 1 : 2;
+  if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T < 1 || T > std::min(kGvMaxT, tune().gvmax)) return false;
+  if (d % 16 || ff % 16 || r_gu % 16 || r_d % 16) return false;
+  const int64_t lim = (int64_t)1 << 31;
+  for (int64_t bytes : {d * r_gu * 2, r_gu * ff * 2, ff * r_d * 2, r_d * d * 2})
+    if (bytes >= lim) return false;
+  const int grid = gemv_layer_grid(rw);
+  if (grid <= 0) return false;
+  const int64_t strip = 512 / rw, group = 8 * rw;
+  auto rows = [&](int64_t nm, int64_t K, int64_t N) {
+    const int64_t groups = nm * ((N + strip - 1) / strip) * (K / group);
+    return group * ((groups + grid - 1) / grid);
+  };
+  const int64_t most = std::max(std::max(rows(2, d, r_gu), rows(2, r_gu, ff)), std::max(rows(1, ff, r_d), rows(1, r_d, d)));
+  return most * T <= gemv_layer_a_floats();
+}
+
+int gemv_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+               const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
+               char* ws, const Ws& L) {
+  const int rw = tune().gvrw == 1 ? 1 : 2;
+  GvParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.ug = static_cast<const uint16_t*>(ug);
+  p.vg = static_cast<const uint16_t*>(vg);
+  p.uu = static_cast<const uint16_t*>(uu);
+  p.vu = static_cast<const uint16_t*>(vu);
+  p.ud = static_cast<const uint16_t*>(ud);
+  p.vd = static_cast<const uint16_t*>(vd);
+  p.y = static_cast<uint16_t*>(y);
+  p.xu32 = reinterpret_cast<float*>(ws + L.xu32);
+  p.xd32 = p.xu32 + 2 * T * r_gu;
+  p.gu32 = reinterpret_cast<float*>(ws + L.gu32);
+  p.y32 = reinterpret_cast<float*>(ws + L.y32);
+  p.sync = reinterpret_cast<uint64_t*>(ws + L.sync);
+  p.T = (int)T;
+  p.d = (int)d;
+  p.ff = (int)ff;
+  p.r_gu = (int)r_gu;
+  p.r_d = (int)r_d;
+  const char* why = nullptr;
+  StageScope ss(ST_DEC_GEMV, c.st);
+  return check(launch_gemv_layer(p, rw, gemv_layer_grid(rw), c.st, &why), "decode GEMV layer", why);
+}
+
 int validate_dims(int64_t T, int64_t a, int64_t b, int64_t r) {
   if (T <= 0 || a <= 0 || b <= 0 || r <= 0)
     return fail("dimensions must be positive, got T=%lld, %lld, %lld, r=%lld", (long long)T, (long long)a,
@@ -890,6 +946,8 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
   if (fp8)
     for (int i = 0; i < 6; ++i) S[i] = scales[i];
 
+  if (gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec))
+    return gemv_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L);
   if (decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec))
     return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L);
 

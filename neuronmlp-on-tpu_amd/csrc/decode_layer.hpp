@@ -75,7 +75,10 @@ constexpr int kDlLine = 16;
 constexpr int kDlRoot = kDlGroups * kDlLine;
 constexpr int kDlGen = kDlRoot + kDlLine;
 constexpr int kDlFlag = kDlGen + kDlLine;
-constexpr int kDlSyncBytes = (kDlFlag + kDlLine) * 8;
+// Block-done counter of the streaming-GEMV decode layer (monotone, like the
+// barrier counters: the last of every G arrivals finishes the launch).
+constexpr int kGvDone = kDlFlag + kDlLine;
+constexpr int kDlSyncBytes = (kGvDone + kDlLine) * 8;
 
 // Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
 // weight bytes per block barrier) and the ring holds NS stages, as far as

@@ -62,6 +62,12 @@ hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hip
 int decode_layer_mt(int T);
 int decode_layer_grid(int mt);
 hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why);
+// Streaming-GEMV decode layer (T <= 4): rows per wave load rw (1 or 2),
+// grid = CU count when the kernel fits one block per CU, else 0.
+struct GvParams;
+int gemv_layer_grid(int rw);
+int gemv_layer_a_floats();
+hipError_t launch_gemv_layer(const GvParams& p, int rw, int grid, hipStream_t st, const char** why);
 hipError_t launch_cvt_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t st);
 // out[i] = bf16(sum_s in[s * stride + i]) for s < slices.
 hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint16_t* out, int64_t n,

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 BF16_TOL = 1e-2
 FP8_TOL = 3e-2
-DECODE_LAYER_MIN_T = 4   # kDlMinT in csrc/api.hip
+GEMV_LAYER_MAX_T = 4   # kGvMaxT in csrc/decode_gemv.hpp
 
 
 def _to(a, dtype, dev):
@@ -163,7 +163,7 @@ def test_8b_prefill_T1024_row_subset(gpu, layer8b):
     assert err_h < BF16_TOL, err_h
 
 
-@pytest.mark.parametrize("T", [1, 8, 32, 64])
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 32, 64])
 def test_8b_decode(gpu, layer8b, T):
     shape, f, ft = layer8b
     x = _x(T, shape.d, 100 + T)
@@ -209,9 +209,10 @@ def _barrier_state(ws):
     (inputs.LayerShape(1024, 32768, 256), (5, 33)),                     # 512 column tiles: two units per block
 ])
 def test_decode_layer_workspace_reuse(gpu, shape, Ts):
-    """The persistent decode kernel (one cooperative launch, grid barriers
-    in the workspace's first 256 bytes) over one reused workspace: results
-    match the oracle, every call advances the barrier generation by its five
+    """The persistent decode kernels (the streaming-GEMV layer up to 4
+    tokens, the MFMA layer above; one launch each, grid barriers in the
+    workspace's first 4096 bytes) over one reused workspace: results match
+    the oracle, every call advances the shared barrier generation by its
     barriers and no barrier times out."""
     x, f = inputs.make_layer(shape, T=max(Ts), seed=31)
     xb, *fb = _rounded((x, *f), torch.bfloat16)
@@ -222,8 +223,26 @@ def test_decode_layer_workspace_reuse(gpu, shape, Ts):
         y = _np(ops.svd_mlp(t[0][:T].contiguous(), *t[1:], workspace=ws))
         err = _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16"))
         assert err < BF16_TOL, (T, err)
-        gen += 5 if T >= DECODE_LAYER_MIN_T else 0   # fewer tokens take the per-stage kernels
+        gen += 4 if T <= GEMV_LAYER_MAX_T else 5   # GEMV layer: 4 barriers, MFMA layer: 5
         assert _barrier_state(ws) == (gen, 0), T
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+def test_gemv_decode_layer_ragged_strips(gpu, T):
+    """Streaming-GEMV layer on a shape whose column counts cut its 256- and
+    512-column strips (400, 272, 1040, 2064) and whose row counts are only
+    multiples of 16: partial strips, ranges that start mid-strip, and block
+    ranges that cross from one factor into the other."""
+    shape = inputs.LayerShape(1040, 2064, 400, 272)
+    x, f = inputs.make_layer(shape, T=T, seed=60 + T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ws = ops.svd_mlp_workspace(t[0], r=shape.r, ff=shape.ff)
+    y = _np(ops.svd_mlp(*t, workspace=ws))
+    err = _rel(y, O.svd_mlp_ref(xb, *fb, dtype="bfloat16"))
+    print(f"gemv layer T={T} rel_l2={err:.3e}")
+    assert err < BF16_TOL
+    assert _barrier_state(ws) == (4, 0)
 
 
 def test_decode_and_prefill_paths_agree(gpu, layer8b):
