@@ -349,6 +349,7 @@ struct Tune {
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = 4;       // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
+  int nw = 8;          // waves per block of the fn-8 X.U and XU.V stages (8, or 4: faster in isolation, not in the layer)
 };
 
 const Tune& tune() {
@@ -375,6 +376,7 @@ const Tune& tune() {
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
+        if (k == "nw") r.nw = v;
       }
       pos = end + 1;
     }
@@ -426,7 +428,7 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   p.ntiles = (N + 32 * fn - 1) / (32 * fn);
   p.k_split = k_split;
   const int splits = (K + k_split - 1) / k_split;
-  const BigDesc d{fn, b_kc, epi, out_f32, fp8};
+  const BigDesc d{fn, b_kc, epi, out_f32, fp8, (fn == 8 && epi == BEPI_STORE && !b_kc && tune().nw == 4) ? 4 : 8};
   const char* why = nullptr;
   StageScope ss(stage, c.st);
   return check(launch_big(d, p, splits, batch, c.st, &why), "large-tile GEMM", why);

@@ -33,6 +33,7 @@ struct BigDesc {
   int epi;       // BigEpi
   bool out_f32;  // fp32 output (split-K partial slices)
   bool fp8 = false;  // fp8 e4m3fn B (natural layout) with per-column scales
+  int nw = 8;        // waves per block: 8, or 4 (natural-layout fn-8 STORE tiles)
 };
 
 struct BigParams;

@@ -6,16 +6,21 @@ namespace svdmlp {
 
 namespace {
 
-template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false>
+template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8>
 hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
-  using C = BigCfg<FN, BK, EPI, F32, F8>;
+  using C = BigCfg<FN, BK, EPI, F32, F8, NW>;
   dim3 grid(p.mtiles * p.ntiles, splits, batch);
-  hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(kBigThreads), 0, st, p);
+  hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(C::THREADS), 0, st, p);
   return hipGetLastError();
 }
 
 template <int FN, int EPI, bool F32 = false>
 hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st) {
+  if constexpr (FN == 8 && EPI == BEPI_STORE) {  // 4-wave instances: natural layout, STORE
+    if (d.nw == 4 && !d.b_kc)
+      return d.fp8 ? go<FN, false, EPI, F32, true, 4>(p, splits, batch, st)
+                   : go<FN, false, EPI, F32, false, 4>(p, splits, batch, st);
+  }
   if (d.fp8) return go<FN, false, EPI, F32, true>(p, splits, batch, st);  // fp8 B: natural layout only
   return d.b_kc ? go<FN, true, EPI, F32>(p, splits, batch, st) : go<FN, false, EPI, F32>(p, splits, batch, st);
 }

@@ -99,11 +99,8 @@ __device__ __forceinline__ void dma16_dev(i32x4 rsrc, uint32_t voff, uint32_t so
 
 template <int N>
 __device__ __forceinline__ void wait_dma() {
-  static_assert(N == 0 || N == 4 || N == 6 || N == 8, "vmcnt literal");
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // A-tile chunk swizzle for 64-byte rows.  A ds_read_b128 serves 8 lanes
@@ -164,11 +161,15 @@ struct BigParams {
   int k_split;
 };
 
-constexpr int kBigThreads = 512;
-
-template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false>
+template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8>
 struct BigCfg {
-  static constexpr int FM = 4, FN = FN_;  // per wave: 64 x 16*FN
+  // NW waves per block in a 2 (n) x NW/2 (m) arrangement: a wave's tile is
+  // (BM / (NW/2)) x 16*FN, i.e. 64 x 16*FN with 8 waves (two per SIMD) or
+  // 128 x 16*FN with 4 (one per SIMD, accumulators in AGPRs), which reads
+  // a third less from LDS per MFMA.
+  static constexpr int NW = NW_;
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int FM = 32 / NW, FN = FN_;  // per wave: 16*FM x 16*FN
   static constexpr bool B_KC = B_KC_;
   static constexpr int EPI = EPI_;
   static constexpr bool OUT_F32 = OUT_F32_;
@@ -181,9 +182,10 @@ struct BigCfg {
   static constexpr int B_PITCH = FP8_B ? 256 : 512;
   static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (fp8: 8 KB; Linear: rows >= BN read zeros)
   static constexpr int STAGE = A_BYTES + B_BYTES;
-  static constexpr int A_UNITS = A_BYTES / 1024 / 8;  // 2 DMA instructions per wave
-  static constexpr int B_UNITS = B_BYTES / 1024 / 8;  // 2 (fp8: 1)
-  static_assert(A_UNITS == 2 && B_UNITS == (FP8_B ? 1 : 2), "DMA instructions per wave and stage");
+  static constexpr int A_UNITS = A_BYTES / 1024 / NW;  // DMA instructions per wave: 2 (NW 4: 4)
+  static constexpr int B_UNITS = B_BYTES / 1024 / NW;  // 2 (fp8: 1); NW 4: 4 (fp8: 2)
+  static_assert(NW == 8 || NW == 4, "8 or 4 waves");
+  static_assert(A_UNITS * NW == 16 && B_UNITS * NW == (FP8_B ? 8 : 16), "DMA instructions per wave and stage");
   static_assert(!(FP8_B && B_KC), "fp8 B is read in natural layout only");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
   static_assert(B_KC ? BN <= 256 : true, "Linear-layout B tile holds at most 256 rows");
@@ -191,8 +193,8 @@ struct BigCfg {
 };
 
 template <class C>
-__global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
-  constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN, BK = C::BK;
+__global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
+  constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW;
   constexpr int NS = C::STAGES;
   // LDS: the A tiles of the 4 stages in the first 64 KB, the B tiles in the
   // next 64 KB, so that every fragment read of any stage is one base
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
-  const int wm0 = (wave >> 1) * (BM / 4);
+  const int wm0 = (wave >> 1) * (16 * FM);
   const int wn0 = (wave & 1) * (BN / 2);
 
   const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
@@ -234,7 +236,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   // matrix.  K and the split length are whole 32-k stages, so a stage lies
   // either below kend or wholly past it; stages past it (the pipeline's
   // run-out) use a descriptor with no records and fetch zeros.
-  // A: instruction i of this wave fills LDS rows 16*(wave + 8i) + lane/4;
+  // A: instruction i of this wave fills LDS rows 16*(wave + NW*i) + lane/4;
   // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row).
   const i32x4 r_none = make_rsrc_sgpr(p.a[zb], 0);
   const int a_row0 = 16 * wave + (lane >> 2);
@@ -242,10 +244,10 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   uint32_t a_voff[C::A_UNITS];
 #pragma unroll
   for (int i = 0; i < C::A_UNITS; ++i) {
-    const int row = m0 + a_row0 + 128 * i;
+    const int row = m0 + a_row0 + 16 * NW * i;
     a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
   }
-  // B natural: instruction i fills LDS k-row 2*(wave + 8i) + lane/32, slot
+  // B natural: instruction i fills LDS k-row 2*(wave + NW*i) + lane/32, slot
   // lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
   // B Linear: like A with rows n.
   uint32_t b_voff[C::B_UNITS];
@@ -254,23 +256,26 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
     const int kk = 8 * ((lane & 3) ^ a_swz(row0));
 #pragma unroll
     for (int i = 0; i < C::B_UNITS; ++i) {
-      const int row = row0 + 128 * i;
+      const int row = row0 + 16 * NW * i;
       b_voff[i] = (row < BN && n0 + row < p.N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
     }
   } else if constexpr (C::FP8_B) {
-    // fp8 natural: the wave's one instruction fills k-rows 4*wave + lane/16
+    // fp8 natural: instruction i fills k-rows 4*(wave + NW*i) + lane/16
     // (256 bytes each); slot lane%16 holds logical 16-byte chunk
     // (lane%16) ^ (row & 7), i.e. columns 16 * that chunk .. +15.
-    const int kk = 4 * wave + (lane >> 4);
-    const int col = 16 * ((lane & 15) ^ (kk & 7));
-    b_voff[0] = (col < BN && n0 + col < p.N) ? (uint32_t)kk * (uint32_t)p.ldb + (uint32_t)(n0 + col) : kOOB;
+#pragma unroll
+    for (int i = 0; i < C::B_UNITS; ++i) {
+      const int kk = 4 * (wave + NW * i) + (lane >> 4);
+      const int col = 16 * ((lane & 15) ^ (kk & 7));
+      b_voff[i] = (col < BN && n0 + col < p.N) ? (uint32_t)kk * (uint32_t)p.ldb + (uint32_t)(n0 + col) : kOOB;
+    }
   } else {
     const int kk = 2 * wave + (lane >> 5);
     const int q = lane & 31;
     const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
 #pragma unroll
     for (int i = 0; i < C::B_UNITS; ++i)
-      b_voff[i] = (col < BN && n0 + col < p.N) ? (uint32_t)(kk + 16 * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+      b_voff[i] = (col < BN && n0 + col < p.N) ? (uint32_t)(kk + 2 * NW * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
   }
 
   // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
@@ -278,11 +283,11 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
     const int k0 = kbeg + kt * BK;
     const bool live = k0 < kend;  // uniform
     if (d < C::A_UNITS) {
-      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u, lbase + s * C::A_BYTES + (wave + 8 * d) * 1024);
+      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
     } else {
       const int i = d - C::A_UNITS;
       const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)p.ldb : (uint32_t)k0 * ldb2);
-      dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + 8 * i) * 1024);
+      dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + NW * i) * 1024);
     }
   };
   constexpr int NDMA = C::A_UNITS + C::B_UNITS;
@@ -382,7 +387,7 @@ __global__ __launch_bounds__(kBigThreads, 1) void big_gemm_kernel(BigParams p) {
   // sched_barriers pin this instruction order.
   Frags f0, f1;
   constexpr int NMFMA = FM * FN;
-  static_assert(NREAD <= NMFMA && (NDMA == 4 || NDMA == 3), "one fragment read per MFMA slot");
+  static_assert(NREAD <= NMFMA && NDMA <= NMFMA / 2, "one fragment read per MFMA slot");
   auto step = [&](int kt, int s, const Frags& cur, Frags& nxt) {
 #pragma unroll
     for (int m = 0; m < NMFMA; ++m) {

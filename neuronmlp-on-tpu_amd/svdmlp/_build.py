@@ -35,6 +35,10 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed fp32 ops stay disabled for all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # The 4-wave large-tile kernels unroll 64 MFMA slots per k-step; a lower
+    # pragma-unroll threshold leaves that loop rolled and the accumulators in
+    # scratch memory.
+    "-mllvm", "-pragma-unroll-threshold=100000",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
