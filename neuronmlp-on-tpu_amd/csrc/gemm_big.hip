@@ -6,9 +6,9 @@ namespace svdmlp {
 
 namespace {
 
-template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8>
+template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8, int NS = 4>
 hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
-  using C = BigCfg<FN, BK, EPI, F32, F8, NW>;
+  using C = BigCfg<FN, BK, EPI, F32, F8, NW, NS>;
   dim3 grid(p.mtiles * p.ntiles, splits, batch);
   hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(C::THREADS), 0, st, p);
   return hipGetLastError();

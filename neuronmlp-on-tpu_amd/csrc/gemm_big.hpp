@@ -161,7 +161,7 @@ struct BigParams {
   int k_split;
 };
 
-template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8>
+template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8, int NS_ = 4>
 struct BigCfg {
   // NW waves per block in a 2 (n) x NW/2 (m) arrangement: a wave's tile is
   // (BM / (NW/2)) x 16*FN, i.e. 64 x 16*FN with 8 waves (two per SIMD) or
@@ -177,7 +177,7 @@ struct BigCfg {
   // HBM, widened to bf16 after the transposing LDS read.
   static constexpr bool FP8_B = FP8_B_;
   static constexpr int BM = 256, BN = 32 * FN, BK = 32;  // BK per stage
-  static constexpr int STAGES = 4;
+  static constexpr int STAGES = NS_;  // LDS stages: NS-2 in flight while one is read
   static constexpr int A_BYTES = BM * 64;                      // 16 KB
   static constexpr int B_PITCH = FP8_B ? 256 : 512;
   static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (fp8: 8 KB; Linear: rows >= BN read zeros)
@@ -189,16 +189,16 @@ struct BigCfg {
   static_assert(!(FP8_B && B_KC), "fp8 B is read in natural layout only");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
   static_assert(B_KC ? BN <= 256 : true, "Linear-layout B tile holds at most 256 rows");
-  static_assert(STAGES * STAGE <= 160 * 1024, "LDS budget");
+  static_assert(STAGES >= 4 && STAGES * STAGE <= 160 * 1024, "LDS budget");
 };
 
 template <class C>
 __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   constexpr int FM = C::FM, FN = C::FN, BM = C::BM, BN = C::BN, BK = C::BK, NW = C::NW;
   constexpr int NS = C::STAGES;
-  // LDS: the A tiles of the 4 stages in the first 64 KB, the B tiles in the
-  // next 64 KB, so that every fragment read of any stage is one base
-  // register plus a 16-bit immediate offset.
+  // LDS: the A tiles of the NS stages, then their B tiles, so that every
+  // fragment read of any stage is one base register plus an immediate offset
+  // (16-bit: within 64 KB for 4 stages).
   constexpr int B_REGION = NS * C::A_BYTES;
   __shared__ __attribute__((aligned(1024))) char lds[NS * (C::A_BYTES + C::B_BYTES)];
 
@@ -374,17 +374,17 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     }
   };
 
-  // Stage kt sits in slot kt % 4.  Step kt runs the MFMAs of stage kt
+  // Stage kt sits in slot kt % NS.  Step kt runs the MFMAs of stage kt
   // (fragments already in registers, read in step kt-1) and, interleaved
   // one per MFMA so that no wave holds its MFMAs behind a burst of memory
   // instructions:
   //  * the fragment reads of stage kt+1;
-  //  * the DMA of stage kt+4 into slot kt % 4, free since every wave's
+  //  * the DMA of stage kt+NS into slot kt % NS, free since every wave's
   //    reads of stage kt completed before the barrier that ended step kt-1.
-  // Then it waits until stage kt+2 landed (stages kt+3 and kt+4 may still be
-  // in flight: 8 DMA instructions) and meets the other waves at the barrier.
-  // DMAs past kend fetch zeros and keep the per-wave count constant.  The
-  // sched_barriers pin this instruction order.
+  // Then it waits until stage kt+2 landed (stages kt+3 .. kt+NS may still be
+  // in flight: (NS-2) * NDMA instructions) and meets the other waves at the
+  // barrier.  DMAs past kend fetch zeros and keep the per-wave count
+  // constant.  The sched_barriers pin this instruction order.
   Frags f0, f1;
   constexpr int NMFMA = FM * FN;
   static_assert(NREAD <= NMFMA && NDMA <= NMFMA / 2, "one fragment read per MFMA slot");
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       mfma_one(m, cur);
       __builtin_amdgcn_sched_barrier(0);
     }
-    wait_dma<2 * NDMA>();
+    wait_dma<(NS - 2) * NDMA>();
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -408,18 +408,25 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int d = 0; d < NDMA; ++d) dma_one(s, s, d);
-    wait_dma<2 * NDMA>();  // stages 0 and 1 landed
+    wait_dma<(NS - 2) * NDMA>();  // stages 0 and 1 landed
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < NREAD; ++r) read_one(0, r, f0);
     __syncthreads();  // every wave holds stage 0 before step 0 refills its slot
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int kt = 0; kt < nk; kt += 4) {
-    step(kt, 0, f0, f1);
-    if (kt + 1 < nk) step(kt + 1, 1, f1, f0);
-    if (kt + 2 < nk) step(kt + 2, 2, f0, f1);
-    if (kt + 3 < nk) step(kt + 3, 3, f1, f0);
+  // unrolled over the slot cycle and the f0/f1 alternation
+  constexpr int UNROLL = NS % 2 ? 2 * NS : NS;
+  for (int kt = 0; kt < nk; kt += UNROLL) {
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (kt + u < nk) {
+        if (u % 2 == 0)
+          step(kt + u, u % NS, f0, f1);
+        else
+          step(kt + u, u % NS, f1, f0);
+      }
+    }
   }
   wait_dma<0>();  // drain DMAs of stages past the end before the block exits
 
