@@ -66,9 +66,11 @@ const char* svdmlp_last_error(void);
  * T tokens, hidden size d, intermediate size ff and (maximum) rank r.  The
  * same workspace may be reused by consecutive calls on one stream of one
  * device.  Its first 4096 bytes must be zero before its first use: they hold
- * the grid-barrier counters of the persistent decode kernel, which only ever
- * grow.  The 64-bit word at byte 2304 becomes nonzero only if a barrier timed
- * out (the call's output is then undefined and the 4 KB must be zeroed again).
+ * the grid-barrier and block-done counters of the persistent decode kernels
+ * (the streaming-GEMV layer at 1-4 tokens and the MFMA layer above), which
+ * only ever grow.  The 64-bit word at byte 2304 becomes nonzero only if a
+ * barrier timed out (the call's output is then undefined and the 4 KB must
+ * be zeroed again).
  * Replaces the VMEM planning of test_speedup.py:208-258 (the TPU kernels keep
  * XU in VMEM scratch; here the rank-r intermediate lives in this buffer).
  */

@@ -582,8 +582,9 @@ bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, 
 // The persistent decode layer takes bf16 activations and factors in natural
 // layout, T <= 64, ranks and d multiples of 128 and ff a multiple of 64 (its
 // tiles), every operand below 2 GB (32-bit buffer offsets).
-// Below kDlMinT tokens the per-stage decode kernels are faster (measured on
-// MI355X, 8B shape: T=1 77 us vs 88 us; T=8 120 vs 95; T=64 539 vs 250).
+// Below kDlMinT tokens the per-stage decode kernels beat this MFMA layer
+// (measured on MI355X, 8B shape: T=1 77 us vs 88 us; T=8 120 vs 95; T=64
+// 539 vs 250); the streaming-GEMV layer, tried first, takes 1 <= T <= 4.
 constexpr int64_t kDlMinT = 4;
 
 bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,

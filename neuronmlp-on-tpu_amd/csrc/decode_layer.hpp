@@ -1,5 +1,5 @@
 // The whole SVD-MLP layer at decode shapes (T <= 64 tokens) in one
-// persistent, cooperatively launched kernel.
+// persistent launch (a plain launch of one block per CU; see the launcher).
 //
 // At these shapes the layer is a stream of 311 MB of bf16 factors (LLaMA3-8B,
 // r = 2816) against a few KB of activations, so the design goal is to keep
