@@ -11,6 +11,9 @@ Host package over libsvdmlp.so (hand-written HIP kernels for gfx950):
 * :mod:`svdmlp.inputs`  -- seeded synthetic inputs of the benchmark configs.
 * :mod:`svdmlp.fp8`     -- fp8 e4m3fn per-channel factor quantization.
 * :mod:`svdmlp.stack`   -- the N-layer MLP stack (RMSNorm, MLP, residual).
+* :mod:`svdmlp.checkpoint` -- SVD factors from sharded safetensors checkpoints
+  (models/hf_svd.py), and :mod:`svdmlp.checkpoint_speedup`, the per-layer
+  real-checkpoint runner (bench/checkpoint_speedup.py).
 """
 
 from ._lib import SvdMlpError, load, version, workspace_bytes  # noqa: F401

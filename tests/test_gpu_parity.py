@@ -359,3 +359,52 @@ def test_mlp_stack_nonuniform_ranks(gpu):
     x0 = x.float().cpu().numpy()
     assert _rel(y, ref) < BF16_TOL
     assert _rel(y - x0, ref - x0) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------
+# safetensors SVD checkpoint (models/hf_svd.py) -> the HIP layer
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("layout,T", [("natural", 1), ("natural", 300), ("linear", 64)])
+def test_checkpoint_layers_run_on_the_hip_path(gpu, tmp_path, layout, T):
+    """Factors written as a two-shard checkpoint (stored as Linear weights with
+    the v/u names swapped), loaded back onto the GPU, give the oracle's layer."""
+    from svdmlp import checkpoint
+
+    shape = inputs.LayerShape(1024, 2048, 512)
+    layers = []
+    for seed in (3, 4):
+        _, f = inputs.make_layer(shape, T=1, seed=seed)
+        layers.append([torch.from_numpy(inputs.as_float32(a, torch.bfloat16)).to(torch.bfloat16) for a in f])
+    checkpoint.save_mlp_checkpoint(tmp_path, layers, hidden_size=shape.d, intermediate_size=shape.ff)
+    loaded = checkpoint.load_mlp_factors(tmp_path, [1, 0], device=gpu, layout=layout)
+    x = _x(T, shape.d, 500 + T)
+    xt = _to(x, torch.bfloat16, gpu)
+    for got, want in zip(loaded, (layers[1], layers[0])):
+        y = _np(ops.svd_mlp(xt, *got))
+        err = _rel(y, O.svd_mlp_ref(x, *[w.float().numpy() for w in want], dtype="bfloat16"))
+        assert err < BF16_TOL, (layout, T, err)
+
+
+def test_checkpoint_runner_per_layer_report(gpu, tmp_path):
+    """python -m svdmlp.checkpoint_speedup on a synthetic checkpoint: every
+    (layer, T) verified against the fp32 arm, timed, summarised."""
+    from svdmlp import checkpoint, checkpoint_speedup
+
+    shape = inputs.LayerShape(1024, 2048, 512)
+    layers = []
+    for seed in (5, 6):
+        _, f = inputs.make_layer(shape, T=1, seed=seed)
+        layers.append([torch.from_numpy(a).to(torch.bfloat16) for a in f])
+    ckpt = tmp_path / "ckpt"
+    checkpoint.save_mlp_checkpoint(ckpt, layers, hidden_size=shape.d, intermediate_size=shape.ff)
+    out = tmp_path / "report.json"
+    report = checkpoint_speedup.run(checkpoint_speedup._parser().parse_args(
+        ["--model-path", str(ckpt), "--seq-lens", "1", "128", "--warmup", "1", "--repeats", "3",
+         "--output", str(out)]))
+    assert report["complete"] and len(report["records"]) == 4
+    for rec in report["records"]:
+        assert rec["passed"] and rec["fused_vs_fp32"]["relative_l2"] < BF16_TOL
+        assert rec["fused_ms"] > 0 and rec["unfused_low_rank_ms"] > 0
+    assert all(s["complete"] and s["passed"] for s in report["summaries"])
+    assert out.with_suffix(".csv").exists()
