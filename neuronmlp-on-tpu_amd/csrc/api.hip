@@ -144,6 +144,7 @@ struct Ws {
   size_t y32;      // [T][big] fp32 output accumulator (decode)
   size_t part;     // [splits][batch][T][N] fp32 split-K partial slices (prefill)
   size_t norm;     // [T][d] RMSNorm output of the MLP block (4 bytes/elem worst case)
+  size_t g;        // bf16 gate values of the large-tile g pass, fragment order over padded tiles
   size_t total;
 };
 
@@ -204,6 +205,10 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   off += a256(part);
   w.norm = off;
   off += a256(T * d * 4);
+  // the large-tile path serves T > kDecodeMaxT only; its g tiles are 256 rows
+  // by 224 or 256 columns
+  w.g = off;
+  off += dec ? 0 : a256(((T + 255) / 256 * 256) * std::max((big + 223) / 224 * 224, (big + 255) / 256 * 256) * 2);
   w.total = off;
   return w;
 }
@@ -402,8 +407,10 @@ bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes, std
 int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
-             bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr) {
+             bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
+             int gfrag = 0) {
   BigParams p{};
+  p.gfrag = gfrag;
   const bool fp8 = c.wt == SVDMLP_FP8_E4M3;
   if (fp8 && (!s0 || b_kc)) return fail("fp8 large-tile GEMM needs natural-layout weights and scales");
   p.scale[0] = s0;
@@ -510,10 +517,10 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   if (fn == 0) fn = (ff % 224 == 0) ? 7 : 8;
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * ff * wbytes(c);
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r,
-                    1, fn, BEPI_STORE, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
+                    1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
   if (rc) return rc;
   return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r, 1,
-                  fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf, false, 0, s_vu);
+                  fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1);
 }
 
 // y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
@@ -834,7 +841,7 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
     const float* sus[2] = {s_ug, s_uu};
     if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L, fp8 ? sus : nullptr))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
-    uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.h);
+    uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
     return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h, fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr);
   }
 
@@ -1012,7 +1019,7 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
     if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L, sus))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
-    uint16_t* gbuf = hbuf + T * ff;
+    uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
     if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf, S[1], S[3]))) return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};

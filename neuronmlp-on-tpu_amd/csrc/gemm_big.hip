@@ -37,6 +37,9 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
     case BEPI_SWIGLU_MEM:
       if constexpr (FN != 4) return go_b<FN, BEPI_SWIGLU_MEM>(d, p, splits, batch, st);
       break;
+    case BEPI_STORE_FRAG:
+      if constexpr (FN != 4) return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
+      break;
     default: break;
   }
   *why = "big GEMM: unsupported epilogue for this tile";

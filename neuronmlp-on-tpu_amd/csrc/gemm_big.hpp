@@ -143,7 +143,13 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 v) {
 // 32-byte unit swizzle of a natural-layout B row k.
 __device__ __forceinline__ int bnat_swz(int k) { return k & 3; }
 
-enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2 };
+// BEPI_STORE_FRAG writes bf16 in fragment order: the 16x16 block (i, j) of
+// wave w of output tile t = m_tile + mtiles * n_tile is 512 contiguous bytes
+// at element ((t * NW + w) * FM * FN + i * FN + j) * 256 + 4 * lane, so every
+// store (and the SwiGLU epilogue's matching load, with p.gfrag) moves one
+// contiguous 512-byte piece.  Padded tiles are written too (zeros): the
+// buffer holds mtiles * 256 x ntiles * BN elements.
+enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2, BEPI_STORE_FRAG = 3 };
 
 struct BigParams {
   const void* a[2];  // per batch entry (blockIdx.z)
@@ -156,6 +162,7 @@ struct BigParams {
   int64_t out_sstride;   // elements between split-K partial slices (fp32 output)
   const uint16_t* gmem;  // BEPI_SWIGLU_MEM: bf16 gate values, same layout as out
   const float* scale[2]; // fp8 B: one fp32 scale per output column, per batch entry
+  int gfrag;             // BEPI_SWIGLU_MEM: gmem holds g in fragment order (BEPI_STORE_FRAG)
   int M, N, K;
   int mtiles, ntiles;
   int k_split;
@@ -433,16 +440,26 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
   const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
   char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
+  constexpr bool FRAG = C::EPI == BEPI_STORE_FRAG;
+  // fragment-order element offset of this lane's block (0, 0)
+  const int64_t frag0 = ((((int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN)) * NW + wave) * FM * FN) * 256 + 4 * lane;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm0 + 16 * i + lr;
-    if (m >= p.M) continue;
+    if (!FRAG && m >= p.M) continue;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn0 + 16 * j + 4 * lg;
-      if (n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+      if (!FRAG && n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
       f32x4 v = acc[i][j];
-      if constexpr (C::FP8_B) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
+      if constexpr (C::FP8_B)
+        if (n < p.N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
+      const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
+      if constexpr (FRAG) {
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + fo) =
+            u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+        continue;
+      }
       const int64_t o = (int64_t)m * p.ldo + n;
       if constexpr (C::EPI == BEPI_ATOMIC) {
         float* op = reinterpret_cast<float*>(outp) + o;
@@ -453,7 +470,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       } else if constexpr (C::OUT_F32) {
         *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + o) = v;
       } else if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
-        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + o);
+        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : o));
         const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
         const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
         *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) =
