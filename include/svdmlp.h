@@ -68,9 +68,10 @@ const char* svdmlp_last_error(void);
  * device.  Its first 4096 bytes must be zero before its first use: they hold
  * the grid-barrier and block-done counters of the persistent decode kernels
  * (the streaming-GEMV layer at 1-4 tokens and the MFMA layer above), which
- * only ever grow.  The 64-bit word at byte 2304 becomes nonzero only if a
- * barrier timed out (the call's output is then undefined and the 4 KB must
- * be zeroed again).
+ * only ever grow, and the MFMA layer's split-K tile counters (from byte
+ * 2560), which every call leaves at zero.  The 64-bit word at byte 2304
+ * becomes nonzero only if a barrier timed out (the call's output is then
+ * undefined and the 4 KB must be zeroed again).
  * Replaces the VMEM planning of test_speedup.py:208-258 (the TPU kernels keep
  * XU in VMEM scratch; here the rank-r intermediate lives in this buffer).
  */

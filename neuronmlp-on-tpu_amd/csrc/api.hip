@@ -145,6 +145,7 @@ struct Ws {
   size_t part;     // [splits][batch][T][N] fp32 split-K partial slices (prefill)
   size_t norm;     // [T][d] RMSNorm output of the MLP block (4 bytes/elem worst case)
   size_t g;        // bf16 gate values of the large-tile g pass, fragment order over padded tiles
+  size_t slices;   // split-K partial sums of the MFMA decode layer (decode only)
   size_t total;
 };
 
@@ -209,6 +210,8 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   // by 224 or 256 columns
   w.g = off;
   off += dec ? 0 : a256(((T + 255) / 256 * 256) * std::max((big + 223) / 224 * 224, (big + 255) / 256 * 256) * 2);
+  w.slices = off;
+  off += dec ? a256((int64_t)kDlMaxGrid * decode_layer_mt((int)T) * 2048 * 4) : 0;
   w.total = off;
   return w;
 }
@@ -599,6 +602,9 @@ bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t 
   if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T > kDecodeMaxT || !tune().dlayer) return false;
   if (T < std::min<int64_t>(kDlMinT, tune().dlmin)) return false;
   if (d % 128 || r_gu % 128 || r_d % 128 || ff % 64) return false;
+  // one counter per split-K tile of phases 1, 3 and 4; the bf16 XU_d
+  // lives in the decode-only gu32 region (2 T max(d, ff) fp32)
+  if (2 * r_gu / 128 + r_d / 128 + d / 128 > kDlMaxTiles || r_d > 4 * std::max(d, ff)) return false;
   const int64_t lim = (int64_t)1 << 31;
   for (int64_t bytes : {T * d * 2, d * r_gu * 2, r_gu * ff * 2, ff * r_d * 2, r_d * d * 2, T * ff * 2, 2 * T * r_gu * 4})
     if (bytes >= lim) return false;
@@ -630,10 +636,10 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.ud = ud;
   p.vd = vd;
   p.y = y;
-  p.xu32 = reinterpret_cast<float*>(ws + L.xu32);
-  p.xd32 = p.xu32 + 2 * T * r_gu;
+  p.xu16 = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
+  p.xd16 = reinterpret_cast<uint16_t*>(ws + L.gu32);
   p.h = reinterpret_cast<uint16_t*>(ws + L.h);
-  p.y32 = reinterpret_cast<float*>(ws + L.y32);
+  p.slices = reinterpret_cast<float*>(ws + L.slices);
   p.sync = reinterpret_cast<uint64_t*>(ws + L.sync);
   p.T = (int)T;
   p.d = (int)d;
@@ -644,6 +650,9 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.units2 = (int)(ff / 64);
   p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
   p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
+  p.splits1 = p.units1 / (int)(2 * r_gu / 128);
+  p.splits3 = p.units3 / (int)(r_d / 128);
+  p.splits4 = p.units4 / (int)(d / 128);
   const char* why = nullptr;
   StageScope ss(ST_DEC_LAYER, c.st);
   return check(launch_decode_layer(p, mt, grid, c.st, &why), "decode layer", why);

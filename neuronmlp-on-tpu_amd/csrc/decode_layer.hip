@@ -1,10 +1,13 @@
-// Launcher of the persistent decode-layer kernel.  Grid = CU count with one
-// block per CU (its LDS takes most of a CU), so on an otherwise idle device
-// every block is resident at once.  A plain launch is used: a cooperative
+// Launcher of the persistent decode-layer kernel.  Grid = CU count (at most
+// kDlMaxGrid, the units the workspace's slice area holds) with one block per
+// CU (its LDS takes most of a CU), so on an otherwise idle device every block
+// is resident at once.  A plain launch is used: a cooperative
 // launch guarantees residency but costs ~20 us per launch on this stack
 // (~2.3 us for a plain one).  If other work holds CUs, late blocks only delay
 // the barriers; the bounded barrier spin turns a true deadlock into a flagged
 // error instead of a hang.
+#include <algorithm>
+
 #include "decode_layer.hpp"
 #include "dispatch.hpp"
 
@@ -36,7 +39,7 @@ int decode_layer_grid(int mt) {
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   const int per = mt == 1 ? blocks_per_cu<1>() : (mt == 2 ? blocks_per_cu<2>() : blocks_per_cu<4>());
-  return per >= 1 ? cus : 0;
+  return per >= 1 ? std::min(cus, kDlMaxGrid) : 0;
 }
 
 hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why) {

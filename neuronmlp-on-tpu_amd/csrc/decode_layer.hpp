@@ -12,22 +12,27 @@
 //    k & 3, and read with the transposing ds_read_b64_tr_b16, so no
 //    register transpose exists;
 //  * the activation rows (zero-padded to 16 * MT) follow in the same ring;
-//  * the layer runs as phases separated by grid barriers:
-//      0  zero the fp32 accumulators
-//      1  XU_g, XU_u += X . [Ug | Uu]               (split-K, fp32 atomics)
+//  * the layer runs as four phases separated by three grid barriers:
+//      1  XU_g, XU_u = X . [Ug | Uu]                (split-K)
 //      2  h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu))    (a block owns 64 columns
-//         of both branches over the whole rank: no split, no atomics)
-//      3  XU_d += h . Ud                             (split-K, fp32 atomics)
-//      4  y32 += XU_d . Vd                           (split-K, fp32 atomics)
-//      5  y = bf16(y32)
-//    The fp32 rank sums XU and XU_d are rounded to bf16 where they are read
-//    (the reference rounds the rank-r intermediate to the activation dtype);
+//         of both branches over the whole rank: no split)
+//      3  XU_d = h . Ud                              (split-K)
+//      4  y = XU_d . Vd                              (split-K)
+//  * split-K tiles (128 columns) are combined without atomics or a zero
+//    fill: every unit stores its fp32 accumulators, in register order, as a
+//    slice of the workspace and counts its arrival on the tile's counter;
+//    the block whose arrival completes the count adds the other slices to
+//    its registers and rounds the tile to bf16 once: XU and XU_d (the
+//    reference rounds the rank-r intermediate to the activation dtype) and y
+//    itself, so phases 2 to 4 stream bf16 activations and no barrier
+//    follows phase 4 (fp32 atomics onto shared sums cost ~20 us per phase at
+//    64 tokens);
 //  * before waiting at a barrier, every block already issues the weight DMAs
 //    of its first stages of the next phase (weights do not depend on the
 //    barrier), so barrier latency overlaps the weight stream.
-// Data crosses phases only through device-coherent accesses: fp32 atomics,
-// device-scope (sc1) stores of h and of the zero fill, and device-scope
-// loads (the activation DMAs, the final read of y32).  Each wave waits for
+// Data crosses blocks only through device-coherent accesses: device-scope
+// (sc1) stores and loads (slices, bf16 tiles, the activation DMAs) and the
+// counters' atomics.  Each wave waits for
 // its own writes (vmcnt(0)) before its block arrives at a barrier, so the
 // barriers need no cache write-back or invalidation (with agent-scope fences
 // a barrier costs ~9 us, without ~2 us).
@@ -55,17 +60,21 @@ struct DecLayerParams {
   const void* ud;
   const void* vd;
   void* y;         // (T, d) bf16
-  float* xu32;     // (2, T, r_gu) gate/up rank sums
+  uint16_t* xu16;  // (2, T, r_gu) bf16 gate/up rank intermediates
   uint16_t* h;     // (T, ff) bf16
-  float* xd32;     // (T, r_d)
-  float* y32;      // (T, d)
-  uint64_t* sync;  // barrier words, one per 128-byte line (kDlSync*)
+  uint16_t* xd16;  // (T, r_d) bf16 down rank intermediate
+  float* slices;   // split-K partial sums, MT * 2048 floats per unit (kDlMaxGrid units)
+  uint64_t* sync;  // barrier words, one per 128-byte line (kDl*), then split-K tile counters
   int T, d, ff, r_gu, r_d;
   int ks1, ks3, ks4;                   // K per split, phases 1, 3, 4 (multiples of 32)
   int units1, units2, units3, units4;  // tiles x splits
+  int splits1, splits3, splits4;       // splits per tile, phases 1, 3 and 4
 };
 
 constexpr int kDlThreads = 512;
+// Largest grid: a split-K phase has at most one unit per block, so the
+// slice area holds kDlMaxGrid units.
+constexpr int kDlMaxGrid = 256;
 constexpr int kDlWStage = 8192;    // 32 k x 128 columns bf16
 constexpr uint32_t kDlSpinLimit = 1u << 22;
 // Barrier words in the workspace's sync area, one 128-byte line each (in
@@ -78,7 +87,12 @@ constexpr int kDlFlag = kDlGen + kDlLine;
 // Block-done counter of the streaming-GEMV decode layer (monotone, like the
 // barrier counters: the last of every G arrivals finishes the launch).
 constexpr int kGvDone = kDlFlag + kDlLine;
-constexpr int kDlSyncBytes = (kGvDone + kDlLine) * 8;
+// 32-bit arrival counters of the split-K tiles of phases 1, 3 and 4 (in
+// that order) fill the rest of the 4 KB area.  The last arrival of a launch
+// resets its tile's counter to zero.
+constexpr int kDlTileWords = kGvDone + kDlLine;
+constexpr int kDlMaxTiles = (512 - kDlTileWords) * 2;
+constexpr int kDlSyncBytes = kDlTileWords * 8 + kDlMaxTiles * 4;
 
 // Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
 // weight bytes per block barrier) and the ring holds NS stages, as far as
@@ -153,14 +167,14 @@ struct DlUnit {
   int64_t ldb;  // elements
   uint32_t a_bytes, b_bytes;
   int n0, kb, ke;
-  float* out;  // atomic target (row-major, ldo)
+  uint16_t* dst;  // bf16 result (row-major, ldo)
   int64_t ldo;
 };
 
-// Compile-time shape of a unit: AF32 = fp32 activations (rank sums).
-template <int MT, bool AF32, bool DUAL>
+// Compile-time shape of a unit (bf16 activations).
+template <int MT, bool DUAL>
 struct DlShape {
-  static constexpr int A_ROW = AF32 ? 128 : 64;            // bytes per 32-k activation row
+  static constexpr int A_ROW = 64;                          // bytes per 32-k activation row
   static constexpr int A_SUB = 16 * MT * A_ROW;             // one branch of one stage
   static constexpr int NA = (DUAL ? 2 : 1) * A_SUB / 1024;  // 1 KB DMA instructions per stage
   static constexpr int CNT_A = (NA + 7) / 8;                // per wave per chunk (padded with dummies)
@@ -172,13 +186,14 @@ template <int MT>
 struct DlLds {
   static constexpr int NS = DlDepth<MT>::NS;
   static constexpr int KC = DlDepth<MT>::KC;
-  static constexpr int A_CHUNK = MT * 16 * 128 * 2;  // one 32-k chunk: fp32, two branches (the largest case)
+  static constexpr int A_CHUNK = MT * 16 * 64 * 2;  // one 32-k chunk: bf16, two branches (the largest case)
   static constexpr int W_SLOT = KC * kDlWStage;
   static constexpr int A_SLOT = KC * A_CHUNK;
   static constexpr int W_OFF = 0;
   static constexpr int A_OFF = NS * W_SLOT;
   static constexpr int DUMMY_OFF = A_OFF + NS * A_SLOT;
-  static constexpr int BYTES = DUMMY_OFF + 1024;
+  static constexpr int FLAG_OFF = DUMMY_OFF + 1024;  // one int: "this block finishes the tile"
+  static constexpr int BYTES = FLAG_OFF + 16;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -210,14 +225,13 @@ __device__ __forceinline__ void dl_dma_w(const DlCtx& c, const DlUnit& U, int j,
   }
 }
 
-// Activation DMAs of stage j into ring slot `slot` (CNT_A per wave).
-// bf16: instruction q holds rows 16q..16q+15 (64 bytes each, 16-byte chunk
-// XOR a_swz(row)); fp32: instruction q holds rows 8q..8q+7 (128 bytes each,
-// chunk XOR (row & 7)) of branch q / (NA/2) when DUAL.  Instructions past NA
-// are dummies (no records) into a scratch slot, keeping the per-wave count.
-template <int MT, bool AF32, bool DUAL>
+// Activation DMAs of stage j into ring slot `slot` (CNT_A per wave):
+// instruction q holds rows 16q..16q+15 (64 bytes each, 16-byte chunk XOR
+// a_swz(row)) of branch q / (NA/2) when DUAL.  Instructions past NA are
+// dummies (no records) into a scratch slot, keeping the per-wave count.
+template <int MT, bool DUAL>
 __device__ __forceinline__ void dl_dma_a(const DlCtx& c, const DlUnit& U, int j, int slot) {
-  using S = DlShape<MT, AF32, DUAL>;
+  using S = DlShape<MT, DUAL>;
   using L = DlLds<MT>;
 #pragma unroll
   for (int kc = 0; kc < L::KC; ++kc) {
@@ -231,18 +245,10 @@ __device__ __forceinline__ void dl_dma_a(const DlCtx& c, const DlUnit& U, int j,
         const int br = DUAL ? q / PER : 0, qq = q % PER;
         const void* ap = br ? U.a1 : U.a0;
         const i32x4 rs = make_rsrc_sgpr(ap, live ? U.a_bytes : 0u);
-        int row, lchunk;
-        uint32_t voff;
-        if constexpr (AF32) {
-          row = 8 * qq + (c.lane >> 3);
-          lchunk = (c.lane & 7) ^ (row & 7);
-          voff = row < c.T ? (uint32_t)row * (uint32_t)U.lda * 4u + (uint32_t)lchunk * 16u : kOOB;
-        } else {
-          row = 16 * qq + (c.lane >> 2);
-          lchunk = (c.lane & 3) ^ a_swz(row);
-          voff = row < c.T ? (uint32_t)row * (uint32_t)U.lda * 2u + (uint32_t)lchunk * 16u : kOOB;
-        }
-        const uint32_t soff = live ? (uint32_t)k0 * (AF32 ? 4u : 2u) : 0u;
+        const int row = 16 * qq + (c.lane >> 2);
+        const int lchunk = (c.lane & 3) ^ a_swz(row);
+        const uint32_t voff = row < c.T ? (uint32_t)row * (uint32_t)U.lda * 2u + (uint32_t)lchunk * 16u : kOOB;
+        const uint32_t soff = live ? (uint32_t)k0 * 2u : 0u;
         dma16_dev(rs, voff, soff, c.lbase + L::A_OFF + slot * L::A_SLOT + kc * L::A_CHUNK + br * S::A_SUB + qq * 1024);
       } else {
         dma16_dev(make_rsrc_sgpr(U.a0, 0u), kOOB, 0u, c.lbase + L::DUMMY_OFF);
@@ -271,9 +277,9 @@ __device__ __forceinline__ void dl_wait_head(int j) {
 // weight DMAs of stages 0..NS-2 (before the grid barrier); wave 0 issues
 // its own here, ahead of the activation DMAs, keeping every wave's order
 // W(0..NS-2), A(0..NS-2), then (W, A) per step.
-template <int MT, bool AF32, bool DUAL>
+template <int MT, bool DUAL>
 __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool prefetched, f32x4 (&acc)[MT]) {
-  using S = DlShape<MT, AF32, DUAL>;
+  using S = DlShape<MT, DUAL>;
   using L = DlLds<MT>;
   constexpr int NS = L::NS, KC = L::KC;
   const int nk = (U.ke - U.kb + 32 * KC - 1) / (32 * KC);
@@ -282,7 +288,7 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
 
   if (!prefetched || c.wave == 0)
     for (int s = 0; s < NS - 1; ++s) dl_dma_w<MT, DUAL>(c, U, s, s);
-  for (int s = 0; s < NS - 1; ++s) dl_dma_a<MT, AF32, DUAL>(c, U, s, s);
+  for (int s = 0; s < NS - 1; ++s) dl_dma_a<MT, DUAL>(c, U, s, s);
 
   // fragment addresses within a slot
   const int sub = c.wave >> 2, lu = c.wave & 3;
@@ -298,7 +304,7 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
     dl_block_sync();
     const int sn = j + NS - 1, slot_n = sn % NS;
     dl_dma_w<MT, DUAL>(c, U, sn, slot_n);
-    dl_dma_a<MT, AF32, DUAL>(c, U, sn, slot_n);
+    dl_dma_a<MT, DUAL>(c, U, sn, slot_n);
 
     const int slot = j % NS;
 #pragma unroll
@@ -310,19 +316,7 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int row = 16 * mt + c.lr;
-        u32x4 fa;
-        if constexpr (AF32) {
-          const lds_cptr rp = ab + row * 128;
-          const int x = row & 7;
-          const u32x4 v0 = lds_read_b128(rp + (((2 * c.lg) ^ x) << 4));
-          const u32x4 v1 = lds_read_b128(rp + (((2 * c.lg + 1) ^ x) << 4));
-          fa = u32x4{pack_bf16x2(__uint_as_float(v0.x), __uint_as_float(v0.y)),
-                     pack_bf16x2(__uint_as_float(v0.z), __uint_as_float(v0.w)),
-                     pack_bf16x2(__uint_as_float(v1.x), __uint_as_float(v1.y)),
-                     pack_bf16x2(__uint_as_float(v1.z), __uint_as_float(v1.w))};
-        } else {
-          fa = lds_read_b128(ab + row * 64 + ((c.lg ^ a_swz(row)) << 4));
-        }
+        const u32x4 fa = lds_read_b128(ab + row * 64 + ((c.lg ^ a_swz(row)) << 4));
         acc[mt] = mfma_chunk(fb, fa, acc[mt], __bf16{});
       }
     }
@@ -331,20 +325,69 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
   dl_block_sync();
 }
 
-// fp32 atomics of a unit's accumulators into U.out.
-template <int MT, bool DUAL>
-__device__ __forceinline__ void dl_atomic_out(const DlCtx& c, const DlUnit& U, const f32x4 (&acc)[MT]) {
-  const int n = U.n0 + (DUAL ? 0 : 64 * (c.wave >> 2)) + 16 * (c.wave & 3) + 4 * c.lg;
+// Split-K combination of unit u = tile + split * nt (splits per tile) into
+// the bf16 tile at `dst` (row pitch U.ldo, columns from U.n0).  Lane layout
+// of acc: D[n = 4*lg + t][m = lr] of each 16-row block mt.
+//  * one split: the accumulators are rounded straight to dst;
+//  * otherwise the unit stores its rows < T as slice u (16 bytes per lane
+//    and block mt, in register order) and, once every wave's stores have
+//    completed, counts its arrival on the tile's counter; the block that
+//    completes the count adds the other splits' slices to its registers (four
+//    slices in flight at a time), resets the counter and rounds to dst.
+// Units of a split phase never exceed the grid (at most one per block).
+template <int MT>
+__device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x4 (&acc)[MT], int u, int nt,
+                                           int splits, uint32_t* cnt, float* slices, int* flag, uint16_t* dst) {
+  const int n = U.n0 + 64 * (c.wave >> 2) + 16 * (c.wave & 3) + 4 * c.lg;
+  if (splits > 1) {
+    float* mine = slices + (int64_t)u * MT * 2048 + 4 * threadIdx.x;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      if (16 * mt + c.lr < c.T) {
+        dl_store8(mine + mt * 2048, u32x2{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y)});
+        dl_store8(mine + mt * 2048 + 2, u32x2{__float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)});
+      }
+    dl_wait_vm<0>();
+    dl_block_sync();
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old + 1 == (uint32_t)splits;
+      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    dl_block_sync();
+    if (!*flag) return;
+    const int split = u / nt, tile = u - split * nt;
+    for (int s0 = 0; s0 < splits; s0 += 4) {
+      u32x2 v[4][MT][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int s = s0 + i;
+        const float* o = slices + (int64_t)(tile + s * nt) * MT * 2048 + 4 * threadIdx.x;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const bool live = s < splits && s != split && 16 * mt + c.lr < c.T;
+          v[i][mt][0] = live ? dl_load8(o + mt * 2048) : u32x2{0u, 0u};
+          v[i][mt][1] = live ? dl_load8(o + mt * 2048 + 2) : u32x2{0u, 0u};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[mt].x += __uint_as_float(v[i][mt][0].x);
+          acc[mt].y += __uint_as_float(v[i][mt][0].y);
+          acc[mt].z += __uint_as_float(v[i][mt][1].x);
+          acc[mt].w += __uint_as_float(v[i][mt][1].y);
+        }
+    }
+  }
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + c.lr;
-    if (m < c.T) {
-      float* o = U.out + (int64_t)m * U.ldo + n;
-      dl_atomic_add(o + 0, acc[mt].x);
-      dl_atomic_add(o + 1, acc[mt].y);
-      dl_atomic_add(o + 2, acc[mt].z);
-      dl_atomic_add(o + 3, acc[mt].w);
-    }
+    if (m < c.T)
+      dl_store8(dst + (int64_t)m * U.ldo + n,
+                u32x2{pack_bf16x2(acc[mt].x, acc[mt].y), pack_bf16x2(acc[mt].z, acc[mt].w)});
   }
 }
 
@@ -360,6 +403,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   c.lr = c.lane & 15;
   c.lg = c.lane >> 4;
   c.T = p.T;
+  int* const flag = reinterpret_cast<int*>(lds + L::FLAG_OFF);
+  uint32_t* const tiles = reinterpret_cast<uint32_t*>(p.sync + kDlTileWords);
   const int G = gridDim.x, b = blockIdx.x;
   const int T = p.T;
   constexpr int NS = L::NS;
@@ -381,13 +426,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.n0 = (tile % per) * 128;
       U.kb = split * p.ks1;
       U.ke = min(p.d, U.kb + p.ks1);
-      U.out = p.xu32 + (int64_t)br * T * p.r_gu;
+      U.dst = p.xu16 + (int64_t)br * T * p.r_gu;
       U.ldo = p.r_gu;
     } else if (phase == 2) {
-      U.a0 = p.xu32;
-      U.a1 = p.xu32 + (int64_t)T * p.r_gu;
+      U.a0 = p.xu16;
+      U.a1 = p.xu16 + (int64_t)T * p.r_gu;
       U.lda = p.r_gu;
-      U.a_bytes = (uint32_t)((int64_t)T * p.r_gu * 4);
+      U.a_bytes = (uint32_t)((int64_t)T * p.r_gu * 2);
       U.b0 = p.vg;
       U.b1 = p.vu;
       U.ldb = p.ff;
@@ -395,7 +440,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.n0 = u * 64;
       U.kb = 0;
       U.ke = p.r_gu;
-      U.out = nullptr;
+      U.dst = p.h;
       U.ldo = p.ff;
     } else if (phase == 3) {
       const int nt = p.r_d / 128;
@@ -409,21 +454,21 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.n0 = tile * 128;
       U.kb = split * p.ks3;
       U.ke = min(p.ff, U.kb + p.ks3);
-      U.out = p.xd32;
+      U.dst = p.xd16;
       U.ldo = p.r_d;
     } else {
       const int nt = p.d / 128;
       const int tile = u % nt, split = u / nt;
-      U.a0 = U.a1 = p.xd32;
+      U.a0 = U.a1 = p.xd16;
       U.lda = p.r_d;
-      U.a_bytes = (uint32_t)((int64_t)T * p.r_d * 4);
+      U.a_bytes = (uint32_t)((int64_t)T * p.r_d * 2);
       U.b0 = U.b1 = p.vd;
       U.ldb = p.d;
       U.b_bytes = (uint32_t)((int64_t)p.r_d * p.d * 2);
       U.n0 = tile * 128;
       U.kb = split * p.ks4;
       U.ke = min(p.r_d, U.kb + p.ks4);
-      U.out = p.y32;
+      U.dst = static_cast<uint16_t*>(p.y);
       U.ldo = p.d;
     }
   };
@@ -443,26 +488,15 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     }
   };
 
-  // ---- phase 0: zero the accumulators ----
-  {
-    const int64_t tid = (int64_t)b * kDlThreads + threadIdx.x, stride = (int64_t)G * kDlThreads;
-    const u32x2 z = {0u, 0u};
-    const int64_t n1 = (int64_t)2 * T * p.r_gu / 2, n2 = (int64_t)T * p.r_d / 2, n3 = (int64_t)T * p.d / 2;
-    for (int64_t i = tid; i < n1; i += stride) dl_store8(p.xu32 + 2 * i, z);
-    for (int64_t i = tid; i < n2; i += stride) dl_store8(p.xd32 + 2 * i, z);
-    for (int64_t i = tid; i < n3; i += stride) dl_store8(p.y32 + 2 * i, z);
-  }
-  dl_wait_vm<0>();
-  prefetch(1);
-  dl_grid_sync(p.sync, gen0, ++nbar);
+  const int nt1 = 2 * (p.r_gu / 128), nt3 = p.r_d / 128, nt4 = p.d / 128;
 
-  // ---- phase 1: XU_g, XU_u += X . [Ug | Uu] ----
+  // ---- phase 1: XU_g, XU_u = X . [Ug | Uu] -> bf16 XU ----
   for (int u = b; u < units[1]; u += G) {
     DlUnit U;
     unit_of(1, u, U);
     f32x4 acc[MT];
-    dl_run<MT, false, false>(c, U, u == b, acc);
-    dl_atomic_out<MT, false>(c, U, acc);
+    dl_run<MT, false>(c, U, false, acc);
+    dl_combine<MT>(c, U, acc, u, nt1, p.splits1, tiles + u % nt1, p.slices, flag, U.dst);
   }
   dl_wait_vm<0>();
   prefetch(2);
@@ -473,7 +507,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     DlUnit U;
     unit_of(2, u, U);
     f32x4 acc[MT];
-    dl_run<MT, true, true>(c, U, u == b, acc);
+    dl_run<MT, true>(c, U, u == b, acc);
     // waves 4..7 hold u, waves 0..3 g, for the same lanes' (m, n)
     f32x4* xch = reinterpret_cast<f32x4*>(lds + L::A_OFF);
     if (c.wave >= 4) {
@@ -500,39 +534,26 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   prefetch(3);
   dl_grid_sync(p.sync, gen0, ++nbar);
 
-  // ---- phase 3: XU_d += h . Ud ----
+  // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
   for (int u = b; u < units[3]; u += G) {
     DlUnit U;
     unit_of(3, u, U);
     f32x4 acc[MT];
-    dl_run<MT, false, false>(c, U, u == b, acc);
-    dl_atomic_out<MT, false>(c, U, acc);
+    dl_run<MT, false>(c, U, u == b, acc);
+    dl_combine<MT>(c, U, acc, u, nt3, p.splits3, tiles + nt1 + u % nt3, p.slices, flag, U.dst);
   }
   dl_wait_vm<0>();
   prefetch(4);
   dl_grid_sync(p.sync, gen0, ++nbar);
 
-  // ---- phase 4: y32 += XU_d . Vd ----
+  // ---- phase 4: y = bf16(XU_d . Vd) ----
   for (int u = b; u < units[4]; u += G) {
     DlUnit U;
     unit_of(4, u, U);
     f32x4 acc[MT];
-    dl_run<MT, true, false>(c, U, u == b, acc);
-    dl_atomic_out<MT, false>(c, U, acc);
+    dl_run<MT, false>(c, U, u == b, acc);
+    dl_combine<MT>(c, U, acc, u, nt4, p.splits4, tiles + nt1 + nt3 + u % nt4, p.slices, flag, U.dst);
   }
-  dl_wait_vm<0>();
-  dl_grid_sync(p.sync, gen0, ++nbar);
-
-  // ---- phase 5: y = bf16(y32) ----
-  {
-    const int64_t tid = (int64_t)b * kDlThreads + threadIdx.x, stride = (int64_t)G * kDlThreads;
-    const int64_t n = (int64_t)T * p.d / 2;
-    for (int64_t i = tid; i < n; i += stride) {
-      const u32x2 v = dl_load8(p.y32 + 2 * i);
-      reinterpret_cast<uint32_t*>(p.y)[i] = pack_bf16x2(__uint_as_float(v.x), __uint_as_float(v.y));
-    }
-  }
-
 }
 
 }  // namespace svdmlp

@@ -204,16 +204,24 @@ def _barrier_state(ws):
     return w[272], w[288]
 
 
+def _tile_counters(ws):
+    """The MFMA decode layer's split-K tile arrival counters (32-bit words
+    from byte 2560 of the workspace's sync area to its end)."""
+    return ws[2560:4096].view(torch.int32).cpu().tolist()
+
+
 @pytest.mark.parametrize("shape,Ts", [
     (inputs.LayerShape(1024, 2048, 512), (1, 3, 17, 40, 64, 16)),      # every token-tile count, reused workspace
     (inputs.LayerShape(1024, 32768, 256), (5, 33)),                     # 512 column tiles: two units per block
+    (inputs.LayerShape(16640, 1024, 128), (8, 64)),                     # 130 output tiles: phase 4 unsplit
 ])
 def test_decode_layer_workspace_reuse(gpu, shape, Ts):
     """The persistent decode kernels (the streaming-GEMV layer up to 4
-    tokens, the MFMA layer above; one launch each, grid barriers in the
-    workspace's first 4096 bytes) over one reused workspace: results match
-    the oracle, every call advances the shared barrier generation by its
-    barriers and no barrier times out."""
+    tokens, the MFMA layer above; one launch each, grid barriers and split-K
+    tile counters in the workspace's first 4096 bytes) over one reused
+    workspace: results match the oracle, every call advances the shared
+    barrier generation by its barriers, no barrier times out and every tile
+    counter is back at zero."""
     x, f = inputs.make_layer(shape, T=max(Ts), seed=31)
     xb, *fb = _rounded((x, *f), torch.bfloat16)
     t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
@@ -223,8 +231,9 @@ def test_decode_layer_workspace_reuse(gpu, shape, Ts):
         y = _np(ops.svd_mlp(t[0][:T].contiguous(), *t[1:], workspace=ws))
         err = _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16"))
         assert err < BF16_TOL, (T, err)
-        gen += 4 if T <= GEMV_LAYER_MAX_T else 5   # GEMV layer: 4 barriers, MFMA layer: 5
+        gen += 4 if T <= GEMV_LAYER_MAX_T else 3   # GEMV layer: 4 barriers, MFMA layer: 3
         assert _barrier_state(ws) == (gen, 0), T
+        assert not any(_tile_counters(ws)), T
 
 
 @pytest.mark.parametrize("T", [1, 2, 3, 4])
