@@ -355,7 +355,7 @@ struct Tune {
   bool big = true;    // large-tile path enabled
   bool dlayer = true; // persistent decode layer enabled
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
-  int gvmax = 4;       // highest T for the streaming-GEMV decode layer (0: off)
+  int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
   int nw = 8;          // waves per block of the fn-8 X.U and XU.V stages (8, or 4: faster in isolation, not in the layer)
 };
@@ -592,10 +592,10 @@ bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, 
 // The persistent decode layer takes bf16 activations and factors in natural
 // layout, T <= 64, ranks and d multiples of 128 and ff a multiple of 64 (its
 // tiles), every operand below 2 GB (32-bit buffer offsets).
-// Below kDlMinT tokens the per-stage decode kernels beat this MFMA layer
-// (measured on MI355X, 8B shape: T=1 77 us vs 88 us; T=8 120 vs 95; T=64
-// 539 vs 250); the streaming-GEMV layer, tried first, takes 1 <= T <= 4.
-constexpr int64_t kDlMinT = 4;
+// It beats the per-stage decode kernels at every T (measured on MI355X, 8B
+// shape: T=1 83 us vs 88 us; T=8 82 vs 95; T=64 118 vs 250); the
+// streaming-GEMV layer, tried first, takes 1 <= T <= kGvMaxT.
+constexpr int64_t kDlMinT = 1;
 
 bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
                      bool vec) {

@@ -1,4 +1,4 @@
-// Launcher of the streaming-GEMV decode layer (1..4 tokens).  Grid = CU
+// Launcher of the streaming-GEMV decode layer (1 or 2 tokens).  Grid = CU
 // count, one block per CU, plain launch; the grid barriers' polls are
 // bounded, as in the MFMA decode layer.
 #include "decode_gemv.hpp"
@@ -19,8 +19,6 @@ hipError_t go_t(const GvParams& p, int grid, hipStream_t st) {
   switch (p.T) {
     case 1: return go<1, RW>(p, grid, st);
     case 2: return go<2, RW>(p, grid, st);
-    case 3: return go<3, RW>(p, grid, st);
-    case 4: return go<4, RW>(p, grid, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -37,8 +35,8 @@ int gemv_layer_grid(int rw) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  const void* k = rw == 1 ? reinterpret_cast<const void*>(&gemv_layer_kernel<4, 1>)
-                          : reinterpret_cast<const void*>(&gemv_layer_kernel<4, 2>);
+  const void* k = rw == 1 ? reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 1>)
+                          : reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 2>);
   return resident(k) >= 1 ? cus : 0;
 }
 

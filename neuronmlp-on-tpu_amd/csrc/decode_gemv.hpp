@@ -1,7 +1,7 @@
-// The SVD-MLP layer at 1..4 tokens as four weight-streaming GEMV phases in
+// The SVD-MLP layer at 1 or 2 tokens as four weight-streaming GEMV phases in
 // one persistent launch.
 //
-// At T <= 4 every factor element is used at most four times, so the layer is
+// At T <= 2 every factor element is used at most twice, so the layer is
 // a pure stream of the 311 MB of bf16 factors (LLaMA3-8B, r = 2816) and the
 // arithmetic is a few VALU FMAs per element.  The design keeps HBM busy:
 //  * one block of 8 waves per CU (grid = CU count);
@@ -52,7 +52,9 @@ struct GvParams {
 
 constexpr int kGvThreads = 512;
 constexpr int kGvDepth = 16;             // 16-byte loads in flight per lane
-constexpr int kGvMaxT = 4;
+// Highest token count: above it the MFMA decode layer is faster (8B layer on
+// MI355X: 78 / 81 / 86 / 87 us here at T = 1..4, 83 us there for each).
+constexpr int kGvMaxT = 2;
 constexpr int kGvAFloats = 12 * 1024;    // activation slice capacity (floats)
 
 // Phase geometry: Y_m += A_m . W_m (m < nm), W_m of K x N, natural layout.
