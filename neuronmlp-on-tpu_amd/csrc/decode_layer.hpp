@@ -88,11 +88,18 @@ constexpr int kDlFlag = kDlGen + kDlLine;
 // barrier counters: the last of every G arrivals finishes the launch).
 constexpr int kGvDone = kDlFlag + kDlLine;
 // 32-bit arrival counters of the split-K tiles of phases 1, 3 and 4 (in
-// that order) fill the rest of the 4 KB area.  The last arrival of a launch
-// resets its tile's counter to zero.
+// that order) fill the rest of the 4 KB area, kDlTileLines 128-byte lines.
+// Tile t's counter is word t / kDlTileLines of line t % kDlTileLines, so
+// neighbouring tiles, whose units finish together, hit different lines
+// (packed consecutively, ~100 blocks' atomics on 3 lines cost ~2 us per
+// layer).  The last arrival of a launch resets its tile's counter to zero.
 constexpr int kDlTileWords = kGvDone + kDlLine;
-constexpr int kDlMaxTiles = (512 - kDlTileWords) * 2;
+constexpr int kDlTileLines = (512 - kDlTileWords) / kDlLine;
+constexpr int kDlMaxTiles = kDlTileLines * 32;
 constexpr int kDlSyncBytes = kDlTileWords * 8 + kDlMaxTiles * 4;
+__device__ __forceinline__ uint32_t* dl_tile_counter(uint64_t* sync, int t) {
+  return reinterpret_cast<uint32_t*>(sync + kDlTileWords) + (t % kDlTileLines) * 32 + t / kDlTileLines;
+}
 
 // Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
 // weight bytes per block barrier) and the ring holds NS stages, as far as
@@ -332,7 +339,7 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
 //  * otherwise the unit stores its rows < T as slice u (16 bytes per lane
 //    and block mt, in register order) and, once every wave's stores have
 //    completed, counts its arrival on the tile's counter; the block that
-//    completes the count adds the other splits' slices to its registers (four
+//    completes the count adds the other splits' slices to its registers (eight
 //    slices in flight at a time), resets the counter and rounds to dst.
 // Units of a split phase never exceed the grid (at most one per block).
 template <int MT>
@@ -358,10 +365,10 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
     dl_block_sync();
     if (!*flag) return;
     const int split = u / nt, tile = u - split * nt;
-    for (int s0 = 0; s0 < splits; s0 += 4) {
-      u32x2 v[4][MT][2];
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+      u32x2 v[8][MT][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 8; ++i) {
         const int s = s0 + i;
         const float* o = slices + (int64_t)(tile + s * nt) * MT * 2048 + 4 * threadIdx.x;
 #pragma unroll
@@ -372,7 +379,7 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[mt].x += __uint_as_float(v[i][mt][0].x);
@@ -404,7 +411,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   c.lg = c.lane >> 4;
   c.T = p.T;
   int* const flag = reinterpret_cast<int*>(lds + L::FLAG_OFF);
-  uint32_t* const tiles = reinterpret_cast<uint32_t*>(p.sync + kDlTileWords);
   const int G = gridDim.x, b = blockIdx.x;
   const int T = p.T;
   constexpr int NS = L::NS;
@@ -496,7 +502,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(1, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, false, acc);
-    dl_combine<MT>(c, U, acc, u, nt1, p.splits1, tiles + u % nt1, p.slices, flag, U.dst);
+    dl_combine<MT>(c, U, acc, u, nt1, p.splits1, dl_tile_counter(p.sync, u % nt1), p.slices, flag, U.dst);
   }
   dl_wait_vm<0>();
   prefetch(2);
@@ -540,7 +546,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(3, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt3, p.splits3, tiles + nt1 + u % nt3, p.slices, flag, U.dst);
+    dl_combine<MT>(c, U, acc, u, nt3, p.splits3, dl_tile_counter(p.sync, nt1 + u % nt3), p.slices, flag, U.dst);
   }
   dl_wait_vm<0>();
   prefetch(4);
@@ -552,7 +558,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(4, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt4, p.splits4, tiles + nt1 + nt3 + u % nt4, p.slices, flag, U.dst);
+    dl_combine<MT>(c, U, acc, u, nt4, p.splits4, dl_tile_counter(p.sync, nt1 + nt3 + u % nt4), p.slices, flag, U.dst);
   }
 }
 
