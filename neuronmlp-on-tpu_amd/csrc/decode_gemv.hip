@@ -1,6 +1,10 @@
 // Launcher of the streaming-GEMV decode layer (1 or 2 tokens).  Grid = CU
-// count, one block per CU, plain launch; the grid barriers' polls are
-// bounded, as in the MFMA decode layer.
+// count (at most kDlMaxGrid, the MFMA decode layer's grid: both layers share
+// the workspace's barrier counters, which need one grid size), one block per
+// CU, plain launch; the grid barriers' polls are bounded, as in the MFMA
+// decode layer.
+#include <algorithm>
+
 #include "decode_gemv.hpp"
 #include "dispatch.hpp"
 
@@ -37,7 +41,7 @@ int gemv_layer_grid(int rw) {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   const void* k = rw == 1 ? reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 1>)
                           : reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 2>);
-  return resident(k) >= 1 ? cus : 0;
+  return resident(k) >= 1 ? std::min(cus, kDlMaxGrid) : 0;
 }
 
 int gemv_layer_a_floats() { return kGvAFloats; }

@@ -443,6 +443,25 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   constexpr bool FRAG = C::EPI == BEPI_STORE_FRAG;
   // fragment-order element offset of this lane's block (0, 0)
   const int64_t frag0 = ((((int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN)) * NW + wave) * FM * FN) * 256 + 4 * lane;
+  // SwiGLU: every gate value of the wave's tile is loaded before the first
+  // h store (the stores could alias the loads as far as the compiler knows,
+  // which would serialise one load round trip per fragment); the main
+  // loop's fragment registers are free by now.
+  u32x2 gv[C::EPI == BEPI_SWIGLU_MEM ? FM : 1][C::EPI == BEPI_SWIGLU_MEM ? FN : 1];
+  if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm0 + 16 * i + lr;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn0 + 16 * j + 4 * lg;
+        const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
+        gv[i][j] = (m < p.M && n < p.N)
+                       ? *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (int64_t)m * p.ldo + n))
+                       : u32x2{0u, 0u};
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm0 + 16 * i + lr;
@@ -470,7 +489,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       } else if constexpr (C::OUT_F32) {
         *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + o) = v;
       } else if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
-        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : o));
+        const u32x2 g = gv[i][j];
         const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
         const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
         *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) =
