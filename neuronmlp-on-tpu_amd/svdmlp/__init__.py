@@ -14,6 +14,12 @@ Host package over libsvdmlp.so (hand-written HIP kernels for gfx950):
 * :mod:`svdmlp.checkpoint` -- SVD factors from sharded safetensors checkpoints
   (models/hf_svd.py), and :mod:`svdmlp.checkpoint_speedup`, the per-layer
   real-checkpoint runner (bench/checkpoint_speedup.py).
+* :mod:`svdmlp.pallas_ops` -- the pallas_ops operator names and keywords of
+  the reference's benches (``svd_mlp``, ``fused_gate_up``, ``xuv_matmul``,
+  ``dense_mlp``, ``contracted_svd_mlp``).
+* :mod:`svdmlp.speedup` -- the three-way fused / dense / unfused benchmark
+  (test_speedup.py's synthetic branch); :mod:`svdmlp.e2e_block` -- the
+  N-layer transformer prefill with attention (bench/e2e_block.py).
 """
 
 from ._lib import SvdMlpError, load, version, workspace_bytes  # noqa: F401

@@ -12,7 +12,10 @@ Drop-in names and argument meanings for the SVD-MLP path:
            down_v_proj, down_u_proj, ...)          :658-666 (PyTorch layouts)
     get_fused_mlp_up_T_params(S), get_fused_three_mm_XTUV_params(S) :169-191
     jax_low_rank_down(hidden_t, u_down, v_down)     :618-628 (vendor down)
+    nki_matmul_fully_optimized_(lhsT, rhs, ...)     :545-615 (plain matmul, lhsT.T . rhs)
+    nki_baseline(x, up_proj, gate_proj, down_proj)  :669-678 (dense arm)
     _unfused_reference / _unfused_low_rank          :681-696 (comparison arms)
+    _unfused_low_rank_pallas                        :699-735 (unfused arm on the plain matmul)
 
 Block parameters (``*_tiles_in_block``) describe the TPU kernels' VMEM
 blocking.  They are validated exactly as the reference does -- positive
@@ -242,6 +245,62 @@ def _unfused_low_rank(x, u_up, v_up, u_gate, v_gate, u_down, v_down):
     return (hidden @ u_down) @ v_down
 
 
+def nki_matmul_fully_optimized_(lhsT, rhs, TILES_IN_BLOCK_M=2, TILES_IN_BLOCK_N=2, TILES_IN_BLOCK_K=4, *,
+                                mixed_precision=True, interpret=False):
+    """The reference's plain matmul kernel (test_speedup.py:545-615):
+    lhsT (K, M), rhs (K, N) -> (M, N) = lhsT^T . rhs at the input dtype.
+
+    It is the building block of the dense and unfused comparison arms, not of
+    the SVD-MLP path, so it runs on the vendor library (hipBLASLt via torch;
+    the transposed operand is made contiguous first).  The validation and
+    the VMEM estimate follow the reference, so the same shapes raise."""
+    ops.validate_arrays(lhsT, rhs)
+    K, M = lhsT.shape
+    if rhs.shape[0] != K:
+        raise ValueError("lhsT and rhs must have the same contraction dimension")
+    N = rhs.shape[1]
+    for name, value in zip(("TILES_IN_BLOCK_M", "TILES_IN_BLOCK_N", "TILES_IN_BLOCK_K"),
+                           (TILES_IN_BLOCK_M, TILES_IN_BLOCK_N, TILES_IN_BLOCK_K)):
+        _positive(name, value)
+    TILE_M, TILE_K, TILE_N = K_TILE, M_TILE, N_TILE
+    BLOCK_M, BLOCK_K, BLOCK_N = TILE_M * TILES_IN_BLOCK_M, TILE_K * TILES_IN_BLOCK_K, TILE_N * TILES_IN_BLOCK_N
+    Mp = _round_up(M, BLOCK_M)
+    itemsize = _ITEMSIZE[lhsT.dtype]
+    _check_vmem((Mp * BLOCK_N + BLOCK_K * BLOCK_N + BLOCK_K * BLOCK_M + TILE_M * BLOCK_N) * itemsize
+                + TILE_M * TILE_N * 8)
+    _no_interpret(interpret)
+    if lhsT.device.type != "cuda":
+        raise ValueError(f"the matmul arm runs on a ROCm GPU; got tensors on {lhsT.device}")
+    return lhsT.t().contiguous() @ rhs
+
+
+def nki_baseline(x, up_proj, gate_proj, down_proj, *, mixed_precision=True, interpret=False,
+                 matmul_params=None):
+    """Dense SwiGLU comparison arm with ``Linear.weight`` layouts (out, in)
+    (test_speedup.py:669-678): silu(x.Wg) * (x.Wu), then .Wd, with the SiLU
+    product in fp32 rounded to x.dtype."""
+    params = {} if matmul_params is None else matmul_params
+    up = nki_matmul_fully_optimized_(x.t(), up_proj.t(), **params, mixed_precision=mixed_precision,
+                                     interpret=interpret)
+    gate = nki_matmul_fully_optimized_(x.t(), gate_proj.t(), **params, mixed_precision=mixed_precision,
+                                       interpret=interpret)
+    act = torch.nn.functional.silu(gate.float()).to(x.dtype) * up
+    return nki_matmul_fully_optimized_(act.t(), down_proj.t(), **params, mixed_precision=mixed_precision,
+                                       interpret=interpret)
+
+
+def _unfused_low_rank_pallas(x, u_up, v_up, u_gate, v_gate, u_down, v_down, *, mixed_precision=True,
+                             interpret=False):
+    """Unfused low-rank arm on the same plain matmul as the dense arm
+    (test_speedup.py:699-735): six GEMMs, SiLU in fp32 rounded to x.dtype."""
+    mm = lambda a, b: nki_matmul_fully_optimized_(a, b, mixed_precision=mixed_precision,  # noqa: E731
+                                                  interpret=interpret)
+    gate = mm(mm(x.t(), u_gate).t(), v_gate)
+    up = mm(mm(x.t(), u_up).t(), v_up)
+    hidden = torch.nn.functional.silu(gate.float()).to(x.dtype) * up
+    return mm(mm(hidden.t(), u_down).t(), v_down)
+
+
 def relative_l2(got, expected) -> float:
     """test_speedup.py:854 / bench/speedup.py:113-119."""
     g = got.float()
@@ -258,5 +317,6 @@ def tflops(T: int, d: int, ff: int, r: int, r_down: int | None = None) -> float:
 __all__ = [
     "M_TILE", "R_TILE", "K_TILE", "N_TILE", "VMEM_LIMIT", "VMEM_HEADROOM", "FusionShape",
     "get_fused_mlp_up_T_params", "get_fused_three_mm_XTUV_params", "fused_mlp_up_T", "fused_three_mm_XTUV",
-    "jax_low_rank_down", "svd_mlp_with_fused_kernel", "nki_mm", "relative_l2", "tflops",
+    "jax_low_rank_down", "svd_mlp_with_fused_kernel", "nki_mm", "nki_matmul_fully_optimized_", "nki_baseline",
+    "relative_l2", "tflops",
 ]
