@@ -33,6 +33,10 @@ using namespace svdmlp;
 namespace {
 
 constexpr int64_t kDecodeMaxT = 64;
+// Largest T of the persistent MFMA decode layer (token tiles up to 128 rows):
+// at the 8B shape it takes 164 us at T=128 against 221 us for the
+// large-tile path, whose XU.V stages have only T/256 x ff/224 blocks there.
+constexpr int64_t kDlMaxT = 128;
 constexpr int kTargetBlocks = 384;  // ~1.5 blocks per CU on 256 CUs
 
 thread_local std::string g_err;
@@ -196,7 +200,7 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   w.xu32 = off;
   off += a256(3 * T * r * 4);
   w.gu32 = off;
-  off += dec ? a256(2 * T * big * 4) : 0;
+  off += T <= kDlMaxT ? a256(2 * T * big * 4) : 0;
   w.h = off;
   off += a256(T * big * 4);
   w.y32 = off;
@@ -211,7 +215,7 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   w.g = off;
   off += dec ? 0 : a256(((T + 255) / 256 * 256) * std::max((big + 223) / 224 * 224, (big + 255) / 256 * 256) * 2);
   w.slices = off;
-  off += dec ? a256((int64_t)kDlMaxGrid * decode_layer_mt((int)T) * 2048 * 4) : 0;
+  off += T <= kDlMaxT ? a256((int64_t)kDlMaxGrid * decode_layer_mt((int)T) * 2048 * 4) : 0;
   w.total = off;
   return w;
 }
@@ -590,8 +594,8 @@ bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, 
 }
 
 // The persistent decode layer takes bf16 activations and factors in natural
-// layout, T <= 64, ranks and d multiples of 128 and ff a multiple of 64 (its
-// tiles), every operand below 2 GB (32-bit buffer offsets).
+// layout, T <= kDlMaxT, ranks and d multiples of 128 and ff a multiple of 64
+// (its tiles), every operand below 2 GB (32-bit buffer offsets).
 // It beats the per-stage decode kernels at every T (measured on MI355X, 8B
 // shape: T=1 83 us vs 88 us; T=8 82 vs 95; T=64 118 vs 250); the
 // streaming-GEMV layer, tried first, takes 1 <= T <= kGvMaxT.
@@ -599,7 +603,7 @@ constexpr int64_t kDlMinT = 1;
 
 bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
                      bool vec) {
-  if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T > kDecodeMaxT || !tune().dlayer) return false;
+  if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T > kDlMaxT || !tune().dlayer) return false;
   if (T < std::min<int64_t>(kDlMinT, tune().dlmin)) return false;
   if (d % 128 || r_gu % 128 || r_d % 128 || ff % 64) return false;
   // one counter per split-K tile of phases 1, 3 and 4; the bf16 XU_d
@@ -980,7 +984,7 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
     float* y32 = reinterpret_cast<float*>(ws + L.y32);
     {
       StageScope z(ST_ZERO, c.st);
-      rc = check(launch_fill_zero(xu32, (int64_t)(L.total - L.xu32) / 4, c.st), "zero accumulators");
+      rc = check(launch_fill_zero(xu32, (int64_t)(L.part - L.xu32) / 4, c.st), "zero accumulators");
     }
     if (rc) return rc;
     const Operand ax{x, nullptr, d};

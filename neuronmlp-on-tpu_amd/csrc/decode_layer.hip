@@ -32,13 +32,14 @@ int blocks_per_cu() {
 
 }  // namespace
 
-int decode_layer_mt(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
+int decode_layer_mt(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : (T <= 64 ? 4 : 8)); }
 
 int decode_layer_grid(int mt) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  const int per = mt == 1 ? blocks_per_cu<1>() : (mt == 2 ? blocks_per_cu<2>() : blocks_per_cu<4>());
+  const int per = mt == 1 ? blocks_per_cu<1>()
+                  : (mt == 2 ? blocks_per_cu<2>() : (mt == 4 ? blocks_per_cu<4>() : blocks_per_cu<8>()));
   return per >= 1 ? std::min(cus, kDlMaxGrid) : 0;
 }
 
@@ -54,6 +55,8 @@ hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStr
     e = coop<2>(p, grid, st);
   else if (mt == 4)
     e = coop<4>(p, grid, st);
+  else if (mt == 8)
+    e = coop<8>(p, grid, st);
   else {
     *why = "decode layer: no instance for this token count";
     return hipErrorInvalidValue;

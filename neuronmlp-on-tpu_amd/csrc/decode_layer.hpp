@@ -1,4 +1,4 @@
-// The whole SVD-MLP layer at decode shapes (T <= 64 tokens) in one
+// The whole SVD-MLP layer at decode shapes (T <= 128 tokens) in one
 // persistent launch (a plain launch of one block per CU; see the launcher).
 //
 // At these shapes the layer is a stream of 311 MB of bf16 factors (LLaMA3-8B,
@@ -106,8 +106,8 @@ __device__ __forceinline__ uint32_t* dl_tile_counter(uint64_t* sync, int t) {
 // the activation tile, which shares the ring, leaves room.
 template <int MT>
 struct DlDepth {
-  static constexpr int KC = MT == 4 ? 1 : 2;
-  static constexpr int NS = MT == 2 ? 4 : 6;
+  static constexpr int KC = MT >= 4 ? 1 : 2;
+  static constexpr int NS = MT == 2 || MT == 8 ? 4 : 6;
 };
 
 template <int N>
@@ -365,10 +365,11 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
     dl_block_sync();
     if (!*flag) return;
     const int split = u / nt, tile = u - split * nt;
-    for (int s0 = 0; s0 < splits; s0 += 8) {
-      u32x2 v[8][MT][2];
+    constexpr int SB = MT >= 8 ? 2 : 8;  // slices in flight (registers: SB * MT * 4)
+    for (int s0 = 0; s0 < splits; s0 += SB) {
+      u32x2 v[SB][MT][2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < SB; ++i) {
         const int s = s0 + i;
         const float* o = slices + (int64_t)(tile + s * nt) * MT * 2048 + 4 * threadIdx.x;
 #pragma unroll
@@ -379,7 +380,7 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
         }
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < SB; ++i)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[mt].x += __uint_as_float(v[i][mt][0].x);

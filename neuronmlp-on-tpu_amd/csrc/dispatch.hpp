@@ -58,12 +58,13 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 hipError_t launch_rmsnorm(const void* x, const float* gain, void* y, int64_t T, int64_t d, float eps, bool bf16,
                           hipStream_t st);
 hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hipStream_t st);
-// Persistent decode layer (T <= 64): token tiles of 16 rows (1, 2 or 4),
-// grid = CU count when the kernel fits one block per CU, else 0.
+// Persistent decode layer (T <= 128): token tiles of 16 * MT rows (MT = 1,
+// 2, 4 or 8), grid = CU count (at most kDlMaxGrid) when the kernel fits one
+// block per CU, else 0.
 int decode_layer_mt(int T);
 int decode_layer_grid(int mt);
 hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why);
-// Streaming-GEMV decode layer (T <= 4): rows per wave load rw (1 or 2),
+// Streaming-GEMV decode layer (T <= 2): rows per wave load rw (1 or 2),
 // grid = CU count when the kernel fits one block per CU, else 0.
 struct GvParams;
 int gemv_layer_grid(int rw);

@@ -163,7 +163,7 @@ def test_8b_prefill_T1024_row_subset(gpu, layer8b):
     assert err_h < BF16_TOL, err_h
 
 
-@pytest.mark.parametrize("T", [1, 2, 4, 8, 32, 64])
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 32, 64, 65, 128])
 def test_8b_decode(gpu, layer8b, T):
     shape, f, ft = layer8b
     x = _x(T, shape.d, 100 + T)
@@ -211,7 +211,7 @@ def _tile_counters(ws):
 
 
 @pytest.mark.parametrize("shape,Ts", [
-    (inputs.LayerShape(1024, 2048, 512), (1, 3, 2, 17, 40, 64, 16)),   # every token-tile count, reused workspace
+    (inputs.LayerShape(1024, 2048, 512), (1, 3, 2, 17, 40, 64, 100, 16, 128)),  # every token-tile count, reused workspace
     (inputs.LayerShape(1024, 32768, 256), (5, 33)),                     # 512 column tiles: two units per block
     (inputs.LayerShape(16640, 1024, 128), (8, 64)),                     # 130 output tiles: phase 4 unsplit
 ])
@@ -255,15 +255,18 @@ def test_gemv_decode_layer_ragged_strips(gpu, T):
 
 
 def test_decode_and_prefill_paths_agree(gpu, layer8b):
-    """T=64 runs the decode kernels, T=128 the tiled GEMMs; the first 64 rows
-    of the two must agree with each other and with the oracle."""
+    """T=64 and T=128 run the persistent decode layer (16- and 128-row token
+    tiles), T=256 the tiled GEMMs; the first 64 rows of the three must agree
+    with each other and with the oracle."""
     shape, f, ft = layer8b
-    x = _x(128, shape.d, 7)
-    y128 = _np(ops.svd_mlp(_to(x, torch.bfloat16, gpu), *ft))
+    x = _x(256, shape.d, 7)
+    y256 = _np(ops.svd_mlp(_to(x, torch.bfloat16, gpu), *ft))
+    y128 = _np(ops.svd_mlp(_to(x[:128], torch.bfloat16, gpu), *ft))
     y64 = _np(ops.svd_mlp(_to(x[:64], torch.bfloat16, gpu), *ft))
     ref = O.svd_mlp_ref(x[:64], *f, dtype="bfloat16")
-    assert _rel(y64, ref) < BF16_TOL and _rel(y128[:64], ref) < BF16_TOL
-    assert _rel(y64, y128[:64]) < 5e-3
+    for y in (y64, y128[:64], y256[:64]):
+        assert _rel(y, ref) < BF16_TOL
+    assert _rel(y64, y256[:64]) < 5e-3 and _rel(y128[:64], y256[:64]) < 5e-3
 
 
 def test_linear_layout_weights_bf16(gpu, layer8b):
