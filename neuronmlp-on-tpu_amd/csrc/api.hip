@@ -354,7 +354,7 @@ int prefill_v(const Common& c, int a_src, const void* xu, const void* v, const f
 struct Tune {
   int s1 = 8;         // X.U stages: block tile 256 x 32*s1
   int s4 = 8;         // XU.V of the down half: 256 x 32*s4 (8: split-K over r)
-  int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 7 when ff % 224 == 0)
+  int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 4 for T <= 512, else 7 when ff % 224 == 0)
   int split = 256;    // CUs assumed by the split-K planner
   bool big = true;    // large-tile path enabled
   bool dlayer = true; // persistent decode layer enabled
@@ -521,7 +521,11 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
                bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, const float* s_vg = nullptr,
                const float* s_vu = nullptr) {
   int fn = tune().s2fn;
-  if (fn == 0) fn = (ff % 224 == 0) ? 7 : 8;
+  // 256 x 224 tiles (fn 7) leave most CUs idle at one or two 256-row tiles
+  // of tokens; 256 x 128 tiles (fn 4) double the block count there (8B
+  // layer: T=256 268 -> 245 us, T=512 298 -> 288 us; from three row tiles on
+  // fn 7 is faster: T=768 349 vs 428 us).
+  if (fn == 0) fn = (T <= 512 && ff % 128 == 0) ? 4 : ((ff % 224 == 0) ? 7 : 8);
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * ff * wbytes(c);
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r,
                     1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);

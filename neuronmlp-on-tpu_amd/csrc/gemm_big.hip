@@ -35,11 +35,9 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
       }
       return go_b<FN, BEPI_STORE>(d, p, splits, batch, st);
     case BEPI_SWIGLU_MEM:
-      if constexpr (FN != 4) return go_b<FN, BEPI_SWIGLU_MEM>(d, p, splits, batch, st);
-      break;
+      return go_b<FN, BEPI_SWIGLU_MEM>(d, p, splits, batch, st);
     case BEPI_STORE_FRAG:
-      if constexpr (FN != 4) return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
-      break;
+      return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
     default: break;
   }
   *why = "big GEMM: unsupported epilogue for this tile";
