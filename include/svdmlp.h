@@ -126,6 +126,32 @@ int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const vo
                          void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * svdmlp_svd_mlp and svdmlp_svd_mlp_block for factors whose rows are padded
+ * (no counterpart in the reference, whose operators take dense arrays; the
+ * math is that of kernels/reference.py:85-93).  ld holds the leading
+ * dimension (elements between consecutive rows as stored) of ug, vg, uu, vu,
+ * ud, vd in that order; 0 or a NULL ld means the row length.  Padded factors
+ * must be bf16, natural layout, 16-byte aligned, with leading dimensions
+ * that are multiples of 8 and equal for gate and up.  With row pitches that
+ * are multiples of 4 KB (V rows of 4096 or 14336 bf16 elements), each column
+ * stripe of a factor maps onto a fixed subset of HBM channels, and at
+ * decode shapes the slowest such subset bounds the weight stream; padding
+ * V rows by 64 elements spreads every stripe over all channels (8B layer at
+ * 8 tokens: 80 -> 73 us).  Shapes that only other kernels take (fp32, fp8,
+ * Linear layout, odd sizes) return SVDMLP_EINVAL with padded factors.
+ */
+int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                      const void* ud, const void* vd, const float* const* scales /* 6 or NULL */,
+                      const int64_t* ld /* 6 or NULL */, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu,
+                      int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags, void* workspace,
+                      size_t ws_bytes, void* stream);
+int svdmlp_svd_mlp_block_ld(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
+                            const void* uu, const void* vu, const void* ud, const void* vd,
+                            const float* const* scales /* 6 or NULL */, const int64_t* ld /* 6 or NULL */, void* y,
+                            int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
+                            int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * Per-stage GPU timing (no counterpart in the reference, whose timing is host
  * wall clock around block_until_ready, test_speedup.py:739-749).  While
  * enabled, every stage launch of the calls above is bracketed by hipEvents

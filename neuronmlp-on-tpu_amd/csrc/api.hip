@@ -490,25 +490,37 @@ int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
   return (int)((K + ks - 1) / ks);
 }
 
+// Row pitch (elements) of the factors as stored, natural layout: ug and uu
+// share one, vg and vu one, then ud and vd.  Dense factors have the row
+// length as pitch.
+struct FactorLd {
+  int64_t u, v, ud, vd;
+  bool dense;
+};
+
+FactorLd dense_ld(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d) { return FactorLd{r_gu, ff, r_d, d, true}; }
+
 // XU_b = A . U_b (b < batch) into bf16 ws.xu_bf16, batch stride T*r.  With
 // too few output tiles for the chip, K is split: each split writes an fp32
 // slice (plain stores) and one pass sums the slices in order into bf16.
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
-           int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr) {
+           int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr,
+           int64_t ldu = 0) {
   const int fn = tune().s1;
   const int ks = plan_ksplit(T, K, r, fn, batch);
   const int splits = (K + ks - 1) / ks;
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
-  const int64_t u_bytes = (int64_t)K * r * wbytes(c);
+  const int64_t ldb = u_lin ? K : (ldu ? ldu : r);  // natural U may carry padded rows
+  const int64_t u_bytes = (int64_t)(u_lin ? r : K) * ldb * wbytes(c);
   const void* u1 = batch > 1 ? u[1] : u[0];
   const float* s0 = su ? su[0] : nullptr;
   const float* s1 = su && batch > 1 ? su[1] : s0;
   if (splits == 1)
-    return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, u_lin ? K : r, u_bytes, u_lin, T, r, K, batch, fn,
+    return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
                     BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1);
   float* part = reinterpret_cast<float*>(ws + L.part);
   const int64_t slice = (int64_t)batch * T * r;
-  int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, u_lin ? K : r, u_bytes, u_lin, T, r, K, batch, fn,
+  int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
                     BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice, s0, s1);
   if (rc) return rc;
   StageScope fin(ST_FINALIZE, c.st);
@@ -519,34 +531,36 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
 // u pass whose epilogue applies SiLU(g) * u.
 int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, const void* vg, const void* vu,
                bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, const float* s_vg = nullptr,
-               const float* s_vu = nullptr) {
+               const float* s_vu = nullptr, int64_t ldv = 0) {
   int fn = tune().s2fn;
   // 256 x 224 tiles (fn 7) leave most CUs idle at one or two 256-row tiles
   // of tokens; 256 x 128 tiles (fn 4) double the block count there (8B
   // layer: T=256 268 -> 245 us, T=512 298 -> 288 us; from three row tiles on
   // fn 7 is faster: T=768 349 vs 428 us).
   if (fn == 0) fn = (T <= 512 && ff % 128 == 0) ? 4 : ((ff % 224 == 0) ? 7 : 8);
-  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * ff * wbytes(c);
-  int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r,
+  const int64_t ldb = v_lin ? r : (ldv ? ldv : ff);
+  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? ff : r) * ldb * wbytes(c);
+  int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,
                     1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
   if (rc) return rc;
-  return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, v_lin ? r : ff, v_bytes, v_lin, T, ff, r, 1,
+  return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1,
                   fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1);
 }
 
 // y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
 int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T, int r, int dout, char* ws,
-          const Ws& L, void* y, const float* sv = nullptr) {
+          const Ws& L, void* y, const float* sv = nullptr, int64_t ldv = 0) {
   const int fn = tune().s4 > 0 ? tune().s4 : 8;
-  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)r * dout * wbytes(c);
+  const int64_t ldb = v_lin ? r : (ldv ? ldv : dout);
+  const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? dout : r) * ldb * wbytes(c);
   const int ks = tune().s4 > 0 && tune().s4 != 8 ? r : plan_ksplit(T, r, dout, fn, 1);
   const int splits = (r + ks - 1) / ks;
   if (splits == 1)
-    return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, v_lin ? r : dout, v_bytes, v_lin, T, dout, r, 1,
+    return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1,
                     fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv);
   float* part = reinterpret_cast<float*>(ws + L.part);
   const int64_t slice = (int64_t)T * dout;
-  int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, v_lin ? r : dout, v_bytes, v_lin, T, dout, r,
+  int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r,
                     1, fn, BEPI_STORE, ks, part, dout, 0, nullptr, true, slice, sv);
   if (rc) return rc;
   StageScope fin(ST_FINALIZE, c.st);
@@ -606,7 +620,7 @@ bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, 
 constexpr int64_t kDlMinT = 1;
 
 bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
-                     bool vec) {
+                     bool vec, const FactorLd& ld) {
   if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T > kDlMaxT || !tune().dlayer) return false;
   if (T < std::min<int64_t>(kDlMinT, tune().dlmin)) return false;
   if (d % 128 || r_gu % 128 || r_d % 128 || ff % 64) return false;
@@ -614,7 +628,8 @@ bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t 
   // lives in the decode-only gu32 region (2 T max(d, ff) fp32)
   if (2 * r_gu / 128 + r_d / 128 + d / 128 > kDlMaxTiles || r_d > 4 * std::max(d, ff)) return false;
   const int64_t lim = (int64_t)1 << 31;
-  for (int64_t bytes : {T * d * 2, d * r_gu * 2, r_gu * ff * 2, ff * r_d * 2, r_d * d * 2, T * ff * 2, 2 * T * r_gu * 4})
+  for (int64_t bytes : {T * d * 2, d * ld.u * 2, r_gu * ld.v * 2, ff * ld.ud * 2, r_d * ld.vd * 2, T * ff * 2,
+                        2 * T * r_gu * 4})
     if (bytes >= lim) return false;
   return decode_layer_grid(decode_layer_mt((int)T)) > 0;
 }
@@ -632,7 +647,7 @@ int dl_plan(int64_t K, int64_t tiles, int grid, int* units) {
 
 int decode_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
                  const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
-                 char* ws, const Ws& L) {
+                 char* ws, const Ws& L, const FactorLd& ld) {
   const int mt = decode_layer_mt((int)T);
   const int grid = decode_layer_grid(mt);
   DecLayerParams p{};
@@ -661,6 +676,10 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits1 = p.units1 / (int)(2 * r_gu / 128);
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
+  p.ld_u = (int)ld.u;
+  p.ld_v = (int)ld.v;
+  p.ld_ud = (int)ld.ud;
+  p.ld_vd = (int)ld.vd;
   const char* why = nullptr;
   StageScope ss(ST_DEC_LAYER, c.st);
   return check(launch_decode_layer(p, mt, grid, c.st, &why), "decode layer", why);
@@ -670,12 +689,12 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
 // layout, every K a multiple of the 16-row group, each factor below 2 GB and
 // each block's activation rows within the kernel's LDS slice.
 bool gemv_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
-                   bool vec) {
+                   bool vec, const FactorLd& ld) {
   const int rw = tune().gvrw == 1 ? 1 : 2;
   if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T < 1 || T > std::min(kGvMaxT, tune().gvmax)) return false;
   if (d % 16 || ff % 16 || r_gu % 16 || r_d % 16) return false;
   const int64_t lim = (int64_t)1 << 31;
-  for (int64_t bytes : {d * r_gu * 2, r_gu * ff * 2, ff * r_d * 2, r_d * d * 2})
+  for (int64_t bytes : {d * ld.u * 2, r_gu * ld.v * 2, ff * ld.ud * 2, r_d * ld.vd * 2})
     if (bytes >= lim) return false;
   const int grid = gemv_layer_grid(rw);
   if (grid <= 0) return false;
@@ -690,7 +709,7 @@ bool gemv_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_
 
 int gemv_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
                const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
-               char* ws, const Ws& L) {
+               char* ws, const Ws& L, const FactorLd& ld) {
   const int rw = tune().gvrw == 1 ? 1 : 2;
   GvParams p{};
   p.x = static_cast<const uint16_t*>(x);
@@ -711,6 +730,10 @@ int gemv_layer(const Common& c, const void* x, const void* ug, const void* vg, c
   p.ff = (int)ff;
   p.r_gu = (int)r_gu;
   p.r_d = (int)r_d;
+  p.ld_u = (int)ld.u;
+  p.ld_v = (int)ld.v;
+  p.ld_ud = (int)ld.ud;
+  p.ld_vd = (int)ld.vd;
   const char* why = nullptr;
   StageScope ss(ST_DEC_GEMV, c.st);
   return check(launch_gemv_layer(p, rw, gemv_layer_grid(rw), c.st, &why), "decode GEMV layer", why);
@@ -738,6 +761,15 @@ int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const vo
                          const void* uu, const void* vu, const void* ud, const void* vd, const float* const* scales,
                          void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
                          int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
+  return svdmlp_svd_mlp_block_ld(x, norm_w, eps, ug, vg, uu, vu, ud, vd, scales, nullptr, y, T, d, ff, r_gu, r_d,
+                                 act_dtype, w_dtype, flags, workspace, ws_bytes, stream);
+}
+
+int svdmlp_svd_mlp_block_ld(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
+                            const void* uu, const void* vu, const void* ud, const void* vd,
+                            const float* const* scales, const int64_t* ld, void* y, int64_t T, int64_t d, int64_t ff,
+                            int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                            void* workspace, size_t ws_bytes, void* stream) {
   g_err.clear();
   int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
   if (rc) return rc;
@@ -752,8 +784,8 @@ int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const vo
   hipStream_t st = (hipStream_t)stream;
   void* h = static_cast<char*>(workspace) + L.norm;
   if ((rc = check(launch_rmsnorm(x, norm_w, h, T, d, eps, bf16, st), "RMSNorm"))) return rc;
-  if ((rc = svdmlp_svd_mlp(h, ug, vg, uu, vu, ud, vd, scales, y, T, d, ff, r_gu, r_d, act_dtype, w_dtype, flags,
-                           workspace, ws_bytes, stream)))
+  if ((rc = svdmlp_svd_mlp_ld(h, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_gu, r_d, act_dtype, w_dtype,
+                              flags, workspace, ws_bytes, stream)))
     return rc;
   return check(launch_residual_add(x, y, T * d, bf16, st), "residual add");
 }
@@ -947,6 +979,14 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
                    const void* vd, const float* const* scales, void* y, int64_t T, int64_t d, int64_t ff,
                    int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags, void* workspace,
                    size_t ws_bytes, void* stream) {
+  return svdmlp_svd_mlp_ld(x, ug, vg, uu, vu, ud, vd, scales, nullptr, y, T, d, ff, r_gu, r_d, act_dtype, w_dtype, flags,
+                           workspace, ws_bytes, stream);
+}
+
+int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void* uu, const void* vu, const void* ud,
+                      const void* vd, const float* const* scales, const int64_t* ld_in, void* y, int64_t T, int64_t d,
+                      int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                      void* workspace, size_t ws_bytes, void* stream) {
   g_err.clear();
   int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
   if (rc) return rc;
@@ -968,15 +1008,40 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
   bool vec = d % 8 == 0 && ff % 8 == 0 && r_gu % 8 == 0 && r_d % 8 == 0;
   for (const void* q : {x, ug, vg, uu, vu, ud, vd, (const void*)y, (const void*)workspace}) vec = vec && aligned16(q);
   if (fp8 && !vec) return fail("fp8 weights need d, ff and ranks to be multiples of 8 and 16-byte aligned buffers");
+  FactorLd ld = dense_ld(d, ff, r_gu, r_d);
+  if (ld_in) {
+    const int64_t rows[6] = {r_gu, ff, r_gu, ff, r_d, d};  // row length of ug, vg, uu, vu, ud, vd
+    int64_t got[6];
+    for (int i = 0; i < 6; ++i) {
+      got[i] = ld_in[i] ? ld_in[i] : rows[i];
+      if (got[i] < rows[i])
+        return fail("leading dimension %lld of factor %d is below its row length %lld", (long long)got[i], i,
+                    (long long)rows[i]);
+      if (got[i] != rows[i]) ld.dense = false;
+    }
+    if (!ld.dense) {
+      if (fp8 || c.f32 || flags || !vec)
+        return fail("factors with padded rows need bf16 natural-layout factors, 16-byte aligned");
+      for (int i = 0; i < 6; ++i)
+        if (got[i] % 8) return fail("leading dimensions must be multiples of 8 elements (16-byte rows)");
+      if (got[0] != got[2] || got[1] != got[3]) return fail("gate and up factors must share their leading dimensions");
+      ld = FactorLd{got[0], got[1], got[4], got[5], false};
+    }
+  }
   char* ws = static_cast<char*>(workspace);
   const float* S[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (fp8)
     for (int i = 0; i < 6; ++i) S[i] = scales[i];
 
-  if (gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec))
-    return gemv_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L);
-  if (decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec))
-    return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L);
+  if (gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld))
+    return gemv_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld);
+  if (decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld))
+    return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld);
+  const bool big = big_ok(c, vec, {T * d * 2, d * ld.u * 2, r_gu * ld.v * 2, T * ff * 2, ff * ld.ud * 2, r_d * ld.vd * 2},
+                          {d, r_gu, ff, r_d});
+  if (!ld.dense && (T <= kDecodeMaxT || !big))
+    return fail("factors with padded rows: no kernel takes this shape (the decode layers need d, ranks and ff in "
+                "multiples of 128, 128 and 64, the large-tile path more than %lld tokens)", (long long)kDecodeMaxT);
 
   if (decode_ok(c, T, {d, ff, r_gu, r_d}, vec)) {
     float* xu32 = reinterpret_cast<float*>(ws + L.xu32);
@@ -1030,18 +1095,18 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
   }
 
   // Prefill: h stays in the workspace between the two halves.
-  if (big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2, ff * r * 2}, {d, r_gu, ff, r_d})) {
+  if (big) {
     const void* us[2] = {ug, uu};
     const float* sus[2] = {S[0], S[2]};
-    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L, sus))) return rc;
+    if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r_gu, 2, ws, L, sus, ld.u))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
-    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf, S[1], S[3]))) return rc;
+    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf, S[1], S[3], ld.v))) return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};
-    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud))) return rc;
-    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5]);
+    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) return rc;
+    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);
   }
 
   const Operand ax{x, nullptr, d};

@@ -48,6 +48,7 @@ struct GvParams {
   float* y32;      // (T, d)
   uint64_t* sync;  // barrier words (kDl* layout)
   int T, d, ff, r_gu, r_d;
+  int ld_u, ld_v, ld_ud, ld_vd;  // row pitch (elements) of ug and uu, vg and vu, ud, vd
 };
 
 constexpr int kGvThreads = 512;
@@ -63,7 +64,7 @@ struct GvPhase {
   const uint16_t* w1;
   float* o0;
   float* o1;
-  int K, N, S, KG, nm, groups;
+  int K, N, L, S, KG, nm, groups;  // L: row pitch of w0 and w1 (elements)
 };
 
 template <int RW>
@@ -72,12 +73,16 @@ __device__ __forceinline__ GvPhase gv_phase(const GvParams& p, int ph) {
   const int T = p.T;
   if (ph == 1) {
     P.w0 = p.ug; P.w1 = p.uu; P.o0 = p.xu32; P.o1 = p.xu32 + (int64_t)T * p.r_gu; P.K = p.d; P.N = p.r_gu; P.nm = 2;
+    P.L = p.ld_u;
   } else if (ph == 2) {
     P.w0 = p.vg; P.w1 = p.vu; P.o0 = p.gu32; P.o1 = p.gu32 + (int64_t)T * p.ff; P.K = p.r_gu; P.N = p.ff; P.nm = 2;
+    P.L = p.ld_v;
   } else if (ph == 3) {
     P.w0 = P.w1 = p.ud; P.o0 = P.o1 = p.xd32; P.K = p.ff; P.N = p.r_d; P.nm = 1;
+    P.L = p.ld_ud;
   } else {
     P.w0 = P.w1 = p.vd; P.o0 = P.o1 = p.y32; P.K = p.r_d; P.N = p.d; P.nm = 1;
+    P.L = p.ld_vd;
   }
   constexpr int STRIP = 512 / RW, GROUP = 8 * RW;
   P.S = (P.N + STRIP - 1) / STRIP;
@@ -157,10 +162,10 @@ __device__ __forceinline__ u32x4 gv_issue(const GvPhase& P, GvCursor& c, int lro
   constexpr int STRIP = 512 / RW, GROUP = 8 * RW;
   const bool live = c.left > 0;
   const uint16_t* w = c.mat ? P.w1 : P.w0;
-  const i32x4 rs = make_rsrc_sgpr(w, live ? (uint32_t)P.K * (uint32_t)P.N * 2u : 0u);
+  const i32x4 rs = make_rsrc_sgpr(w, live ? (uint32_t)P.K * (uint32_t)P.L * 2u : 0u);
   const int col = STRIP * c.s + lcol;
-  const uint32_t voff = col < P.N ? ((uint32_t)lrow * (uint32_t)P.N + (uint32_t)col) * 2u : kOOB;
-  const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(GROUP * c.kg) * (uint32_t)P.N * 2u));
+  const uint32_t voff = col < P.N ? ((uint32_t)lrow * (uint32_t)P.L + (uint32_t)col) * 2u : kOOB;
+  const uint32_t soff = (uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(GROUP * c.kg) * (uint32_t)P.L * 2u));
   const u32x4 v = gv_load(rs, voff, soff);
   if (live) {
     gv_advance(c, P);

@@ -69,6 +69,7 @@ struct DecLayerParams {
   int ks1, ks3, ks4;                   // K per split, phases 1, 3, 4 (multiples of 32)
   int units1, units2, units3, units4;  // tiles x splits
   int splits1, splits3, splits4;       // splits per tile, phases 1, 3 and 4
+  int ld_u, ld_v, ld_ud, ld_vd;        // row pitch (elements) of ug and uu, vg and vu, ud, vd
 };
 
 constexpr int kDlThreads = 512;
@@ -428,8 +429,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.lda = p.d;
       U.a_bytes = (uint32_t)((int64_t)T * p.d * 2);
       U.b0 = U.b1 = br ? p.uu : p.ug;
-      U.ldb = p.r_gu;
-      U.b_bytes = (uint32_t)((int64_t)p.d * p.r_gu * 2);
+      U.ldb = p.ld_u;
+      U.b_bytes = (uint32_t)((int64_t)p.d * p.ld_u * 2);
       U.n0 = (tile % per) * 128;
       U.kb = split * p.ks1;
       U.ke = min(p.d, U.kb + p.ks1);
@@ -442,8 +443,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.a_bytes = (uint32_t)((int64_t)T * p.r_gu * 2);
       U.b0 = p.vg;
       U.b1 = p.vu;
-      U.ldb = p.ff;
-      U.b_bytes = (uint32_t)((int64_t)p.r_gu * p.ff * 2);
+      U.ldb = p.ld_v;
+      U.b_bytes = (uint32_t)((int64_t)p.r_gu * p.ld_v * 2);
       U.n0 = u * 64;
       U.kb = 0;
       U.ke = p.r_gu;
@@ -456,8 +457,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.lda = p.ff;
       U.a_bytes = (uint32_t)((int64_t)T * p.ff * 2);
       U.b0 = U.b1 = p.ud;
-      U.ldb = p.r_d;
-      U.b_bytes = (uint32_t)((int64_t)p.ff * p.r_d * 2);
+      U.ldb = p.ld_ud;
+      U.b_bytes = (uint32_t)((int64_t)p.ff * p.ld_ud * 2);
       U.n0 = tile * 128;
       U.kb = split * p.ks3;
       U.ke = min(p.ff, U.kb + p.ks3);
@@ -470,8 +471,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.lda = p.r_d;
       U.a_bytes = (uint32_t)((int64_t)T * p.r_d * 2);
       U.b0 = U.b1 = p.vd;
-      U.ldb = p.d;
-      U.b_bytes = (uint32_t)((int64_t)p.r_d * p.d * 2);
+      U.ldb = p.ld_vd;
+      U.b_bytes = (uint32_t)((int64_t)p.r_d * p.ld_vd * 2);
       U.n0 = tile * 128;
       U.kb = split * p.ks4;
       U.ke = min(p.r_d, U.kb + p.ks4);

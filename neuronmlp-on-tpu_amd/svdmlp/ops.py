@@ -92,9 +92,10 @@ def _check_device(*tensors) -> torch.device:
 
 class _Factor:
     """A factor prepared for the C ABI: keeps the tensor alive, records the
-    layout (natural or Linear) and the fp8 scale."""
+    layout (natural or Linear), the row pitch of a row-padded natural-layout
+    view (``ld``, elements; 0 when dense) and the fp8 scale."""
 
-    __slots__ = ("tensor", "ptr", "linear", "scale", "scale_ptr", "rows", "cols")
+    __slots__ = ("tensor", "ptr", "linear", "scale", "scale_ptr", "rows", "cols", "ld")
 
     def __init__(self, f):
         if isinstance(f, QuantizedFactor):
@@ -109,15 +110,45 @@ class _Factor:
         else:
             t = f
             linear = False
+            self.ld = 0
             if not t.is_contiguous():
                 if t.t().is_contiguous():
                     linear = True
+                elif padded_rows(t):
+                    self.ld = int(t.stride(0))
                 else:
                     t = t.contiguous()
             self.tensor, self.linear = t, linear
             self.scale, self.scale_ptr = None, None
+        if isinstance(f, QuantizedFactor):
+            self.ld = 0
         self.ptr = self.tensor.data_ptr()
         self.rows, self.cols = int(f.shape[0]), int(f.shape[1])
+
+    def dense(self) -> None:
+        """Replace a row-padded view by a contiguous copy."""
+        if self.ld:
+            self.tensor, self.ld = self.tensor.contiguous(), 0
+            self.ptr = self.tensor.data_ptr()
+
+
+def padded_rows(t: torch.Tensor) -> bool:
+    """A natural-layout bf16 view whose rows are spaced wider than their
+    length (a column slice of a wider buffer), 16-byte aligned rows: the
+    layered entry points read it in place."""
+    return (t.dim() == 2 and t.dtype == torch.bfloat16 and t.stride(1) == 1 and t.stride(0) > t.shape[1]
+            and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0)
+
+
+def pad_rows(t: torch.Tensor, pad: int = 64) -> torch.Tensor:
+    """A copy of the 2-D tensor t whose rows are ``pad`` elements longer in
+    memory, returned as the (rows, cols) view: the row pitch that spreads a
+    factor's column stripes over all HBM channels (rows of 4096 or 14336
+    bf16 elements otherwise map each stripe onto a subset)."""
+    rows, cols = t.shape
+    buf = torch.zeros((rows, cols + pad), dtype=t.dtype, device=t.device)
+    buf[:, :cols] = t
+    return buf[:, :cols]
 
 
 def _w_code(x: torch.Tensor, factors) -> int:
@@ -146,7 +177,7 @@ def _uniform(factors, linear: bool) -> None:
             # A mix of layouts: give the odd one out the uniform layout.
             # f.tensor is always the logical (d_in, d_out) view.
             f.tensor = f.tensor.t().contiguous().t() if linear else f.tensor.contiguous()
-            f.linear = linear
+            f.linear, f.ld = linear, 0
             f.ptr = f.tensor.data_ptr()
 
 
@@ -181,6 +212,8 @@ def fused_gate_up(x, u_gate, v_gate, u_up, v_up, *, out_transposed: bool = False
     lib = _lib.load()
     x = _activation(x)
     ug, vg, uu, vu = (_Factor(f) for f in (u_gate, v_gate, u_up, v_up))
+    for f in (ug, vg, uu, vu):
+        f.dense()  # this entry point takes dense rows
     _uniform((ug, uu), ug.linear and uu.linear)
     _uniform((vg, vu), vg.linear and vu.linear)
     flags = _layout_flags((ug, uu), (vg, vu)) | (_lib.SVDMLP_OUT_T if out_transposed else 0)
@@ -211,6 +244,8 @@ def fused_xuv(x, u, v, *, x_transposed: bool = False) -> torch.Tensor:
     lib = _lib.load()
     x = _activation(x)
     fu, fv = _Factor(u), _Factor(v)
+    fu.dense()
+    fv.dense()
     flags = _layout_flags((fu,), (fv,)) | (_lib.SVDMLP_X_T if x_transposed else 0)
     w_code = _w_code(x, (u,))
     out = torch.empty((T, dout), dtype=x.dtype, device=dev)
@@ -243,6 +278,15 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
     _uniform(vs, all(f.linear for f in vs))
     flags = _layout_flags(us, vs)
     w_code = _w_code(x, (u_gate,))
+    # padded rows: bf16 natural layout only, one pitch for gate and up
+    if x.dtype != torch.bfloat16 or w_code == _lib.SVDMLP_FP8_E4M3 or flags:
+        for f in fs:
+            f.dense()
+    for a, b in ((fs[0], fs[2]), (fs[1], fs[3])):
+        if a.ld != b.ld:
+            a.dense()
+            b.dense()
+    ld_arr = (ctypes.c_int64 * 6)(*[f.ld for f in fs]) if any(f.ld for f in fs) else None
     scale_arr = None
     if w_code == _lib.SVDMLP_FP8_E4M3:
         scale_arr = (ctypes.c_void_p * 6)(*[f.scale_ptr for f in fs])
@@ -253,7 +297,7 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
     if workspace is None:
         workspace = svd_mlp_workspace(x, r=max(r_gu, r_d), ff=ff, w_code=w_code)
     dims = (T, d, ff, r_gu, r_d)
-    return x, fs, flags, w_code, scale_arr, out, workspace, dims, dev
+    return x, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev
 
 
 def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
@@ -263,12 +307,13 @@ def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.T
     rank may differ.  ``workspace``/``out`` may be supplied to avoid
     per-call allocation (see :func:`svd_mlp_workspace`)."""
     lib = _lib.load()
-    x, fs, flags, w_code, scale_arr, out, workspace, dims, dev = _prepare_layer(
+    x, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
         x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
     with torch.cuda.device(dev):
-        _lib.check(lib.svdmlp_svd_mlp(
+        _lib.check(lib.svdmlp_svd_mlp_ld(
             x.data_ptr(), *(f.ptr for f in fs),
-            ctypes.addressof(scale_arr) if scale_arr is not None else None, out.data_ptr(),
+            ctypes.addressof(scale_arr) if scale_arr is not None else None,
+            ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
             *dims, _ACT_CODES[x.dtype], w_code, flags,
             workspace.data_ptr(), workspace.numel(), _stream(dev)))
     return out
@@ -281,7 +326,7 @@ def svd_mlp_block(x, norm_weight, u_gate, v_gate, u_up, v_up, u_down, v_down, *,
     add of bench/e2e_block.py:268-278, both rounded to x.dtype.
     ``norm_weight`` is the (d,) gain (any float dtype; used in fp32)."""
     lib = _lib.load()
-    x, fs, flags, w_code, scale_arr, out, workspace, dims, dev = _prepare_layer(
+    x, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
         x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
     if out.data_ptr() == x.data_ptr():
         raise ValueError("out must not alias x")
@@ -293,9 +338,10 @@ def svd_mlp_block(x, norm_weight, u_gate, v_gate, u_up, v_up, u_down, v_down, *,
     if not eps > 0:
         raise ValueError(f"eps must be positive, got {eps}")
     with torch.cuda.device(dev):
-        _lib.check(lib.svdmlp_svd_mlp_block(
+        _lib.check(lib.svdmlp_svd_mlp_block_ld(
             x.data_ptr(), gain.data_ptr(), eps, *(f.ptr for f in fs),
-            ctypes.addressof(scale_arr) if scale_arr is not None else None, out.data_ptr(),
+            ctypes.addressof(scale_arr) if scale_arr is not None else None,
+            ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
             *dims, _ACT_CODES[x.dtype], w_code, flags,
             workspace.data_ptr(), workspace.numel(), _stream(dev)))
     return out

@@ -420,3 +420,77 @@ def test_checkpoint_runner_per_layer_report(gpu, tmp_path):
         assert rec["fused_ms"] > 0 and rec["unfused_low_rank_ms"] > 0
     assert all(s["complete"] and s["passed"] for s in report["summaries"])
     assert out.with_suffix(".csv").exists()
+
+
+# ---------------------------------------------------------------------------
+# factors with padded rows (svdmlp_svd_mlp_ld)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T", [1, 2, 8, 64, 128, 300])
+def test_padded_factor_rows(gpu, T):
+    """Row-padded natural-layout views (column slices of wider buffers) are
+    read in place by the GEMV layer (T <= 2), the MFMA decode layer (T <= 128)
+    and the large-tile path, with each factor's own pitch."""
+    shape = inputs.LayerShape(1024, 2048, 512, 384)
+    x, f = inputs.make_layer(shape, T=T, seed=700 + T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    pads = (8, 64, 8, 64, 24, 128)  # ug, vg, uu, vu, ud, vd
+    padded = [ops.pad_rows(a, p) for a, p in zip(t[1:], pads)]
+    assert all(ops.padded_rows(a) for a in padded)
+    ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
+    err = _rel(_np(ops.svd_mlp(t[0], *padded)), ref)
+    assert err < BF16_TOL, err
+    dense = _np(ops.svd_mlp(*t))
+    # same kernels and math; split-K partial sums are combined in arrival
+    # order, so bf16 roundings of the rank intermediates may differ by an ulp
+    assert _rel(_np(ops.svd_mlp(t[0], *padded)), dense) < 5e-3
+
+
+def test_padded_factor_rows_block_and_mixed_pitch(gpu):
+    shape = inputs.LayerShape(1024, 2048, 512)
+    x, f = inputs.make_layer(shape, T=48, seed=77)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    gain = np.random.default_rng(3).uniform(0.9, 1.1, size=shape.d).astype(np.float32)
+    g = torch.from_numpy(gain).to(gpu)
+    padded = [ops.pad_rows(a, 64) for a in t[1:]]
+    got = _np(ops.svd_mlp_block(t[0], g, *padded))
+    assert _rel(got, O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")) < BF16_TOL
+    # gate and up with different pitches: the host mirror reads them densely
+    mixed = list(padded)
+    mixed[2] = ops.pad_rows(t[3], 32)
+    assert _rel(_np(ops.svd_mlp(t[0], *mixed)), O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
+
+
+def test_padded_factor_rows_invalid(gpu):
+    """The C ABI rejects pitches below the row length, unaligned pitches,
+    different gate / up pitches and padded rows with fp32 factors."""
+    import ctypes
+
+    from svdmlp import _lib
+
+    lib = _lib.load()
+    T, d, ff, r = 8, 1024, 2048, 512
+    dev = gpu
+    x = torch.zeros((T, d), dtype=torch.bfloat16, device=dev)
+    fs = [torch.zeros(s, dtype=torch.bfloat16, device=dev)
+          for s in ((d, r + 64), (r, ff + 64), (d, r + 64), (r, ff + 64), (ff, r), (r, d))]
+    y = torch.empty((T, d), dtype=torch.bfloat16, device=dev)
+    ws = ops.svd_mlp_workspace(x, r=r, ff=ff)
+
+    def call(ld, act=_lib.SVDMLP_BF16):
+        arr = (ctypes.c_int64 * 6)(*ld)
+        return lib.svdmlp_svd_mlp_ld(x.data_ptr(), *(f.data_ptr() for f in fs), None, ctypes.addressof(arr),
+                                     y.data_ptr(), T, d, ff, r, r, act, act, 0, ws.data_ptr(), ws.numel(),
+                                     torch.cuda.current_stream(dev).cuda_stream)
+
+    for ld, msg in (((r - 8, 0, 0, 0, 0, 0), "below its row length"),
+                    ((r + 4, ff + 64, r + 4, ff + 64, 0, 0), "multiples of 8"),
+                    ((r + 64, ff + 64, r + 64, ff + 32, 0, 0), "share their leading dimensions")):
+        assert call(ld) == _lib.SVDMLP_EINVAL
+        assert msg in lib.svdmlp_last_error().decode()
+    assert call((r + 64, ff + 64, r + 64, ff + 64, 0, 0), act=_lib.SVDMLP_F32) == _lib.SVDMLP_EINVAL
+    assert "bf16 natural-layout" in lib.svdmlp_last_error().decode()
+    assert call((r + 64, ff + 64, r + 64, ff + 64, 0, 0)) == 0
+    torch.cuda.synchronize()
