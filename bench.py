@@ -64,16 +64,19 @@ def _args(argv=None):
     p.add_argument("--copy-check", type=int, default=0, metavar="MIB",
                    help="before the steps, copy a MIB-sized buffer 3 times (a plain copy kernel of known size "
                         "for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    p.add_argument("--weights-layout", choices=("natural", "linear"), default="natural",
-                   help="natural (in, out) factors as kernels/reference.py takes them, or PyTorch Linear "
-                        "(out, in) storage passed as transposed views (test_speedup.py nki_mm)")
+    p.add_argument("--weights-layout", choices=("natural", "padded", "linear"), default="padded",
+                   help="natural (in, out) factors as kernels/reference.py takes them; padded: natural with the "
+                        "V factors' rows 64 elements apart wider than their length (read in place); or PyTorch "
+                        "Linear (out, in) storage passed as transposed views (test_speedup.py nki_mm)")
     return p.parse_args(argv)
 
 
-def _layer_weights(torch, dev, seed, linear=False):
+def _layer_weights(torch, dev, seed, linear=False, pad_v=0):
     """Synthetic factors of one layer: U ~ N(0, 1/d_in), V ~ N(0, 1/r), bf16,
     drawn on the device from a seeded generator (reference recipe
-    test_speedup.py:803-808, device RNG instead of numpy)."""
+    test_speedup.py:803-808, device RNG instead of numpy).  ``pad_v`` > 0
+    stores the V factors with rows that many elements wider (the same
+    values, read in place through the layered entry points)."""
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
 
@@ -84,6 +87,10 @@ def _layer_weights(torch, dev, seed, linear=False):
 
     uu, vu, ug, vg = rnd(D, R), rnd(R, FF), rnd(D, R), rnd(R, FF)
     ud, vd = rnd(FF, R), rnd(R, D)
+    if pad_v:
+        from svdmlp.ops import pad_rows
+
+        vu, vg, vd = (pad_rows(v, pad_v) for v in (vu, vg, vd))
     return ug, vg, uu, vu, ud, vd  # gate-first, kernels/reference.py order
 
 
@@ -106,6 +113,7 @@ def _stage_work(T):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_8b_T1024_traffic.md"
+TRAFFIC_LAYOUT = "padded"   # the weights layout the PMC summary was taken with
 
 
 def _profiled_traffic(stage):
@@ -274,7 +282,8 @@ def main(argv=None) -> int:
     stream = torch.cuda.current_stream(dev)
     T = args.tokens
     linear = args.weights_layout == "linear"
-    layers = [_layer_weights(torch, dev, args.seed + i, linear) for i in range(args.layers)]
+    pad_v = 64 if args.weights_layout == "padded" else 0
+    layers = [_layer_weights(torch, dev, args.seed + i, linear, pad_v) for i in range(args.layers)]
     gx = torch.Generator(device=dev)
     gx.manual_seed(args.seed + 1000)
     x = torch.randn(T, D, generator=gx, device=dev, dtype=torch.float32).to(torch.bfloat16)
@@ -336,7 +345,7 @@ def main(argv=None) -> int:
                 "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4) if achieved else None,
-                "traffic": _profiled_traffic(dom) if (T, args.weights_layout) == (1024, "natural") else None,
+                "traffic": _profiled_traffic(dom) if (T, args.weights_layout) == (1024, TRAFFIC_LAYOUT) else None,
                 "traffic_source": "profiles/prefill_8b_T1024_traffic.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
                                   "per dispatch, calibrated on a 256 MiB copy",
                 "algorithmic_flop_per_launch": dom_flops,

@@ -8,7 +8,8 @@
  * Conventions (every entry point):
  *   - All pointers are device pointers owned by the caller (including the
  *     outputs and the workspace); the library never allocates.  Matrices are
- *     dense and row-major with the leading dimension equal to the row length.
+ *     dense and row-major with the leading dimension equal to the row length
+ *     (the factors of the _ld entry points excepted).
  *   - Factor layouts follow kernels/reference.py: U is (d_in, r), V is
  *     (r, d_out) ("natural" layout).  Setting SVDMLP_U_LINEAR / SVDMLP_V_LINEAR
  *     declares the PyTorch Linear layout instead: U given as (r, d_in) and V as
@@ -137,7 +138,8 @@ int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const vo
  * stripe of a factor maps onto a fixed subset of HBM channels, and at
  * decode shapes the slowest such subset bounds the weight stream; padding
  * V rows by 64 elements spreads every stripe over all channels (8B layer at
- * 8 tokens: 80 -> 73 us).  Shapes that only other kernels take (fp32, fp8,
+ * 8 tokens: 83 -> 76 us; with padded factors the MFMA decode layer also
+ * takes 1-2 tokens, 75.5 us against 78 us at one token).  Shapes that only other kernels take (fp32, fp8,
  * Linear layout, odd sizes) return SVDMLP_EINVAL with padded factors.
  */
 int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,

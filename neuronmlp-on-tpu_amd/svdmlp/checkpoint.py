@@ -159,14 +159,18 @@ def load_mlp_factors(model_path: str | Path, layer_indices: Sequence[int], *, de
                      layout: str = "natural", dtype=None) -> tuple[tuple, ...]:
     """Selected layers' factors on ``device``, gate-first ``(Ug, Vg, Uu, Vu, Ud,
     Vd)`` per layer (models/hf_svd.py:132-196).  ``layout`` is ``"natural"``
-    (contiguous ``(in, out)``, transposed on the device) or ``"linear"``
+    (contiguous ``(in, out)``, transposed on the device), ``"padded"`` (natural,
+    with the V factors' rows 64 elements longer in memory: the row pitch the
+    decode kernels stream fastest, see ``ops.pad_rows``) or ``"linear"``
     (transposed views of the stored ``(out, in)`` tensors).  ``dtype``
     optionally converts (e.g. ``torch.bfloat16``) on the device."""
     import torch
     from safetensors import safe_open
 
-    if layout not in ("natural", "linear"):
-        raise ValueError(f"layout must be 'natural' or 'linear', got {layout!r}")
+    from .ops import pad_rows
+
+    if layout not in ("natural", "padded", "linear"):
+        raise ValueError(f"layout must be 'natural', 'padded' or 'linear', got {layout!r}")
     model_path = Path(model_path)
     config, index = checkpoint_metadata(model_path)
     layer_indices = tuple(layer_indices)
@@ -181,11 +185,16 @@ def load_mlp_factors(model_path: str | Path, layer_indices: Sequence[int], *, de
         shards = {name: stack.enter_context(safe_open(str(model_path / name), framework="pt")) for name in names}
         for layer in layer_indices:
             factors = []
-            for key in factor_keys(layer):
+            for i, key in enumerate(factor_keys(layer)):
                 stored = shards[weight_map[key]].get_tensor(key).to(dev)  # (out, in)
                 if dtype is not None:
                     stored = stored.to(dtype)
-                factors.append(stored.t().contiguous() if layout == "natural" else stored.t())
+                if layout == "linear":
+                    factors.append(stored.t())
+                elif layout == "padded" and i % 2:   # Vg, Vu, Vd
+                    factors.append(pad_rows(stored.t()))
+                else:
+                    factors.append(stored.t().contiguous())
                 del stored
             validate_factor_shapes(factors, hidden_size=int(config["hidden_size"]),
                                    intermediate_size=int(config["intermediate_size"]))

@@ -50,16 +50,19 @@ def test_stored_tensors_are_linear_weights_with_swapped_names(ckpt):
     assert len(set(index.values())) == 2  # three layers, two per shard
 
 
-@pytest.mark.parametrize("layout", ["natural", "linear"])
+@pytest.mark.parametrize("layout", ["natural", "padded", "linear"])
 def test_load_returns_gate_first_natural_operands(ckpt, layout):
     path, layers = ckpt
     loaded = C.load_mlp_factors(path, [2, 0], device="cpu", layout=layout)
     assert len(loaded) == 2
     for got, want in zip(loaded, (layers[2], layers[0])):
-        for g, w in zip(got, want):
+        for i, (g, w) in enumerate(zip(got, want)):
             assert g.shape == w.shape and g.dtype == w.dtype
             assert torch.equal(g, w)
-            assert g.is_contiguous() == (layout == "natural")
+            if layout == "padded" and i % 2:   # V factors: rows 64 elements longer in memory
+                assert g.stride() == (w.shape[1] + 64, 1)
+            else:
+                assert g.is_contiguous() == (layout != "linear")
 
 
 def test_load_converts_dtype(ckpt):

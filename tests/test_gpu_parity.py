@@ -377,7 +377,7 @@ def test_mlp_stack_nonuniform_ranks(gpu):
 # safetensors SVD checkpoint (models/hf_svd.py) -> the HIP layer
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("layout,T", [("natural", 1), ("natural", 300), ("linear", 64)])
+@pytest.mark.parametrize("layout,T", [("natural", 1), ("padded", 1), ("natural", 300), ("padded", 300), ("linear", 64)])
 def test_checkpoint_layers_run_on_the_hip_path(gpu, tmp_path, layout, T):
     """Factors written as a two-shard checkpoint (stored as Linear weights with
     the v/u names swapped), loaded back onto the GPU, give the oracle's layer."""
@@ -429,8 +429,8 @@ def test_checkpoint_runner_per_layer_report(gpu, tmp_path):
 @pytest.mark.parametrize("T", [1, 2, 8, 64, 128, 300])
 def test_padded_factor_rows(gpu, T):
     """Row-padded natural-layout views (column slices of wider buffers) are
-    read in place by the GEMV layer (T <= 2), the MFMA decode layer (T <= 128)
-    and the large-tile path, with each factor's own pitch."""
+    read in place by the MFMA decode layer (T <= 128; it takes T <= 2 too when
+    rows are padded) and the large-tile path, with each factor's own pitch."""
     shape = inputs.LayerShape(1024, 2048, 512, 384)
     x, f = inputs.make_layer(shape, T=T, seed=700 + T)
     xb, *fb = _rounded((x, *f), torch.bfloat16)
@@ -439,12 +439,31 @@ def test_padded_factor_rows(gpu, T):
     padded = [ops.pad_rows(a, p) for a, p in zip(t[1:], pads)]
     assert all(ops.padded_rows(a) for a in padded)
     ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
-    err = _rel(_np(ops.svd_mlp(t[0], *padded)), ref)
+    ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
+    err = _rel(_np(ops.svd_mlp(t[0], *padded, workspace=ws)), ref)
     assert err < BF16_TOL, err
+    if T <= 128:   # one MFMA decode-layer launch: 3 barriers, counters back at zero
+        assert _barrier_state(ws) == (3, 0) and not any(_tile_counters(ws))
     dense = _np(ops.svd_mlp(*t))
     # same kernels and math; split-K partial sums are combined in arrival
     # order, so bf16 roundings of the rank intermediates may differ by an ulp
     assert _rel(_np(ops.svd_mlp(t[0], *padded)), dense) < 5e-3
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_padded_factor_rows_gemv_layer(gpu, T):
+    """Padded rows on a shape only the streaming-GEMV layer takes at decode
+    (d = 1040 is no multiple of 128): ragged strips read with each factor's
+    pitch."""
+    shape = inputs.LayerShape(1040, 2064, 400, 272)
+    x, f = inputs.make_layer(shape, T=T, seed=720 + T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    padded = [ops.pad_rows(a, p) for a, p in zip(t[1:], (8, 64, 8, 64, 24, 128))]
+    ws = ops.svd_mlp_workspace(t[0], r=shape.r, ff=shape.ff)
+    got = _np(ops.svd_mlp(t[0], *padded, workspace=ws))
+    assert _rel(got, O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
+    assert _barrier_state(ws) == (4, 0)   # one GEMV-layer launch: 4 barriers
 
 
 def test_padded_factor_rows_block_and_mixed_pitch(gpu):
