@@ -66,7 +66,7 @@ def _args(argv=None):
                         "for calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     p.add_argument("--weights-layout", choices=("natural", "padded", "linear"), default="padded",
                    help="natural (in, out) factors as kernels/reference.py takes them; padded: natural with the "
-                        "V factors' rows 64 elements apart wider than their length (read in place); or PyTorch "
+                        "V factors' rows 64 elements longer in memory than their length (read in place); or PyTorch "
                         "Linear (out, in) storage passed as transposed views (test_speedup.py nki_mm)")
     return p.parse_args(argv)
 
@@ -113,15 +113,16 @@ def _stage_work(T):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_8b_T1024_traffic.md"
-TRAFFIC_LAYOUT = "padded"   # the weights layout the PMC summary was taken with
+TRAFFIC_LAYOUT = "padded"   # the weights layout the PMC summaries were taken with
+DECODE_TRAFFIC_PROFILE = ROOT / "profiles" / "decode_8b_traffic.md"
 
 
-def _profiled_traffic(stage):
-    """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary
+def _profiled_traffic(stage, path=TRAFFIC_PROFILE):
+    """HBM bytes per launch of a stage from a committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel of known size),
     or None when the summary has no line for it."""
     try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
+        for line in path.read_text().splitlines():
             parts = line.split()
             if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == stage:
                 return int(parts[2])
@@ -380,10 +381,16 @@ def main(argv=None) -> int:
                 _time_steps(torch, dstep, min(args.decode_steps, 50), 0, stream)
             nbytes = factor_bytes + 2 * Td * D * 2
             gbs = nbytes / (msd * 1e-3) / 1e9
+            # measured HBM bytes of the MFMA decode layer's launch (16-row token tiles: 1, 2, 4 or 8 of them)
+            mt = 1 if Td <= 16 else (2 if Td <= 32 else (4 if Td <= 64 else 8))
+            traffic = (_profiled_traffic(f"decode_layer_mt{mt}", DECODE_TRAFFIC_PROFILE)
+                       if args.weights_layout == TRAFFIC_LAYOUT and Td <= 128 else None)
             dec[f"T={Td}"] = {
                 "us_per_layer": round(msd * 1e3, 2),
                 "GB/s": round(gbs, 1),
                 "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                "traffic": traffic,
+                "traffic_GB/s": round(traffic / (msd * 1e-3) / 1e9, 1) if traffic else None,
                 "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),
                 "stages_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.result.items()},
             }
