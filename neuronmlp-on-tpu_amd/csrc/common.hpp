@@ -27,17 +27,21 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
   return __uint_as_float(h16 << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quieted).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+// fp32 -> bf16, round to nearest even, NaN stays NaN: gfx950's
+// v_cvt_pk_bf16_f32, two values per instruction (the vector conversion
+// compiles to it).  It equals the integer form -- u += 0x7fff + ((u >> 16) & 1),
+// keep the high half -- on every non-NaN input, denormals included (checked
+// on MI355X over 2^28 value pairs: every exponent, halfway and near-halfway
+// mantissas); the integer form took ~6 instructions per value in the
+// epilogues.
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_cvt{lo, hi}, bf16x2_cvt));
 }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 
 // fp8 e4m3fn (OCP, no infinities, 0x7f/0xff = NaN, max 448) -> fp32, exact.
 __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
@@ -51,11 +55,15 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
   return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
 }
 
-// Branch-stable SiLU in fp32: every exp argument is <= 0.
+// Branch-stable SiLU in fp32 (kernels/reference.py:37-51): every exp
+// argument is <= 0, so 1 + z lies in [1, 2] and the hardware reciprocal
+// (v_rcp_f32, 1 ulp) stands in for an IEEE division, whose scale / fma /
+// fixup sequence made the SwiGLU epilogue of the 8B layer ~4 us slower; the
+// result is rounded to bf16 (8 bits of mantissa) afterwards.
 __device__ __forceinline__ float silu_f32(float x) {
   const float z = __expf(-fabsf(x));
-  const float sig = (x >= 0.0f) ? 1.0f / (1.0f + z) : z / (1.0f + z);
-  return x * sig;
+  const float r = __builtin_amdgcn_rcpf(1.0f + z);
+  return x * ((x >= 0.0f) ? r : z * r);
 }
 
 // ---------------------------------------------------------------------------

@@ -455,10 +455,14 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int n = n0 + wn0 + 16 * j + 4 * lg;
+        // Unconditional loads (fragment order covers the padded tile; a
+        // row-major g is read at a clamped in-bounds address) so that all of
+        // them issue before the first store: a load under a branch left a
+        // vmcnt(0) per fragment, which also waited for every earlier h store.
         const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
-        gv[i][j] = (m < p.M && n < p.N)
-                       ? *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (int64_t)m * p.ldo + n))
-                       : u32x2{0u, 0u};
+        const bool in = m < p.M && n < p.N;
+        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (in ? (int64_t)m * p.ldo + n : 0)));
+        gv[i][j] = in ? g : u32x2{0u, 0u};
       }
     }
   }
