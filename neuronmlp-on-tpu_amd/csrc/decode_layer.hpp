@@ -162,6 +162,16 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
   dl_block_sync();
 }
 
+// Buffer descriptor of the split-K slice area (kDlMaxGrid units of MT
+// 16-row blocks, 2048 floats each), the cache-policy bits of a device-scope
+// (sc1) buffer access, and an offset past every record.
+constexpr int kDlSc1 = 16;
+constexpr uint32_t kDlPastSlices = 0xfffffff0u;
+template <int MT>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dl_slice_rsrc(float* slices) {
+  return __builtin_amdgcn_make_buffer_rsrc(slices, 0, kDlMaxGrid * MT * 2048 * 4, 0x00020000);
+}
+
 // Device-scope 8-byte store / load (sc1): coherent across XCDs without cache
 // maintenance.
 __device__ __forceinline__ void dl_store8(void* p, u32x2 v) {
@@ -362,13 +372,18 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
                                            int splits, uint32_t* cnt, float* slices, int* flag, uint16_t* dst) {
   const int n = U.n0 + 64 * (c.wave >> 2) + 16 * (c.wave & 3) + 4 * c.lg;
   if (splits > 1) {
-    float* mine = slices + (int64_t)u * MT * 2048 + 4 * threadIdx.x;
+    // Slices move as one 16-byte device-scope (sc1) buffer access per lane
+    // and 16-row block; rows >= T take an offset past the records, which
+    // stores drop and loads read as zeros.  (Pairs of 8-byte atomic accesses
+    // cost 2 us at 1-8 tokens and 21 us at 128 in the 8B layer.)
+    const __amdgpu_buffer_rsrc_t rs = dl_slice_rsrc<MT>(slices);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      if (16 * mt + c.lr < c.T) {
-        dl_store8(mine + mt * 2048, u32x2{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y)});
-        dl_store8(mine + mt * 2048 + 2, u32x2{__float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)});
-      }
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint32_t off = 16 * mt + c.lr < c.T ? (uint32_t)(((u * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y),
+                                                   __float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)},
+                                             rs, off, 0, kDlSc1);
+    }
     dl_wait_vm<0>();
     dl_block_sync();
     if (threadIdx.x == 0) {
@@ -382,26 +397,26 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
     const int split = u / nt, tile = u - split * nt;
     constexpr int SB = MT >= 8 ? 2 : 8;  // slices in flight (registers: SB * MT * 4)
     for (int s0 = 0; s0 < splits; s0 += SB) {
-      u32x2 v[SB][MT][2];
+      u32x4 v[SB][MT];
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const int s = s0 + i;
-        const float* o = slices + (int64_t)(tile + s * nt) * MT * 2048 + 4 * threadIdx.x;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const bool live = s < splits && s != split && 16 * mt + c.lr < c.T;
-          v[i][mt][0] = live ? dl_load8(o + mt * 2048) : u32x2{0u, 0u};
-          v[i][mt][1] = live ? dl_load8(o + mt * 2048 + 2) : u32x2{0u, 0u};
+          const uint32_t off =
+              live ? (uint32_t)((((tile + s * nt) * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+          v[i][mt] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kDlSc1);
         }
       }
 #pragma unroll
       for (int i = 0; i < SB; ++i)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt].x += __uint_as_float(v[i][mt][0].x);
-          acc[mt].y += __uint_as_float(v[i][mt][0].y);
-          acc[mt].z += __uint_as_float(v[i][mt][1].x);
-          acc[mt].w += __uint_as_float(v[i][mt][1].y);
+          acc[mt].x += __uint_as_float(v[i][mt].x);
+          acc[mt].y += __uint_as_float(v[i][mt].y);
+          acc[mt].z += __uint_as_float(v[i][mt].z);
+          acc[mt].w += __uint_as_float(v[i][mt].w);
         }
     }
   }
