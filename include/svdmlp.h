@@ -138,8 +138,8 @@ int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const vo
  * stripe of a factor maps onto a fixed subset of HBM channels, and at
  * decode shapes the slowest such subset bounds the weight stream; padding
  * V rows by 64 elements spreads every stripe over all channels (8B layer at
- * 8 tokens: 83 -> 76 us; with padded factors the MFMA decode layer also
- * takes 1-2 tokens, 75.5 us against 78 us at one token).  Shapes that only other kernels take (fp32, fp8,
+ * 8 tokens: 82 -> 75 us; with padded factors the MFMA decode layer also
+ * takes 1-2 tokens, 74.5 us against 77.6 us at one token).  Shapes that only other kernels take (fp32, fp8,
  * Linear layout, odd sizes) return SVDMLP_EINVAL with padded factors.
  */
 int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
