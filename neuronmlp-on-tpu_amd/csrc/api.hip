@@ -174,10 +174,12 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
   for (int64_t rr = std::min<int64_t>(r, 8); rr <= r; rr += (rr + 8 <= r ? 8 : std::max<int64_t>(1, r - rr))) {
     // {K, N, batch, fn}: the rank is N of the X.U stages and K of the XU.V stages
     const int64_t stages[][4] = {{d, rr, 2, 8}, {ff, rr, 1, 8}, {rr, d, 1, 8}, {rr, ff, 1, 8}, {rr, d, 1, 4},
-                                 {rr, ff, 1, 4}};
+                                 {rr, ff, 1, 4}, {d, rr, 2, 4}, {ff, rr, 1, 4}};
     for (const auto& st : stages) {
       const int sp = plan_splits(T, st[0], st[1], (int)st[3], (int)st[2]);
-      if (sp > 1) part = std::max(part, (int64_t)sp * st[2] * T * st[1] * 4);
+      // slices hold whole 256 x 32*fn tiles (fragment order)
+      const int64_t bn = 32 * st[3], tp = (T + 255) / 256 * 256, np = (st[1] + bn - 1) / bn * bn;
+      if (sp > 1) part = std::max(part, (int64_t)sp * st[2] * tp * np * 4);
     }
     if (rr == r) break;
   }
@@ -205,7 +207,10 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   off += a256(T * big * 4);
   w.y32 = off;
   off += a256(T * big * 4);
-  const int64_t part = part_bytes(T, d, ff, r);
+  // split-K slices serve the large-tile path only, which takes T > kDecodeMaxT
+  // (they hold whole 256-row tiles, so sizing them at decode T would also
+  // make smaller T ask for more than larger T)
+  const int64_t part = dec ? 0 : part_bytes(T, d, ff, r);
   w.part = off;
   off += a256(part);
   w.norm = off;
@@ -411,13 +416,21 @@ bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes, std
   return true;
 }
 
+// Waves per block of a large-tile launch: 4 only for the fn-8 natural-layout
+// store stages under SVDMLP_TUNE=nw=4.
+int big_nw(int fn, int epi, bool b_kc) { return (fn == 8 && epi == BEPI_STORE && !b_kc && tune().nw == 4) ? 4 : 8; }
+
+// Tile shapes whose fragment-order split-K slices the reduction kernel takes.
+bool big_frag_reduce_ok(int fn, int nw) { return (nw == 8 && (fn == 8 || fn == 4)) || (nw == 4 && fn == 8); }
+
 int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
-             int gfrag = 0) {
+             int gfrag = 0, int out_frag = 0) {
   BigParams p{};
   p.gfrag = gfrag;
+  p.out_frag = out_frag;
   const bool fp8 = c.wt == SVDMLP_FP8_E4M3;
   if (fp8 && (!s0 || b_kc)) return fail("fp8 large-tile GEMM needs natural-layout weights and scales");
   p.scale[0] = s0;
@@ -442,7 +455,7 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   p.ntiles = (N + 32 * fn - 1) / (32 * fn);
   p.k_split = k_split;
   const int splits = (K + k_split - 1) / k_split;
-  const BigDesc d{fn, b_kc, epi, out_f32, fp8, (fn == 8 && epi == BEPI_STORE && !b_kc && tune().nw == 4) ? 4 : 8};
+  const BigDesc d{fn, b_kc, epi, out_f32, fp8, big_nw(fn, epi, b_kc)};
   const char* why = nullptr;
   StageScope ss(stage, c.st);
   return check(launch_big(d, p, splits, batch, c.st, &why), "large-tile GEMM", why);
@@ -519,6 +532,18 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
     return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
                     BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1);
   float* part = reinterpret_cast<float*>(ws + L.part);
+  const int nw = big_nw(fn, BEPI_STORE, u_lin);
+  if (big_frag_reduce_ok(fn, nw)) {
+    // slices in fragment order: per split, `batch` blocks of whole tiles
+    const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
+    int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn, BEPI_STORE, ks,
+                      part, r, per, nullptr, true, batch * per, s0, s1, 0, 1);
+    if (rc) return rc;
+    StageScope fin(ST_FINALIZE, c.st);
+    return check(launch_reduce_frag_bf16(part, splits, batch * per, per, xu, r, (int64_t)T * r, T, r, (int)(tp / 256),
+                                         (int)(np / (32 * fn)), fn, nw, batch, c.st),
+                 "split-K reduce");
+  }
   const int64_t slice = (int64_t)batch * T * r;
   int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
                     BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice, s0, s1);
@@ -559,6 +584,17 @@ int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T,
     return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1,
                     fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv);
   float* part = reinterpret_cast<float*>(ws + L.part);
+  const int nw = big_nw(fn, BEPI_STORE, v_lin);
+  if (big_frag_reduce_ok(fn, nw)) {
+    const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)dout + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
+    int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1, fn,
+                      BEPI_STORE, ks, part, dout, per, nullptr, true, per, sv, nullptr, 0, 1);
+    if (rc) return rc;
+    StageScope fin(ST_FINALIZE, c.st);
+    return check(launch_reduce_frag_bf16(part, splits, per, per, static_cast<uint16_t*>(y), dout, (int64_t)T * dout,
+                                         T, dout, (int)(tp / 256), (int)(np / (32 * fn)), fn, nw, 1, c.st),
+                 "split-K reduce");
+  }
   const int64_t slice = (int64_t)T * dout;
   int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r,
                     1, fn, BEPI_STORE, ks, part, dout, 0, nullptr, true, slice, sv);

@@ -44,7 +44,58 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
   return hipErrorInvalidValue;
 }
 
+// One block per wave tile (16*FM x 16*FN, FM*FN*256 floats contiguous in
+// fragment order) of one batch entry: the splits are summed with coalesced
+// 16-byte reads, the bf16 tile is staged in LDS and written as whole row
+// pieces (16 bytes per lane).  Lane L of fragment (i, j) holds rows
+// 16i + L%16, columns 16j + 4*(L/16) .. +3 of the wave tile.
+template <int FM, int FN>
+__global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, int splits, int64_t sstride,
+                                                               int64_t bstride, uint16_t* out, int64_t ldo,
+                                                               int64_t obstride, int M, int N, int mtiles, int nw) {
+  constexpr int ROWS = 16 * FM, COLS = 16 * FN, PITCH = COLS + 8;  // staged row pitch (elements)
+  constexpr int Q = FM * FN * 64;                                   // float4s per wave tile
+  __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS * PITCH];
+  const int zb = blockIdx.y;
+  const int unit = blockIdx.x, wave = unit % nw, t_lin = unit / nw;
+  const int m0 = (t_lin % mtiles) * 256 + (wave >> 1) * ROWS;
+  const int n0 = (t_lin / mtiles) * (2 * COLS) + (wave & 1) * COLS;
+  const float* src = in + (int64_t)zb * bstride + (int64_t)unit * Q * 4;
+  for (int q = threadIdx.x; q < Q; q += 256) {
+    f32x4 a = *reinterpret_cast<const f32x4*>(src + 4 * q);
+    for (int s = 1; s < splits; ++s) a += *reinterpret_cast<const f32x4*>(src + (int64_t)s * sstride + 4 * q);
+    const int fi = q >> 6, l = q & 63;
+    const int r = 16 * (fi / FN) + (l & 15), c = 16 * (fi % FN) + 4 * (l >> 4);
+    *reinterpret_cast<u32x2*>(tile + r * PITCH + c) = u32x2{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w)};
+  }
+  __syncthreads();
+  uint16_t* dst = out + (int64_t)zb * obstride;
+  for (int k = threadIdx.x; k < ROWS * (COLS / 8); k += 256) {
+    const int r = k / (COLS / 8), c = 8 * (k % (COLS / 8));
+    const int m = m0 + r, n = n0 + c;
+    if (m < M && n < N)  // N % 8 == 0
+      *reinterpret_cast<u32x4*>(dst + (int64_t)m * ldo + n) = *reinterpret_cast<const u32x4*>(tile + r * PITCH + c);
+  }
+}
+
+template <int FM, int FN>
+hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out, int64_t ldo,
+                     int64_t obstride, int M, int N, int mtiles, int ntiles, int nw, int batch, hipStream_t st) {
+  hipLaunchKernelGGL((reduce_frag_bf16_kernel<FM, FN>), dim3(mtiles * ntiles * nw, batch), dim3(256), 0, st, in,
+                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
+                                   int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
+                                   int batch, hipStream_t st) {
+  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, st);
+  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, st);
+  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, st);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st,
                       const char** why) {

@@ -163,6 +163,7 @@ struct BigParams {
   const uint16_t* gmem;  // BEPI_SWIGLU_MEM: bf16 gate values, same layout as out
   const float* scale[2]; // fp8 B: one fp32 scale per output column, per batch entry
   int gfrag;             // BEPI_SWIGLU_MEM: gmem holds g in fragment order (BEPI_STORE_FRAG)
+  int out_frag;          // fp32 output (split-K slices) in fragment order, padded tiles included
   int M, N, K;
   int mtiles, ntiles;
   int k_split;
@@ -441,6 +442,10 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
   char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
   constexpr bool FRAG = C::EPI == BEPI_STORE_FRAG;
+  // fp32 split-K slices in fragment order: every lane's 16 bytes of a
+  // fragment are contiguous with its neighbours' (the row-major stores write
+  // 16 rows x 64 bytes per instruction; 8B layer: epilogue 9.1K -> 6K cycles)
+  const bool ffrag = C::OUT_F32 && p.out_frag;
   // fragment-order element offset of this lane's block (0, 0)
   const int64_t frag0 = ((((int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN)) * NW + wave) * FM * FN) * 256 + 4 * lane;
   // SwiGLU: every gate value of the wave's tile is loaded before the first
@@ -469,11 +474,11 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm0 + 16 * i + lr;
-    if (!FRAG && m >= p.M) continue;
+    if (!FRAG && !ffrag && m >= p.M) continue;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn0 + 16 * j + 4 * lg;
-      if (!FRAG && n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+      if (!FRAG && !ffrag && n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
       f32x4 v = acc[i][j];
       if constexpr (C::FP8_B)
         if (n < p.N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
@@ -491,7 +496,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         unsafeAtomicAdd(op + 2, v.z);
         unsafeAtomicAdd(op + 3, v.w);
       } else if constexpr (C::OUT_F32) {
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + o) = v;
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + (ffrag ? fo : o)) = v;
       } else if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
         const u32x2 g = gv[i][j];
         const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
