@@ -60,13 +60,24 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
   const int unit = blockIdx.x, wave = unit % nw, t_lin = unit / nw;
   const int m0 = (t_lin % mtiles) * 256 + (wave >> 1) * ROWS;
   const int n0 = (t_lin / mtiles) * (2 * COLS) + (wave & 1) * COLS;
-  const float* src = in + (int64_t)zb * bstride + (int64_t)unit * Q * 4;
-  for (int q = threadIdx.x; q < Q; q += 256) {
-    f32x4 a = *reinterpret_cast<const f32x4*>(src + 4 * q);
-    for (int s = 1; s < splits; ++s) a += *reinterpret_cast<const f32x4*>(src + (int64_t)s * sstride + 4 * q);
-    const int fi = q >> 6, l = q & 63;
+  const float* src = in + (int64_t)zb * bstride + (int64_t)unit * Q * 4 + 4 * threadIdx.x;
+  static_assert(Q % 256 == 0, "whole rounds");
+  constexpr int PER = Q / 256;  // float4s per thread, all loaded per split before any is summed
+  f32x4 a[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) a[k] = *reinterpret_cast<const f32x4*>(src + 1024 * k);
+  for (int s = 1; s < splits; ++s) {
+    f32x4 b[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) b[k] = *reinterpret_cast<const f32x4*>(src + (int64_t)s * sstride + 1024 * k);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) a[k] += b[k];
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) {
+    const int q = threadIdx.x + 256 * k, fi = q >> 6, l = q & 63;
     const int r = 16 * (fi / FN) + (l & 15), c = 16 * (fi % FN) + 4 * (l >> 4);
-    *reinterpret_cast<u32x2*>(tile + r * PITCH + c) = u32x2{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w)};
+    *reinterpret_cast<u32x2*>(tile + r * PITCH + c) = u32x2{pack_bf16x2(a[k].x, a[k].y), pack_bf16x2(a[k].z, a[k].w)};
   }
   __syncthreads();
   uint16_t* dst = out + (int64_t)zb * obstride;
