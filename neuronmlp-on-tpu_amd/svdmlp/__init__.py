@@ -25,6 +25,7 @@ Host package over libsvdmlp.so (hand-written HIP kernels for gfx950):
 from ._lib import SvdMlpError, load, version, workspace_bytes  # noqa: F401
 from .ops import (  # noqa: F401
     QuantizedFactor,
+    clear_workspace_cache,
     fused_gate_up,
     fused_xuv,
     low_rank_dim,

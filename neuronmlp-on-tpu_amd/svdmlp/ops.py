@@ -194,6 +194,39 @@ def _workspace(dev, T, d, ff, r, w_code) -> torch.Tensor:
     return ws
 
 
+# Workspaces of calls that pass none, one per (device, stream), grown on
+# demand: every call leaves the first 4 KB valid for the next call on its
+# stream (the barrier counters only grow, the tile counters return to zero),
+# so a reused workspace needs no clearing; a fresh one per call cost an
+# allocation and a fill kernel each time.
+_WS_CACHE: dict = {}
+
+
+_WS_BYTES: dict = {}
+
+
+def _shared_workspace(dev, T, d, ff, r, w_code) -> torch.Tensor:
+    size_key = (T, d, ff, r, w_code)
+    nbytes = _WS_BYTES.get(size_key)
+    if nbytes is None:
+        if len(_WS_BYTES) > 4096:
+            _WS_BYTES.clear()
+        nbytes = _WS_BYTES[size_key] = max(_lib.workspace_bytes(T, d, ff, r, w_code), 4096)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), torch.cuda.current_stream(dev).cuda_stream)
+    ws = _WS_CACHE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws[:4096].zero_()
+        _WS_CACHE[key] = ws
+    return ws
+
+
+def clear_workspace_cache() -> None:
+    """Release the workspaces kept for calls that pass none (allocated again
+    on the next such call)."""
+    _WS_CACHE.clear()
+
+
 # ---------------------------------------------------------------------------
 # Operators
 # ---------------------------------------------------------------------------
@@ -219,7 +252,7 @@ def fused_gate_up(x, u_gate, v_gate, u_up, v_up, *, out_transposed: bool = False
     flags = _layout_flags((ug, uu), (vg, vu)) | (_lib.SVDMLP_OUT_T if out_transposed else 0)
     w_code = _w_code(x, (u_gate,))
     out = torch.empty((ff, T) if out_transposed else (T, ff), dtype=x.dtype, device=dev)
-    ws = _workspace(dev, T, d, ff, r, w_code)
+    ws = _shared_workspace(dev, T, d, ff, r, w_code)
     with torch.cuda.device(dev):
         _lib.check(lib.svdmlp_gate_up(
             x.data_ptr(), ug.ptr, vg.ptr, uu.ptr, vu.ptr,
@@ -249,7 +282,7 @@ def fused_xuv(x, u, v, *, x_transposed: bool = False) -> torch.Tensor:
     flags = _layout_flags((fu,), (fv,)) | (_lib.SVDMLP_X_T if x_transposed else 0)
     w_code = _w_code(x, (u,))
     out = torch.empty((T, dout), dtype=x.dtype, device=dev)
-    ws = _workspace(dev, T, din, dout, r, w_code)
+    ws = _shared_workspace(dev, T, din, dout, r, w_code)
     with torch.cuda.device(dev):
         _lib.check(lib.svdmlp_xuv(
             x.data_ptr(), fu.ptr, fv.ptr, fu.scale_ptr, fv.scale_ptr, out.data_ptr(),
@@ -258,8 +291,46 @@ def fused_xuv(x, u, v, *, x_transposed: bool = False) -> torch.Tensor:
     return out
 
 
+# Prepared arguments of layers seen before, keyed on x's dtype, device and
+# width and on every factor's address, shape, strides, dtype and device: a
+# layer called again skips validation and marshalling (~20 us of Python per
+# call, which a lone call's first kernel waits for).  Only layers whose
+# factors are all read in place are kept, as addresses: a key can only match
+# tensors that lie exactly where the cached pointers point.
+_PLANS: dict = {}
+
+
+def _plan_key(x, factors):
+    if type(x) is not torch.Tensor or x.dim() != 2 or x.shape[0] == 0:
+        return None
+    key = [x.dtype, x.device, x.shape[1]]
+    for f in factors:
+        if type(f) is not torch.Tensor:
+            return None
+        key += (f.data_ptr(), f.shape, f.stride(), f.dtype, f.device)
+    return tuple(key)
+
+
 def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out):
-    """Validation and argument marshalling shared by svd_mlp and svd_mlp_block."""
+    """Validation and argument marshalling shared by svd_mlp and svd_mlp_block;
+    returns (x, factor pointers, holders, flags, w_code, scale array, ld
+    array, out, workspace, dims, device).  The caller keeps `holders` (the
+    prepared factors, which may own contiguous copies) until the launch is
+    enqueued."""
+    factors = (u_gate, v_gate, u_up, v_up, u_down, v_down)
+    key = _plan_key(x, factors)
+    plan = _PLANS.get(key) if key is not None else None
+    if plan is not None:
+        ptrs, flags, w_code, ld_arr, (d, ff, r_gu, r_d), dev = plan
+        T = int(x.shape[0])
+        x = _activation(x)
+        if out is None:
+            out = torch.empty((T, d), dtype=x.dtype, device=dev)
+        elif out.shape != (T, d) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
+            raise ValueError("out must be a contiguous (T, d) tensor of x.dtype on x.device")
+        if workspace is None:
+            workspace = _shared_workspace(dev, T, d, ff, max(r_gu, r_d), w_code)
+        return x, ptrs, None, flags, w_code, None, ld_arr, out, workspace, (T, d, ff, r_gu, r_d), dev
     validate_arrays(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
     T, d = _shape(x)
     if u_gate.shape[0] != d or v_gate.shape[0] != u_gate.shape[1]:
@@ -295,9 +366,22 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
     elif out.shape != (T, d) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
         raise ValueError("out must be a contiguous (T, d) tensor of x.dtype on x.device")
     if workspace is None:
-        workspace = svd_mlp_workspace(x, r=max(r_gu, r_d), ff=ff, w_code=w_code)
+        workspace = _shared_workspace(dev, T, d, ff, max(r_gu, r_d), w_code)
     dims = (T, d, ff, r_gu, r_d)
-    return x, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev
+    ptrs = tuple(f.ptr for f in fs)
+    if key is not None and scale_arr is None and all(p == f.data_ptr() for p, f in zip(ptrs, factors)):
+        if len(_PLANS) > 64:
+            _PLANS.clear()
+        _PLANS[key] = (ptrs, flags, w_code, ld_arr, (d, ff, r_gu, r_d), dev)
+    return x, ptrs, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev
+
+
+def _on_device(dev, call):
+    """Run call with dev current (a no-op switch when it already is)."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return call()
+    with torch.cuda.device(dev):
+        return call()
 
 
 def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
@@ -307,15 +391,15 @@ def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.T
     rank may differ.  ``workspace``/``out`` may be supplied to avoid
     per-call allocation (see :func:`svd_mlp_workspace`)."""
     lib = _lib.load()
-    x, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
+    x, ptrs, holders, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
         x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
-    with torch.cuda.device(dev):
-        _lib.check(lib.svdmlp_svd_mlp_ld(
-            x.data_ptr(), *(f.ptr for f in fs),
-            ctypes.addressof(scale_arr) if scale_arr is not None else None,
-            ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
-            *dims, _ACT_CODES[x.dtype], w_code, flags,
-            workspace.data_ptr(), workspace.numel(), _stream(dev)))
+    _on_device(dev, lambda: _lib.check(lib.svdmlp_svd_mlp_ld(
+        x.data_ptr(), *ptrs,
+        ctypes.addressof(scale_arr) if scale_arr is not None else None,
+        ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
+        *dims, _ACT_CODES[x.dtype], w_code, flags,
+        workspace.data_ptr(), workspace.numel(), _stream(dev))))
+    del holders
     return out
 
 
@@ -326,7 +410,7 @@ def svd_mlp_block(x, norm_weight, u_gate, v_gate, u_up, v_up, u_down, v_down, *,
     add of bench/e2e_block.py:268-278, both rounded to x.dtype.
     ``norm_weight`` is the (d,) gain (any float dtype; used in fp32)."""
     lib = _lib.load()
-    x, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
+    x, ptrs, holders, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
         x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
     if out.data_ptr() == x.data_ptr():
         raise ValueError("out must not alias x")
@@ -337,13 +421,13 @@ def svd_mlp_block(x, norm_weight, u_gate, v_gate, u_up, v_up, u_down, v_down, *,
     eps = float(eps)
     if not eps > 0:
         raise ValueError(f"eps must be positive, got {eps}")
-    with torch.cuda.device(dev):
-        _lib.check(lib.svdmlp_svd_mlp_block_ld(
-            x.data_ptr(), gain.data_ptr(), eps, *(f.ptr for f in fs),
-            ctypes.addressof(scale_arr) if scale_arr is not None else None,
-            ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
-            *dims, _ACT_CODES[x.dtype], w_code, flags,
-            workspace.data_ptr(), workspace.numel(), _stream(dev)))
+    _on_device(dev, lambda: _lib.check(lib.svdmlp_svd_mlp_block_ld(
+        x.data_ptr(), gain.data_ptr(), eps, *ptrs,
+        ctypes.addressof(scale_arr) if scale_arr is not None else None,
+        ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
+        *dims, _ACT_CODES[x.dtype], w_code, flags,
+        workspace.data_ptr(), workspace.numel(), _stream(dev))))
+    del holders, gain
     return out
 
 

@@ -236,6 +236,51 @@ def test_decode_layer_workspace_reuse(gpu, shape, Ts):
         assert not any(_tile_counters(ws)), T
 
 
+def test_shared_workspace_across_calls(gpu):
+    """Calls without a workspace share one per (device, stream), grown on
+    demand: decode, prefill and decode again on it, every result the
+    oracle's, its barrier words consistent."""
+    from svdmlp import ops
+
+    ops.clear_workspace_cache()
+    shape = inputs.LayerShape(1024, 2048, 512)
+    x, f = inputs.make_layer(shape, T=300, seed=91)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    for T in (8, 300, 8, 64):
+        y = _np(ops.svd_mlp(t[0][:T].contiguous(), *t[1:]))
+        assert _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16")) < BF16_TOL, T
+    (ws,) = ops._WS_CACHE.values()
+    assert ws.numel() >= ops._lib.workspace_bytes(300, shape.d, shape.ff, shape.r, ops._lib.SVDMLP_BF16)
+    assert _barrier_state(ws)[1] == 0 and not any(_tile_counters(ws))
+    ops.clear_workspace_cache()
+    assert not ops._WS_CACHE
+
+
+def test_prepared_layer_cache(gpu):
+    """A layer called again reuses its prepared arguments (the same result:
+    split-K partial sums are combined in arrival order, so bf16 roundings may
+    differ by an ulp); layers whose factors the host mirror copies (gate and
+    up with different row pitches) are not kept."""
+    from svdmlp import ops
+
+    ops._PLANS.clear()
+    shape = inputs.LayerShape(1024, 2048, 512)
+    x, f = inputs.make_layer(shape, T=8, seed=95)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    y1 = ops.svd_mlp(*t).clone()
+    assert len(ops._PLANS) == 1
+    y2 = ops.svd_mlp(*t)
+    assert _rel(_np(y2), _np(y1)) < 5e-3
+    assert _rel(_np(y2), O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
+    mixed = list(t[1:])
+    mixed[0], mixed[2] = ops.pad_rows(t[1], 8), ops.pad_rows(t[3], 16)
+    y3 = _np(ops.svd_mlp(t[0], *mixed))
+    assert len(ops._PLANS) == 1
+    assert _rel(y3, O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
+
+
 @pytest.mark.parametrize("T", [1, 2])
 def test_gemv_decode_layer_ragged_strips(gpu, T):
     """Streaming-GEMV layer on a shape whose column counts cut its 256- and
