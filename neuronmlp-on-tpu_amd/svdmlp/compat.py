@@ -30,6 +30,7 @@ MFMA, i.e. at least the precision of either reference mode).
 
 from __future__ import annotations
 
+import functools
 from typing import NamedTuple
 
 import numpy as np
@@ -127,7 +128,24 @@ def _check_vmem(estimate: int) -> None:
 
 
 def _fusion_shape(M, r, K, N, dtype, M_count, r_count, K_count, N_count, gate, async_dma=True) -> FusionShape:
-    """test_speedup.py:267-299: validate block counts, pad, check VMEM."""
+    """test_speedup.py:267-299: validate block counts, pad, check VMEM.  The
+    plan is a pure function of its arguments and is remembered per argument
+    tuple (the launchers validate on every call); a failing check raises
+    every time."""
+    try:
+        return _fusion_shape_cached(M, r, K, N, dtype, M_count, r_count, K_count, N_count, gate, async_dma)
+    except TypeError as exc:  # unhashable arguments: plan without the cache
+        if "unhashable" not in str(exc):
+            raise
+        return _fusion_shape_plan(M, r, K, N, dtype, M_count, r_count, K_count, N_count, gate, async_dma)
+
+
+@functools.lru_cache(maxsize=4096)
+def _fusion_shape_cached(M, r, K, N, dtype, M_count, r_count, K_count, N_count, gate, async_dma):
+    return _fusion_shape_plan(M, r, K, N, dtype, M_count, r_count, K_count, N_count, gate, async_dma)
+
+
+def _fusion_shape_plan(M, r, K, N, dtype, M_count, r_count, K_count, N_count, gate, async_dma) -> FusionShape:
     for name, value in zip(("M_tiles_in_block", "r_tiles_in_block", "K_tiles_in_block", "N_tiles_in_block"),
                            (M_count, r_count, K_count, N_count)):
         _positive(name, value)
