@@ -17,7 +17,7 @@ The JSON line also carries:
   cpu_baseline  the numpy oracle (oracle/reference_cpu.py) timed on this
                 host's cores on a bounded row sample of the same layer
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 100]
 """
 
 from __future__ import annotations
@@ -44,8 +44,10 @@ D, FF, R = 4096, 14336, 2816
 def _args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    # the clocks take some tens of milliseconds of load to settle: with 5
+    # warmup steps the 8B layer timed ~375 us, after ~60 steps ~343 us
+    p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--tokens", type=int, default=1024)
     p.add_argument("--layers", type=int, default=4, help="synthetic layers the steps rotate over")
     p.add_argument("--decode-steps", type=int, default=200)
@@ -376,7 +378,7 @@ def main(argv=None) -> int:
             def dstep(i, xd=xd, wsd=wsd, outd=outd):
                 svdmlp.svd_mlp(xd, *layers[i % len(layers)], workspace=wsd, out=outd)
 
-            msd, _ = _time_steps(torch, dstep, args.decode_steps, 10, stream)
+            msd, _ = _time_steps(torch, dstep, args.decode_steps, max(10, args.warmup), stream)
             with _lib.StageProfile() as prof:
                 _time_steps(torch, dstep, min(args.decode_steps, 50), 0, stream)
             nbytes = factor_bytes + 2 * Td * D * 2
@@ -398,7 +400,7 @@ def main(argv=None) -> int:
         if args.only == "decode":
             t1 = dec.get("T=1") or next(iter(dec.values()))
             record.update({"metric": METRIC, "value": t1["GB/s"], "unit": "GB/s", "n_gpus": 1,
-                           "steps": args.decode_steps, "warmup": 10, "ms_per_step": t1["us_per_layer"] / 1e3,
+                           "steps": args.decode_steps, "warmup": max(10, args.warmup), "ms_per_step": t1["us_per_layer"] / 1e3,
                            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
                            "data": "synthetic", "config": {"workload": "LLaMA3-8B SVD-MLP layer, decode"}})
     if args.only in (None, "stack"):
