@@ -183,6 +183,8 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
     }
     if (rr == r) break;
   }
+  // gate/up XU.V passes at one row tile split K in two (big_swiglu)
+  if (T <= 256) part = std::max(part, (int64_t)2 * 256 * ((ff + 127) / 128 * 128) * 4);
   std::lock_guard<std::mutex> lk(mu);
   if (memo.size() > 4096) memo.clear();
   memo[key] = part;
@@ -363,6 +365,7 @@ struct Tune {
   int split = 256;    // CUs assumed by the split-K planner
   bool big = true;    // large-tile path enabled
   bool dlayer = true; // persistent decode layer enabled
+  bool gusplit = true; // split-K gate/up XU.V passes at one row tile
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -390,6 +393,7 @@ const Tune& tune() {
         if (k == "split") r.split = v;
         if (k == "big") r.big = v != 0;
         if (k == "dlayer") r.dlayer = v != 0;
+        if (k == "gusplit") r.gusplit = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -555,8 +559,8 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
 // out = SiLU(XUg . Vg) * (XUu . Vu): a g pass (bf16 g to the workspace) and a
 // u pass whose epilogue applies SiLU(g) * u.
 int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, const void* vg, const void* vu,
-               bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, const float* s_vg = nullptr,
-               const float* s_vu = nullptr, int64_t ldv = 0) {
+               bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, float* part, int64_t part_cap,
+               const float* s_vg = nullptr, const float* s_vu = nullptr, int64_t ldv = 0) {
   int fn = tune().s2fn;
   // 256 x 224 tiles (fn 7) leave most CUs idle at one or two 256-row tiles
   // of tokens; 256 x 128 tiles (fn 4) double the block count there (8B
@@ -565,6 +569,30 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   if (fn == 0) fn = (T <= 512 && ff % 128 == 0) ? 4 : ((ff % 224 == 0) ? 7 : 8);
   const int64_t ldb = v_lin ? r : (ldv ? ldv : ff);
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? ff : r) * ldb * wbytes(c);
+  // One row tile of 256 x 128 tiles: each block streams its whole V column
+  // panel, so the passes run at the panel's stream rate per block (8B layer,
+  // T=256: 62 us for the g pass); two K splits put twice the blocks on the
+  // V stream, and the fp32 slices are summed into g (fragment order) and,
+  // with SiLU(g) applied, into h.
+  const int64_t per = (int64_t)256 * ((ff + 127) / 128 * 128);  // floats of one slice
+  if (T <= 256 && fn == 4 && r >= 64 && tune().gusplit && 2 * per * 4 <= part_cap) {
+    const int ks = (r / 2 + 31) / 32 * 32, splits = (r + ks - 1) / ks;
+    int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
+                      BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
+    if (rc) return rc;
+    {
+      StageScope fin(ST_FINALIZE, c.st);
+      if ((rc = check(launch_reduce_bf16(part, splits, per, gbuf, per, c.st), "split-K reduce"))) return rc;
+    }
+    rc = big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
+                  BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
+    if (rc) return rc;
+    StageScope fin(ST_FINALIZE, c.st);
+    return check(launch_reduce_frag_bf16(part, splits, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff, T,
+                                         ff, 1, (int)(per / 256 / 128), fn, big_nw(fn, BEPI_STORE, v_lin), 1, c.st,
+                                         gbuf),
+                 "split-K SwiGLU reduce");
+  }
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,
                     1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
   if (rc) return rc;
@@ -927,7 +955,8 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
     if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L, fp8 ? sus : nullptr))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
-    return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h, fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr);
+    return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h, reinterpret_cast<float*>(ws + L.part),
+                      (int64_t)(L.norm - L.part), fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr);
   }
 
   const Operand ax{x, nullptr, d};
@@ -1142,7 +1171,9 @@ int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void*
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
-    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf, S[1], S[3], ld.v))) return rc;
+    if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf,
+                         reinterpret_cast<float*>(ws + L.part), (int64_t)(L.norm - L.part), S[1], S[3], ld.v)))
+      return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};
     if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) return rc;

@@ -77,10 +77,11 @@ hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint1
 // Split-K slices of the large-tile kernel in fragment order (out_frag):
 // out[m][n] = bf16(sum_s in[s * sstride + zb * bstride + frag(m, n)]) for
 // tiles of 256 x 32*fn with nw waves, batch entries zb (out batch stride
-// obstride elements).
+// obstride elements); with `gate` (bf16 in the same fragment order),
+// out = bf16(SiLU(gate) * sum).
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
-                                   int batch, hipStream_t st);
+                                   int batch, hipStream_t st, const uint16_t* gate = nullptr);
 hipError_t launch_finalize(const float* g, const float* u, int64_t ldi, uint16_t* out, int64_t ldo, int rows,
                            int cols, bool swiglu, bool out_t, hipStream_t st);
 

@@ -52,7 +52,8 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
 template <int FM, int FN>
 __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, int splits, int64_t sstride,
                                                                int64_t bstride, uint16_t* out, int64_t ldo,
-                                                               int64_t obstride, int M, int N, int mtiles, int nw) {
+                                                               int64_t obstride, int M, int N, int mtiles, int nw,
+                                                               const uint16_t* gate) {
   constexpr int ROWS = 16 * FM, COLS = 16 * FN, PITCH = COLS + 8;  // staged row pitch (elements)
   constexpr int Q = FM * FN * 64;                                   // float4s per wave tile
   __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS * PITCH];
@@ -73,6 +74,17 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
 #pragma unroll
     for (int k = 0; k < PER; ++k) a[k] += b[k];
   }
+  if (gate) {  // SwiGLU: out = SiLU(g) * sum, g bf16 in the same fragment order
+    const uint16_t* gp = gate + (int64_t)zb * bstride + (int64_t)unit * Q * 4 + 4 * threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const u32x2 g = *reinterpret_cast<const u32x2*>(gp + 1024 * k);
+      a[k].x *= silu_f32(bf16_bits_to_f32(g.x & 0xffffu));
+      a[k].y *= silu_f32(bf16_bits_to_f32(g.x >> 16));
+      a[k].z *= silu_f32(bf16_bits_to_f32(g.y & 0xffffu));
+      a[k].w *= silu_f32(bf16_bits_to_f32(g.y >> 16));
+    }
+  }
 #pragma unroll
   for (int k = 0; k < PER; ++k) {
     const int q = threadIdx.x + 256 * k, fi = q >> 6, l = q & 63;
@@ -91,9 +103,10 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
 
 template <int FM, int FN>
 hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out, int64_t ldo,
-                     int64_t obstride, int M, int N, int mtiles, int ntiles, int nw, int batch, hipStream_t st) {
+                     int64_t obstride, int M, int N, int mtiles, int ntiles, int nw, int batch, const uint16_t* gate,
+                     hipStream_t st) {
   hipLaunchKernelGGL((reduce_frag_bf16_kernel<FM, FN>), dim3(mtiles * ntiles * nw, batch), dim3(256), 0, st, in,
-                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw);
+                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw, gate);
   return hipGetLastError();
 }
 
@@ -101,10 +114,10 @@ hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstri
 
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
-                                   int batch, hipStream_t st) {
-  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, st);
-  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, st);
-  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, st);
+                                   int batch, hipStream_t st, const uint16_t* gate) {
+  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
+  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
+  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
   return hipErrorInvalidValue;
 }
 
