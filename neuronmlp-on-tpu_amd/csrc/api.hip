@@ -183,8 +183,8 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
     }
     if (rr == r) break;
   }
-  // gate/up XU.V passes at one row tile split K in two (big_swiglu)
-  if (T <= 256) part = std::max(part, (int64_t)2 * 256 * ((ff + 127) / 128 * 128) * 4);
+  // gate/up XU.V passes at one or two row tiles split K in two (big_swiglu)
+  if (T <= 512) part = std::max(part, (int64_t)2 * ((T + 255) / 256 * 256) * ((ff + 255) / 256 * 256) * 4);
   std::lock_guard<std::mutex> lk(mu);
   if (memo.size() > 4096) memo.clear();
   memo[key] = part;
@@ -574,8 +574,16 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   // T=256: 62 us for the g pass); two K splits put twice the blocks on the
   // V stream, and the fp32 slices are summed into g (fragment order) and,
   // with SiLU(g) applied, into h.
-  const int64_t per = (int64_t)256 * ((ff + 127) / 128 * 128);  // floats of one slice
-  if (T <= 256 && fn == 4 && r >= 64 && tune().gusplit && 2 * per * 4 <= part_cap) {
+  // Two nearly full row tiles (448 < T <= 512): 256 x 256 tiles (whole
+  // 512-byte V rows per DMA instruction) in the same 224 blocks, each
+  // streaming half of K (T=512: 261 -> 249 us); with a mostly padded second
+  // row tile the padding costs more than the split gains (T=320: 208 -> 224,
+  // T=384: 221 -> 233 us).
+  const int sfn = T <= 256 ? 4 : 8;
+  const int64_t per = (int64_t)((T + 255) / 256 * 256) * ((ff + 32 * sfn - 1) / (32 * sfn) * (32 * sfn));
+  if ((T <= 256 || (T > 448 && T <= 512 && ff % 256 == 0)) && fn == 4 && r >= 64 && tune().gusplit &&
+      2 * per * 4 <= part_cap) {
+    fn = sfn;
     const int ks = (r / 2 + 31) / 32 * 32, splits = (r + ks - 1) / ks;
     int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
                       BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
@@ -588,9 +596,10 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
                   BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
+    const int mt = (T + 255) / 256;
     return check(launch_reduce_frag_bf16(part, splits, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff, T,
-                                         ff, 1, (int)(per / 256 / 128), fn, big_nw(fn, BEPI_STORE, v_lin), 1, c.st,
-                                         gbuf),
+                                         ff, mt, (int)(per / (256 * mt) / (32 * fn)), fn, big_nw(fn, BEPI_STORE, v_lin), 1,
+                                         c.st, gbuf),
                  "split-K SwiGLU reduce");
   }
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,
