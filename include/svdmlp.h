@@ -26,7 +26,14 @@
  *   - Return value: 0 on success; SVDMLP_EINVAL for an invalid argument (the
  *     message is available from svdmlp_last_error(), thread-local); SVDMLP_EHIP
  *     for a HIP runtime error.
- *   - Calls on different streams with distinct workspaces may run concurrently.
+ *   - Decode shapes (1 to 128 tokens, bf16) run as one persistent launch of
+ *     one block per CU whose phases meet at grid barriers; it needs the whole
+ *     device.  Do not run it concurrently with other work on the device
+ *     (another stream, another process): blocks that cannot become resident
+ *     stall the barriers, whose bounded waits then give up.  A call whose
+ *     wait gave up writes NaN into y wherever the result could be incomplete
+ *     and records the timeout in the workspace (svdmlp_workspace_status).
+ *     Calls on one stream, or on streams ordered by events, are safe.
  */
 #ifndef SVDMLP_H
 #define SVDMLP_H
@@ -68,15 +75,30 @@ const char* svdmlp_last_error(void);
  * same workspace may be reused by consecutive calls on one stream of one
  * device.  Its first 4096 bytes must be zero before its first use: they hold
  * the grid-barrier and block-done counters of the persistent decode kernels
- * (the streaming-GEMV layer at 1-4 tokens and the MFMA layer above), which
- * only ever grow, and the MFMA layer's split-K tile counters (from byte
- * 2560), which every call leaves at zero.  The 64-bit word at byte 2304
- * becomes nonzero only if a barrier timed out (the call's output is then
- * undefined and the 4 KB must be zeroed again).
+ * (the streaming-GEMV layer at 1-2 tokens and the MFMA layer up to 128),
+ * which only ever grow, and the MFMA layer's split-K tile counters (from byte
+ * 2560), which every call leaves at zero.  The 64-bit word at byte 2304 is
+ * the timeout flag (see svdmlp_workspace_status); a nonzero 32-bit value at
+ * byte 2312 replaces the default bound of the barrier waits (in polls of
+ * about a microsecond; failure tests set a tiny one).
  * Replaces the VMEM planning of test_speedup.py:208-258 (the TPU kernels keep
  * XU in VMEM scratch; here the rank-r intermediate lives in this buffer).
  */
 size_t svdmlp_workspace_bytes(int64_t T, int64_t d, int64_t ff, int64_t r, int32_t w_dtype);
+
+/*
+ * Timeout status of a workspace's persistent decode kernels (no counterpart
+ * in the reference, whose kernels have no cross-block waits).  Returns 1 if a
+ * grid-barrier wait of an earlier call on this workspace gave up (those calls
+ * wrote NaN into y wherever their result could be incomplete; the flag stays
+ * set, and later decode calls write NaN too, until reset), 0 if none did, or a
+ * negative status.  Waits for `stream` (a hipStream_t) first.  With reset
+ * nonzero it then zeroes the 4096-byte sync area (stream-ordered), which makes
+ * the workspace usable again; no call may be in flight on the workspace then.
+ * The reference rejects non-finite layer outputs (test_speedup.py:852-853,
+ * bench/checkpoint_speedup.py:24-25); this names the cause.
+ */
+int svdmlp_workspace_status(void* workspace, size_t ws_bytes, int32_t reset, void* stream);
 
 /*
  * Fused Gate/Up with the SwiGLU epilogue:

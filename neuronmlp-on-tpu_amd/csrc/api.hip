@@ -1,15 +1,23 @@
 // C ABI of libsvdmlp.so (declared in include/svdmlp.h).
 //
-// Stage plans
-//   prefill (T > 64, or shapes the decode kernels do not take):
-//     XU    = X . U                 tiled MFMA GEMM; split-K with fp32 atomics
-//                                   when there are too few output tiles
-//     h     = SiLU(XUg.Vg)*(XUu.Vu) dual-branch GEMM, SwiGLU epilogue
-//     y     = (h . Ud) . Vd         the same two GEMM kinds
-//   decode (bf16 activations, T <= 64, aligned shapes):
-//     zero fp32 accumulators -> X.[Ug|Uu] -> XU.[Vg|Vu] -> SwiGLU(g,u).Ud -> .Vd
-//     every stage streams its factor once from HBM (split-K, fp32 atomics);
-//     h is formed on the fly from the fp32 gate/up sums and never stored.
+// Kernel choice per call (svdmlp_svd_mlp and its variants):
+//   1-2 tokens, dense bf16 factors:  one streaming-GEMV layer launch
+//                                    (decode_gemv.hpp)
+//   1-128 tokens, bf16, aligned:     one persistent MFMA decode-layer launch
+//                                    (decode_layer.hpp): four phases, three
+//                                    grid barriers, split-K tiles combined by
+//                                    the last-arriving unit in split order
+//   more tokens, bf16/fp8, aligned:  the large-tile MFMA GEMM (gemm_big.hpp)
+//                                    X.[Ug|Uu] -> g pass -> u pass with the
+//                                    SwiGLU epilogue -> h.Ud -> XUd.Vd; stages
+//                                    with too few output tiles split K into
+//                                    fp32 slices summed in split order
+//   anything else (fp32, Linear-layout or transposed operands, odd sizes):
+//                                    the general 128x128 GEMM (gemm.hpp) and
+//                                    the per-stage decode kernels (decode.hpp),
+//                                    whose split-K sums use fp32 atomics
+// Every buffer, including the workspace that holds the rank-r intermediates,
+// h and the split-K slices, is owned by the caller.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -899,6 +907,20 @@ int svdmlp_profile_read(double* total_ms, int64_t* launches, int n) {
     g_prof.count[i] = 0;
   }
   return rc == SVDMLP_OK ? ST_COUNT : rc;
+}
+
+int svdmlp_workspace_status(void* workspace, size_t ws_bytes, int32_t reset, void* stream) {
+  g_err.clear();
+  if (!workspace) return fail("null pointer argument");
+  if (ws_bytes < 4096) return fail("workspace too small: the sync area alone is 4096 bytes, got %zu", ws_bytes);
+  hipStream_t st = (hipStream_t)stream;
+  uint64_t flag = 0;
+  int rc = check(hipMemcpyAsync(&flag, static_cast<char*>(workspace) + kDlFlag * 8, 8, hipMemcpyDeviceToHost, st),
+                 "workspace status read");
+  if (!rc) rc = check(hipStreamSynchronize(st), "workspace status read");
+  if (!rc && reset) rc = check(launch_fill_zero(static_cast<float*>(workspace), 4096 / 4, st), "sync area reset");
+  if (rc) return rc;
+  return flag ? 1 : 0;
 }
 
 size_t svdmlp_workspace_bytes(int64_t T, int64_t d, int64_t ff, int64_t r, int32_t w_dtype) {

@@ -176,8 +176,11 @@ __device__ __forceinline__ u32x4 gv_issue(const GvPhase& P, GvCursor& c, int lro
 
 // Activation rows of a block's group range into LDS: a_lds[i * T + t] is
 // token t of local row i (group i / GROUP, row i % GROUP of it).  Phase 1
-// reads X (bf16); 2 the gate/up rank sums; 3 h = bf16(SiLU(G) * U); 4 the
-// down rank sums (device-scope loads of other blocks' atomics).  Loads go
+// reads X (bf16); 2 the gate/up rank sums rounded to bf16; 3
+// h = bf16(SiLU(G) * U); 4 the down rank sums rounded to bf16 (device-scope
+// loads of other blocks' atomics).  The rank-r intermediates are rounded as
+// the MFMA decode layer and the prefill path round them (the reference casts
+// XU to the activation dtype, test_speedup.py:430-437).  Loads go
 // out in batches of SB per thread before any is used; lanes past the end
 // load element 0 and discard it, so no branch splits a batch.
 template <int PH, int T, int RW>
@@ -215,8 +218,10 @@ __device__ __forceinline__ void gv_stage(const GvParams& p, const GvPhase& P, in
       if (i < total) {
         if constexpr (PH == 3)
           a_lds[i] = bf16_bits_to_f32(f32_to_bf16_bits(silu_f32(v[q]) * v2[q]));
-        else
+        else if constexpr (PH == 1)
           a_lds[i] = v[q];
+        else
+          a_lds[i] = bf16_bits_to_f32(f32_to_bf16_bits(v[q]));
       }
     }
   }
@@ -236,6 +241,9 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
   const bool writer = RW == 1 || lane < 32;                  // holds the wave's column sums after the fold
   uint32_t nbar = 0;
   const uint64_t gen0 = __hip_atomic_load(&p.sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t spin = dl_spin_limit(p.sync);
+  __shared__ int s_bad;  // a barrier wait of this block gave up (the done counter carries it to the last block)
+  if (threadIdx.x == 0) s_bad = 0;
   const int64_t gtid = (int64_t)b * kGvThreads + threadIdx.x, gstride = (int64_t)G * kGvThreads;
 
   auto range = [&](const GvPhase& P, int& g0, int& n) {
@@ -259,7 +267,7 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
     for (int u = 0; u < D; ++u) ring[u] = gv_issue<RW>(P1, ic, lrow, lcol);
   }
   dl_wait_vm<D>();  // the zero stores, issued before the D loads, are done
-  dl_grid_sync(p.sync, gen0, ++nbar);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, &s_bad);
 
 #pragma unroll 1
   for (int ph = 1; ph <= 4; ++ph) {
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
     if (after_flush >= 1)
       gv_wait_after<0>(after_flush - 1);
     ic = nc;
-    if (ph < 4) dl_grid_sync(p.sync, gen0, ++nbar);
+    if (ph < 4) dl_grid_sync(p.sync, gen0, ++nbar, spin, &s_bad);
   }
   // drain the run-out loads (no records) before the registers are released
 #pragma unroll
@@ -386,16 +394,21 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
 
   // ---- phase 5: the last block to finish phase 4 writes y = bf16(Y32) ----
   // Every wave has waited for its own atomics; a block counts itself done
-  // once all of its waves have.
+  // once all of its waves have.  A block whose barrier wait gave up set
+  // kGvDoneBad before its own arrival, so the last arrival sees it and
+  // writes NaN instead (the sums may be incomplete).
   __shared__ int s_last;
   dl_block_sync();
   if (threadIdx.x == 0) {
     const uint64_t done =
         __hip_atomic_fetch_add(&p.sync[kGvDone], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
-    s_last = done % (uint64_t)G == 0;
+    s_last = ((done & ~kGvDoneBad) % (uint64_t)G == 0) ? ((done & kGvDoneBad) ? 2 : 1) : 0;
   }
   dl_block_sync();
-  if (s_last) {
+  if (s_last == 2) {
+    uint32_t* yw = reinterpret_cast<uint32_t*>(p.y);
+    for (int64_t i = threadIdx.x; i < (int64_t)p.T * p.d / 2; i += kGvThreads) yw[i] = 0x7fc07fc0u;  // bf16 NaN pairs
+  } else if (s_last) {
     constexpr int SB = 8;
     const int64_t n = (int64_t)p.T * p.d / 2;
     for (int64_t i0 = threadIdx.x; i0 < n; i0 += SB * kGvThreads) {

@@ -43,8 +43,14 @@
 // counters only ever grow: a launch reads the generation at its start and
 // waits for start + k at barrier k, and group / root completion is taken
 // modulo the group size, so no reset is needed as long as every launch on a
-// workspace uses the same grid.  Polls are bounded; on timeout a flag is set
-// and the kernel runs to its end.
+// workspace uses the same grid.  Polls are bounded.  A block whose wait
+// gives up sets the workspace's timeout flag, remembers it, and runs to its
+// end with whatever data it finds (every access stays in bounds, and every
+// block still arrives once at every barrier, so the counters stay
+// consistent); whoever writes y then writes NaN instead wherever the data
+// could be incomplete: a block that timed out itself, and every split-K
+// combination that finds the flag set after its last slice arrived (any
+// incomplete input reached it only after the flag was set).
 #pragma once
 
 #include "gemm_big.hpp"
@@ -77,17 +83,26 @@ constexpr int kDlThreads = 512;
 // slice area holds kDlMaxGrid units.
 constexpr int kDlMaxGrid = 256;
 constexpr int kDlWStage = 8192;    // 32 k x 128 columns bf16
+// Default bound of a grid-barrier wait, in polls (~1 us each with the
+// device-scope load): seconds, far beyond any barrier of a resident grid.
 constexpr uint32_t kDlSpinLimit = 1u << 22;
 // Barrier words in the workspace's sync area, one 128-byte line each (in
-// uint64 units): kDlGroups group counters, then root, generation, timeout.
+// uint64 units): kDlGroups group counters, then root, generation, and the
+// timeout line: word kDlFlag is nonzero once a bounded wait gave up (sticky
+// until the caller zeroes the area), word kDlSpin, if nonzero, replaces
+// kDlSpinLimit (failure tests set a tiny bound so that waits give up at once).
 constexpr int kDlGroups = 16;
 constexpr int kDlLine = 16;
 constexpr int kDlRoot = kDlGroups * kDlLine;
 constexpr int kDlGen = kDlRoot + kDlLine;
 constexpr int kDlFlag = kDlGen + kDlLine;
+constexpr int kDlSpin = kDlFlag + 1;
 // Block-done counter of the streaming-GEMV decode layer (monotone, like the
-// barrier counters: the last of every G arrivals finishes the launch).
+// barrier counters: the last of every G arrivals finishes the launch); bit
+// kGvDoneBad is set with the timeout flag, so the last block learns of a
+// timeout from its own arrival.
 constexpr int kGvDone = kDlFlag + kDlLine;
+constexpr uint64_t kGvDoneBad = (uint64_t)1 << 63;
 // 32-bit arrival counters of the split-K tiles of phases 1, 3 and 4 (in
 // that order) fill the rest of the 4 KB area, kDlTileLines 128-byte lines.
 // Tile t's counter is word t / kDlTileLines of line t % kDlTileLines, so
@@ -135,9 +150,18 @@ __device__ __forceinline__ void dl_wait_vm() {
 // wave's vmcnt wait) without a global-memory fence.
 __device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Bound of this launch's barrier waits: the workspace's override, if set.
+__device__ __forceinline__ uint32_t dl_spin_limit(uint64_t* sync) {
+  const uint64_t o = __hip_atomic_load(&sync[kDlSpin], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return o ? (uint32_t)o : kDlSpinLimit;
+}
+
 // Grid barrier k of this launch (gen0: generation at launch start).  Every
-// wave has completed its own global writes (vmcnt(0)) before calling.
-__device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k) {
+// wave has completed its own global writes (vmcnt(0)) before calling.  If
+// the wait gives up, thread 0 sets the timeout flag (and the GEMV layer's
+// done bit), waits for both to complete, and sets *bad (LDS) for the block;
+// *bad is never cleared within a launch.
+__device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k, uint32_t spin, int* bad) {
   dl_block_sync();
   if (threadIdx.x == 0) {
     const uint32_t G = gridDim.x, b = blockIdx.x;
@@ -153,8 +177,11 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
     uint32_t polls = 0;
     while ((int64_t)(__hip_atomic_load(&sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - gen0 - k) < 0) {
       __builtin_amdgcn_s_sleep(1);
-      if (++polls >= kDlSpinLimit) {
+      if (++polls >= spin) {
         __hip_atomic_fetch_or(&sync[kDlFlag], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(&sync[kGvDone], kGvDoneBad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        dl_wait_vm<0>();  // both flags complete before anything this block writes next
+        *bad = 1;
         break;
       }
     }
@@ -224,7 +251,8 @@ struct DlLds {
   static constexpr int W_OFF = 0;
   static constexpr int A_OFF = NS * W_SLOT;
   static constexpr int DUMMY_OFF = A_OFF + NS * A_SLOT;
-  static constexpr int FLAG_OFF = DUMMY_OFF + 1024;  // one int: "this block finishes the tile"
+  static constexpr int FLAG_OFF = DUMMY_OFF + 1024;  // int: "this block finishes the tile"
+  static constexpr int BAD_OFF = FLAG_OFF + 4;       // int: "a barrier wait of this block gave up"
   static constexpr int BYTES = FLAG_OFF + 16;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
@@ -364,13 +392,20 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
 //  * otherwise the unit stores its rows < T as slice u (16 bytes per lane
 //    and block mt, in register order) and, once every wave's stores have
 //    completed, counts its arrival on the tile's counter; the block that
-//    completes the count adds the other splits' slices to its registers (eight
-//    slices in flight at a time), resets the counter and rounds to dst.
+//    completes the count resets the counter and sums the splits' slices in
+//    split order, 0 + s_0 + s_1 + ..., its own from registers (the values
+//    it stored), so the result does not depend on which unit came last;
+//    then it rounds to dst.
+// `out_y`: dst is the layer output; it receives NaN instead if this block
+// gave up a barrier wait (`bad`) or, after the last arrival, the timeout
+// flag is set.
 // Units of a split phase never exceed the grid (at most one per block).
 template <int MT>
 __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x4 (&acc)[MT], int u, int nt,
-                                           int splits, uint32_t* cnt, float* slices, int* flag, uint16_t* dst) {
+                                           int splits, uint32_t* cnt, float* slices, int* flag, uint16_t* dst,
+                                           bool out_y, bool bad, uint64_t* sync) {
   const int n = U.n0 + 64 * (c.wave >> 2) + 16 * (c.wave & 3) + 4 * c.lg;
+  bool poison = out_y && bad;
   if (splits > 1) {
     // Slices move as one 16-byte device-scope (sc1) buffer access per lane
     // and 16-row block; rows >= T take an offset past the records, which
@@ -394,8 +429,13 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
     }
     dl_block_sync();
     if (!*flag) return;
+    // issued with the first slices, after every split's arrival was seen
+    const uint64_t tflag = out_y ? __hip_atomic_load(&sync[kDlFlag], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
     const int split = u / nt, tile = u - split * nt;
     constexpr int SB = MT >= 8 ? 2 : 8;  // slices in flight (registers: SB * MT * 4)
+    f32x4 sum[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) sum[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < splits; s0 += SB) {
       u32x4 v[SB][MT];
 #pragma unroll
@@ -410,22 +450,32 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
         }
       }
 #pragma unroll
-      for (int i = 0; i < SB; ++i)
+      for (int i = 0; i < SB; ++i) {
+        const int s = s0 + i;
+        if (s < splits) {
+          const bool own = s == split;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          acc[mt].x += __uint_as_float(v[i][mt].x);
-          acc[mt].y += __uint_as_float(v[i][mt].y);
-          acc[mt].z += __uint_as_float(v[i][mt].z);
-          acc[mt].w += __uint_as_float(v[i][mt].w);
+          for (int mt = 0; mt < MT; ++mt) {
+            sum[mt].x += own ? acc[mt].x : __uint_as_float(v[i][mt].x);
+            sum[mt].y += own ? acc[mt].y : __uint_as_float(v[i][mt].y);
+            sum[mt].z += own ? acc[mt].z : __uint_as_float(v[i][mt].z);
+            sum[mt].w += own ? acc[mt].w : __uint_as_float(v[i][mt].w);
+          }
         }
+      }
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = sum[mt];
+    poison = poison || tflag != 0;
   }
+  constexpr uint32_t kNaN2 = 0x7fc07fc0u;  // two bf16 quiet NaNs
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + c.lr;
     if (m < c.T)
       dl_store8(dst + (int64_t)m * U.ldo + n,
-                u32x2{dl_pack_bf16x2(acc[mt].x, acc[mt].y), dl_pack_bf16x2(acc[mt].z, acc[mt].w)});
+                poison ? u32x2{kNaN2, kNaN2}
+                       : u32x2{dl_pack_bf16x2(acc[mt].x, acc[mt].y), dl_pack_bf16x2(acc[mt].z, acc[mt].w)});
   }
 }
 
@@ -442,6 +492,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   c.lg = c.lane >> 4;
   c.T = p.T;
   int* const flag = reinterpret_cast<int*>(lds + L::FLAG_OFF);
+  int* const bad = reinterpret_cast<int*>(lds + L::BAD_OFF);
+  if (threadIdx.x == 0) *bad = 0;  // published by the block barriers ahead of its first read
   const int G = gridDim.x, b = blockIdx.x;
   const int T = p.T;
   constexpr int NS = L::NS;
@@ -449,6 +501,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // Generation at launch start: it cannot advance before every block has
   // arrived at barrier 1, which each block does only after this read.
   const uint64_t gen0 = __hip_atomic_load(&p.sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t spin = dl_spin_limit(p.sync);
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
@@ -533,11 +586,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(1, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, false, acc);
-    dl_combine<MT>(c, U, acc, u, nt1, p.splits1, dl_tile_counter(p.sync, u % nt1), p.slices, flag, U.dst);
+    dl_combine<MT>(c, U, acc, u, nt1, p.splits1, dl_tile_counter(p.sync, u % nt1), p.slices, flag, U.dst, false,
+                   false, p.sync);
   }
   dl_wait_vm<0>();
   prefetch(2);
-  dl_grid_sync(p.sync, gen0, ++nbar);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, bad);
 
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
   for (int u = b; u < units[2]; u += G) {
@@ -569,7 +623,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(3);
-  dl_grid_sync(p.sync, gen0, ++nbar);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, bad);
 
   // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
   for (int u = b; u < units[3]; u += G) {
@@ -577,11 +631,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(3, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt3, p.splits3, dl_tile_counter(p.sync, nt1 + u % nt3), p.slices, flag, U.dst);
+    dl_combine<MT>(c, U, acc, u, nt3, p.splits3, dl_tile_counter(p.sync, nt1 + u % nt3), p.slices, flag, U.dst,
+                   false, false, p.sync);
   }
   dl_wait_vm<0>();
   prefetch(4);
-  dl_grid_sync(p.sync, gen0, ++nbar);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, bad);
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
   for (int u = b; u < units[4]; u += G) {
@@ -589,7 +644,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(4, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt4, p.splits4, dl_tile_counter(p.sync, nt1 + nt3 + u % nt4), p.slices, flag, U.dst);
+    dl_combine<MT>(c, U, acc, u, nt4, p.splits4, dl_tile_counter(p.sync, nt1 + nt3 + u % nt4), p.slices, flag, U.dst,
+                   true, *bad != 0, p.sync);
   }
 }
 

@@ -33,6 +33,7 @@ from .ops import (  # noqa: F401
     svd_mlp,
     svd_mlp_block,
     svd_mlp_workspace,
+    workspace_status,
 )
 
 __version__ = "1.0.0"

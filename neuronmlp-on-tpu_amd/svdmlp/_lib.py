@@ -33,6 +33,7 @@ EXPORTED = (
     "svdmlp_version",
     "svdmlp_last_error",
     "svdmlp_workspace_bytes",
+    "svdmlp_workspace_status",
     "svdmlp_gate_up",
     "svdmlp_xuv",
     "svdmlp_svd_mlp",
@@ -69,6 +70,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.svdmlp_last_error.argtypes = []
     lib.svdmlp_workspace_bytes.restype = _sz
     lib.svdmlp_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _i32]
+    lib.svdmlp_workspace_status.restype = ctypes.c_int
+    lib.svdmlp_workspace_status.argtypes = [_vp, _sz, _i32, _vp]
     lib.svdmlp_gate_up.restype = ctypes.c_int
     lib.svdmlp_gate_up.argtypes = [_vp] * 5 + [_vp] * 4 + [_vp] + [_i64] * 4 + [_i32, _i32, _u32, _vp, _sz, _vp]
     lib.svdmlp_xuv.restype = ctypes.c_int

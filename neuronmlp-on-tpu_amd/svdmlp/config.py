@@ -8,7 +8,6 @@ bench/speedup.py:123-133.
 
 from __future__ import annotations
 
-import math
 from typing import NamedTuple
 
 from .ops import low_rank_dim
@@ -59,25 +58,3 @@ XUV_ROW_TILE = 128
 XUV_INPUT_TILE = 1024
 XUV_RANK_TILE = 512
 XUV_OUTPUT_TILE = 1024
-
-# MI355X kernel tiles (block = 256 threads): prefill GEMM C tile and K step,
-# decode column tile.
-GEMM_TILE_M = 128
-GEMM_TILE_N = 128
-GEMM_TILE_K_BF16 = 64
-DECODE_TILE_N = 128
-DECODE_MAX_T = 64
-
-
-def lds_bytes_gate_up() -> int:
-    """LDS of one gate/up XUV block: 2 stages x 2 branches x (128 + 128) rows x 128 B."""
-    return 2 * 2 * (GEMM_TILE_M + GEMM_TILE_N) * 128
-
-
-def lds_bytes_xuv() -> int:
-    """LDS of one single-branch GEMM block."""
-    return 2 * 1 * (GEMM_TILE_M + GEMM_TILE_N) * 128
-
-
-def padded(n: int, tile: int) -> int:
-    return math.ceil(n / tile) * tile

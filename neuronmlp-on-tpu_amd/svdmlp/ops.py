@@ -438,6 +438,25 @@ def svd_mlp_workspace(x: torch.Tensor, *, r: int, ff: int, w_code: int | None = 
     return _workspace(x.device, T, d, ff, r, code)
 
 
+def workspace_status(workspace: torch.Tensor | None = None, *, reset: bool = False) -> bool:
+    """True if a grid-barrier wait of the persistent decode kernels gave up
+    in an earlier call on ``workspace`` (those calls wrote NaN into y
+    wherever their result could be incomplete; the flag stays set until
+    reset).  Waits for the current stream.  ``reset`` then zeroes the
+    workspace's sync area, which makes it usable again.  Without a workspace,
+    checks (and resets) every workspace kept for calls that pass none."""
+    if workspace is None:
+        return any([workspace_status(ws, reset=reset) for ws in list(_WS_CACHE.values())])
+    if workspace.dtype != torch.uint8 or not workspace.is_cuda:
+        raise TypeError("workspace must be a uint8 CUDA tensor from svd_mlp_workspace")
+    lib = _lib.load()
+    rc = lib.svdmlp_workspace_status(workspace.data_ptr(), workspace.numel(), int(bool(reset)),
+                                     _stream(workspace.device))
+    if rc < 0:
+        _lib.check(rc)
+    return rc == 1
+
+
 # ---------------------------------------------------------------------------
 # Host helpers of kernels/reference.py
 # ---------------------------------------------------------------------------

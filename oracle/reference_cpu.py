@@ -30,6 +30,8 @@ Every function cites the reference lines it follows.  What pins each one
                        W = U.V with identity U.
   rmsnorm_ref ........ closed form on constant rows (output = gain*sign),
                        scale invariance, float64 brute force.
+  mlp_block_f64 ...... float64 triple-loop brute force of the whole block on a
+                       tiny shape; agrees with mlp_block_ref in float32.
   relative_l2 ........ hand-computed vectors; NaN rejection.
   factor_bytes ....... 311,427,072 B for the 8B layer at r=2816
                        (results/real_layer0_cpu.json:21; profiler test :20).
@@ -55,6 +57,7 @@ __all__ = [
     "unfused_reference",
     "rmsnorm_ref",
     "mlp_block_ref",
+    "mlp_block_f64",
     "relative_l2",
     "errors",
     "factor_bytes",
@@ -235,6 +238,20 @@ def mlp_block_ref(x, gain, factors, eps: float = 1e-5, dtype: str = "float32") -
     h = rmsnorm_ref(x, gain, eps, dtype)
     y = svd_mlp_ref(h, *factors, dtype=dtype)
     return _cast(np.asarray(x, F32) + y, dtype)
+
+
+def mlp_block_f64(x, gain, factors, eps: float = 1e-5) -> np.ndarray:
+    """The same block in float64 with no rounding anywhere (the exact math
+    that every bf16 implementation approximates): x + svd_mlp(rmsnorm(x)),
+    rmsnorm and silu as above.  Used to measure how far a bf16 chain drifts
+    from the exact one over many layers."""
+    x = np.asarray(x, np.float64)
+    ug, vg, uu, vu, ud, vd = (np.asarray(a, np.float64) for a in factors)
+    hn = np.asarray(gain, np.float64) * (x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps))
+    g = (hn @ ug) @ vg
+    u = (hn @ uu) @ vu
+    h = g / (1.0 + np.exp(-g)) * u
+    return x + (h @ ud) @ vd
 
 
 # ---------------------------------------------------------------------------

@@ -1,0 +1,104 @@
+"""BASELINE configs 4 and 5 at their full workloads, on the HIP path.
+
+Config 4: the 32-layer LLaMA3-8B MLP stack (T=4096, d=4096, ff=14336,
+per-branch ranks drawn from {2048, ..., 3072}, RMSNorm eps 1e-5, gains
+~U(0.9, 1.1), residual add), exactly as bench.py builds it.  Every layer is
+checked on a row subset against the oracle's block fed with the GPU's own
+input rows (rows are independent through RMSNorm, the MLP and the residual,
+so a row subset is an exact check of those rows): relative Frobenius error
+<= 1e-2 on the output and on the MLP part.  End to end, two correct bf16
+chains drift apart as their rounding differences pass through 32 residual
+blocks, so the whole-stack criterion compares both with the unrounded
+float64 chain: the GPU chain must be as close to it as the oracle's own bf16
+chain is (within 25%).
+
+Config 5: the LLaMA3-70B-shape layer (T=2048, d=8192, ff=28672, r=5632) with
+fp8 e4m3 factors and per-output-channel fp32 scales, bf16 activations, on a
+row subset, <= 3e-2 against the oracle's math on the dequantized factors.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from svdmlp import fp8, ops, stack
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 1e-2
+FP8_TOL = 3e-2
+D, FF = 4096, 14336
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+def test_config4_stack_32_layers_full_shape(gpu):
+    T, L = 4096, 32
+    layers = stack.make_stack(L, D, FF, seed=4, device=gpu)   # bench.py's stack (seed + 4, seed 0)
+    gx = torch.Generator(device=gpu)
+    gx.manual_seed(4000)
+    x = torch.randn(T, D, generator=gx, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+    ws = stack.stack_workspace(x, layers)
+    rows = np.r_[0, 1, 2, 1023, 2048, 4095, np.random.default_rng(4).choice(np.arange(3, 4095), 6, replace=False)]
+    idx = torch.from_numpy(rows).to(gpu)
+    x0 = _np(x[idx])
+    chain_orc, chain_f64 = x0.copy(), x0.astype(np.float64)
+    cur, bufs = x, (torch.empty_like(x), torch.empty_like(x))
+    worst = 0.0
+    for i, layer in enumerate(layers):
+        out = ops.svd_mlp_block(cur, layer.gain, *layer.factors, eps=1e-5, workspace=ws, out=bufs[i % 2])
+        xin, yout = _np(cur[idx]), _np(out[idx])
+        f = [_np(a) for a in layer.factors]
+        gain = layer.gain.cpu().numpy()
+        ref = O.mlp_block_ref(xin, gain, f, eps=1e-5, dtype="bfloat16")
+        e_y, e_mlp = O.relative_l2(yout, ref), O.relative_l2(yout - xin, ref - xin)
+        worst = max(worst, e_mlp)
+        assert e_y < BF16_TOL and e_mlp < BF16_TOL, (i, layer.ranks, e_y, e_mlp)
+        chain_orc = O.mlp_block_ref(chain_orc, gain, f, eps=1e-5, dtype="bfloat16")
+        chain_f64 = O.mlp_block_f64(chain_f64, gain, f, eps=1e-5)
+        cur = out
+    got = _np(cur[idx])
+    e_gpu = O.relative_l2(got, chain_f64.astype(np.float32))
+    e_orc = O.relative_l2(chain_orc, chain_f64.astype(np.float32))
+    print(f"config 4: worst per-layer MLP rel_l2 {worst:.3e}; after {L} layers vs float64: "
+          f"GPU {e_gpu:.3e}, oracle bf16 chain {e_orc:.3e}, GPU vs oracle chain {O.relative_l2(got, chain_orc):.3e}")
+    assert e_gpu <= 1.25 * e_orc, (e_gpu, e_orc)
+
+
+def _q(rows, cols, g, dev):
+    w = torch.randn(rows, cols, generator=g, device=dev, dtype=torch.float32) / math.sqrt(rows)
+    return fp8.quantize_per_channel(w)
+
+
+def _dequant(qf):
+    """The oracle's e4m3 decode (as a 256-entry table) times the scales."""
+    table = O.e4m3_decode(np.arange(256, dtype=np.uint8))
+    return table[qf.data.view(torch.uint8).cpu().numpy()] * qf.scale.cpu().numpy()[None, :]
+
+
+def test_config5_70b_fp8_full_shape(gpu):
+    T, d, ff, r = 2048, 8192, 28672, 5632
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)   # bench.py's fp8 layer (seed + 5, seed 0)
+    fs = [_q(d, r, g, gpu), _q(r, ff, g, gpu), _q(d, r, g, gpu), _q(r, ff, g, gpu), _q(ff, r, g, gpu), _q(r, d, g, gpu)]
+    x = torch.randn(T, d, generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
+    y = ops.svd_mlp(x, *fs)
+    h = ops.fused_gate_up(x, *fs[:4])
+    rows = np.r_[0, 1, 1024, 2047, np.random.default_rng(5).choice(np.arange(2, 2047), 8, replace=False)]
+    idx = torch.from_numpy(rows).to(gpu)
+    xs = _np(x[idx])
+    deq = [_dequant(f) for f in fs]
+    h_ref = O.fused_gate_up_ref(xs, *deq[:4], dtype="bfloat16")
+    e_h = O.relative_l2(_np(h[idx]), h_ref)
+    y_ref = O.fused_xuv_ref(h_ref, deq[4], deq[5], dtype="bfloat16")
+    e_y = O.relative_l2(_np(y[idx]), y_ref)
+    yd = ops.fused_xuv(h, *fs[4:])   # the down half as its own entry point, on the GPU's h
+    e_d = O.relative_l2(_np(yd[idx]), O.fused_xuv_ref(_np(h[idx]), deq[4], deq[5], dtype="bfloat16"))
+    print(f"config 5 (70B fp8, T={T}): h rel_l2 {e_h:.3e}, layer {e_y:.3e}, down entry {e_d:.3e}")
+    assert np.isfinite(_np(y)).all()
+    assert e_h < FP8_TOL and e_y < FP8_TOL and e_d < FP8_TOL

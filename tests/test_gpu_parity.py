@@ -199,9 +199,16 @@ def test_prefill_token_counts(gpu, T):
 
 
 def _barrier_state(ws):
-    """(generation, timeout flag) of the decode kernel's barrier words."""
+    """(generation, timeout flag) of the decode kernel's barrier words (the
+    64-bit words at bytes 2176 and 2304 of the sync area)."""
     w = ws[:4096].view(torch.int64).cpu().tolist()
     return w[272], w[288]
+
+
+def _set_spin_bound(ws, polls):
+    """The bound of the persistent kernels' barrier waits (the 32-bit word at
+    byte 2312 of the sync area; 0 = the kernels' default)."""
+    ws[2312:2316].view(torch.int32).fill_(polls)
 
 
 def _tile_counters(ws):
@@ -258,10 +265,10 @@ def test_shared_workspace_across_calls(gpu):
 
 
 def test_prepared_layer_cache(gpu):
-    """A layer called again reuses its prepared arguments (the same result:
-    split-K partial sums are combined in arrival order, so bf16 roundings may
-    differ by an ulp); layers whose factors the host mirror copies (gate and
-    up with different row pitches) are not kept."""
+    """A layer called again reuses its prepared arguments (the same bits:
+    split-K partial sums are added in split order); layers whose factors the
+    host mirror copies (gate and up with different row pitches) are not
+    kept."""
     from svdmlp import ops
 
     ops._PLANS.clear()
@@ -272,7 +279,7 @@ def test_prepared_layer_cache(gpu):
     y1 = ops.svd_mlp(*t).clone()
     assert len(ops._PLANS) == 1
     y2 = ops.svd_mlp(*t)
-    assert _rel(_np(y2), _np(y1)) < 5e-3
+    assert torch.equal(y2.view(torch.int16), y1.view(torch.int16))
     assert _rel(_np(y2), O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
     mixed = list(t[1:])
     mixed[0], mixed[2] = ops.pad_rows(t[1], 8), ops.pad_rows(t[3], 16)
@@ -326,13 +333,87 @@ def test_linear_layout_weights_bf16(gpu, layer8b):
         assert _rel(got, O.svd_mlp_ref(x[rows], *f, dtype="bfloat16")) < BF16_TOL, T
 
 
-def test_replay_is_stable(gpu, layer8b):
+@pytest.mark.parametrize("T,padded", [(1, True), (8, False), (64, True), (128, False), (300, False), (1024, True)])
+def test_replay_is_bitwise_identical(gpu, layer8b, T, padded):
+    """The analogue of the reference's async-vs-sync bitwise check
+    (tests_test_speedup_migration.py.before:217-233): the same call twice
+    gives the same bits.  Split-K partial sums are added in split order on
+    every path taken here (the MFMA decode layer up to 128 tokens, whichever
+    unit arrives last; the large-tile path's ordered reductions above)."""
     shape, f, ft = layer8b
-    xt = _to(_x(1024, shape.d, 5), torch.bfloat16, gpu)
-    a = ops.svd_mlp(xt, *ft).float()
-    b = ops.svd_mlp(xt, *ft).float()
-    # split-K partial sums use fp32 atomics: replays agree to rounding.
-    assert torch.linalg.norm(a - b) / torch.linalg.norm(a) < 1e-3
+    xt = _to(_x(T, shape.d, 5 + T), torch.bfloat16, gpu)
+    fs = [ops.pad_rows(a, 64) if padded and i % 2 else a for i, a in enumerate(ft)]
+    ws = ops.svd_mlp_workspace(xt, r=shape.r, ff=shape.ff)
+    ys = [ops.svd_mlp(xt, *fs, workspace=ws).clone() for _ in range(3)]
+    for y in ys[1:]:
+        assert torch.equal(y.view(torch.int16), ys[0].view(torch.int16)), T
+    assert _rel(_np(ys[0])[: min(T, 16)], O.svd_mlp_ref(_np(xt)[: min(T, 16)], *f, dtype="bfloat16")) < BF16_TOL
+
+
+@pytest.mark.parametrize("shape,T", [(inputs.LayerShape(1024, 2048, 512), 8),     # MFMA decode layer
+                                     (inputs.LayerShape(1024, 2048, 512), 1),     # streaming-GEMV layer
+                                     (inputs.LayerShape(1040, 2064, 400, 272), 2)])  # GEMV, ragged strips
+def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T):
+    """A persistent decode launch whose grid-barrier waits give up (forced
+    from the host with a bound of one poll, so every block still runs to its
+    end) writes NaN into y, reports the timeout through the workspace
+    status, and the workspace works again once reset."""
+    x, f = inputs.make_layer(shape, T=T, seed=80 + T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
+    ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
+    assert _rel(_np(ops.svd_mlp(*t, workspace=ws)), ref) < BF16_TOL
+    assert ops.workspace_status(ws) is False
+    _set_spin_bound(ws, 1)
+    y = _np(ops.svd_mlp(*t, workspace=ws))
+    assert np.isnan(y).all(), f"{np.isnan(y).mean():.3f} of y is NaN"
+    assert ops.workspace_status(ws) is True
+    assert ops.workspace_status(ws, reset=True) is True   # reports, then zeroes the sync area
+    assert ops.workspace_status(ws) is False and _barrier_state(ws) == (0, 0)
+    for _ in range(2):
+        assert _rel(_np(ops.svd_mlp(*t, workspace=ws)), ref) < BF16_TOL
+    assert ops.workspace_status(ws) is False
+
+
+# ---------------------------------------------------------------------------
+# the reference's transposed launchers in bf16 (test_speedup.py:500-544)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("S,H,R,I", [(1, 136, 64, 200), (13, 264, 136, 520), (129, 256, 72, 392),
+                                     (200, 1024, 256, 2048)])
+def test_transposed_launchers_bf16(gpu, S, H, R, I):
+    """fused_mlp_up_T returns (I, S); fused_three_mm_XTUV takes X as (I, S):
+    bf16 against the oracle at 1e-2, on token counts that are and are not
+    multiples of 8 (the latter leave the 16-byte vector path)."""
+    f = _rounded(_small([(S, H), (H, R), (R, I), (H, R), (R, I), (I, R), (R, H)], seed=S + 7), torch.bfloat16)
+    x, ug, vg, uu, vu, ud, vd = f
+    t = [_to(a, torch.bfloat16, gpu) for a in f]
+    hT = compat.fused_mlp_up_T(t[0], t[1], t[2], t[3], t[4])
+    assert tuple(hT.shape) == (I, S) and hT.dtype == torch.bfloat16
+    h_ref = O.fused_gate_up_ref(x, ug, vg, uu, vu, "bfloat16")
+    assert _rel(_np(hT), h_ref.T) < BF16_TOL
+    y = compat.fused_three_mm_XTUV(_to(np.ascontiguousarray(h_ref.T), torch.bfloat16, gpu), t[5], t[6])
+    assert tuple(y.shape) == (S, H)
+    assert _rel(_np(y), O.fused_xuv_ref(h_ref, ud, vd, "bfloat16")) < BF16_TOL
+    both = compat.svd_mlp_with_fused_kernel(t[0], t[3], t[4], t[1], t[2], t[5], t[6])
+    assert _rel(_np(both), O.svd_mlp_ref(*f, dtype="bfloat16")) < BF16_TOL
+
+
+def test_transposed_launchers_bf16_8b_shape(gpu, layer8b):
+    """The same launchers on the LLaMA3-8B factors at S=128 (the reference's
+    headline TPU shape, test_speedup.py:755)."""
+    shape, f, ft = layer8b
+    S = 128
+    x = _x(S, shape.d, 900)
+    xt = _to(x, torch.bfloat16, gpu)
+    hT = compat.fused_mlp_up_T(xt, ft[0], ft[1], ft[2], ft[3])
+    h_ref = O.fused_gate_up_ref(x, *f[:4], dtype="bfloat16")
+    assert _rel(_np(hT), h_ref.T) < BF16_TOL
+    y = compat.fused_three_mm_XTUV(hT, ft[4], ft[5])
+    hb = inputs.as_float32(_np(hT).T, torch.bfloat16)
+    assert _rel(_np(y), O.fused_xuv_ref(hb, f[4], f[5], "bfloat16")) < BF16_TOL
+    assert _rel(_np(y), O.svd_mlp_ref(x, *f, dtype="bfloat16")) < BF16_TOL
 
 
 # ---------------------------------------------------------------------------
@@ -490,8 +571,8 @@ def test_padded_factor_rows(gpu, T):
     if T <= 128:   # one MFMA decode-layer launch: 3 barriers, counters back at zero
         assert _barrier_state(ws) == (3, 0) and not any(_tile_counters(ws))
     dense = _np(ops.svd_mlp(*t))
-    # same kernels and math; split-K partial sums are combined in arrival
-    # order, so bf16 roundings of the rank intermediates may differ by an ulp
+    # the same math; at T <= 2 dense factors take the streaming-GEMV layer
+    # (fp32 atomics) and padded ones the MFMA layer, so roundings may differ
     assert _rel(_np(ops.svd_mlp(t[0], *padded)), dense) < 5e-3
 
 

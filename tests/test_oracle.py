@@ -260,6 +260,24 @@ def test_mlp_block_is_residual_plus_mlp_of_norm():
     np.testing.assert_allclose(y, x + O.svd_mlp_ref(O.rmsnorm_ref(x, gain), *f), rtol=1e-6, atol=1e-7)
 
 
+def test_mlp_block_f64_brute_force():
+    """The unrounded float64 block against Python-float loops (RMSNorm by
+    hand, the brute-force GEMM chains), and against the float32 block."""
+    d, ff, r = 6, 7, 3
+    x = rng.normal(size=(2, d))
+    gain = rng.uniform(0.9, 1.1, size=d)
+    f = [a.astype(np.float64) for a in _small([(d, r), (r, ff), (d, r), (r, ff), (ff, r), (r, d)], seed=11)]
+    hn = np.zeros_like(x)
+    for s_ in range(2):
+        rms = math.sqrt(sum(float(v) ** 2 for v in x[s_]) / d + 1e-5)
+        hn[s_] = [gain[j] * x[s_, j] / rms for j in range(d)]
+    want = x + _brute_xuv(_brute_gate_up(hn, *f[:4]), f[4], f[5])
+    got = O.mlp_block_f64(x, gain, f, eps=1e-5)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    y32 = O.mlp_block_ref(x.astype(np.float32), gain.astype(np.float32), [a.astype(np.float32) for a in f])
+    np.testing.assert_allclose(y32, got, rtol=2e-5, atol=2e-6)
+
+
 # ---------------------------------------------------------------------------
 # metrics and accounting
 # ---------------------------------------------------------------------------
