@@ -3,14 +3,22 @@
 Config 4: the 32-layer LLaMA3-8B MLP stack (T=4096, d=4096, ff=14336,
 per-branch ranks drawn from {2048, ..., 3072}, RMSNorm eps 1e-5, gains
 ~U(0.9, 1.1), residual add), exactly as bench.py builds it.  Every layer is
-checked on a row subset against the oracle's block fed with the GPU's own
-input rows (rows are independent through RMSNorm, the MLP and the residual,
-so a row subset is an exact check of those rows): relative Frobenius error
-<= 1e-2 on the output and on the MLP part.  End to end, two correct bf16
-chains drift apart as their rounding differences pass through 32 residual
-blocks, so the whole-stack criterion compares both with the unrounded
-float64 chain: the GPU chain must be as close to it as the oracle's own bf16
-chain is (within 25%).
+checked on a row subset (rows are independent through RMSNorm, the MLP and
+the residual, so a row subset is an exact check of those rows):
+  * the block output against the oracle's block fed with the GPU's own input
+    rows, relative Frobenius error <= 1e-2;
+  * the MLP alone, at the layer's real ranks and T=4096 (the same prefill
+    kernels), on the oracle's RMSNorm of the GPU's input: <= 1e-2;
+  * the MLP part of the block output, y - x, <= 2e-2: y = bf16(x + mlp)
+    carries the bf16 quantum of the residual sum, which grows with the
+    residual stream (rms ~3.4 by layer 32 against ~0.6 for the MLP output),
+    so two correct implementations differ there by up to ~1e-2 per layer.
+End to end, two correct bf16 chains drift apart as their rounding
+differences pass through 32 residual blocks (the oracle's bf16 chain and one
+that also rounds the rank intermediates, as the kernels do, end 2.6e-2
+apart on the CPU), so the whole-stack criterion compares both with the
+unrounded float64 chain: the GPU chain must be as close to it as the
+oracle's own bf16 chain is (within 25%).
 
 Config 5: the LLaMA3-70B-shape layer (T=2048, d=8192, ff=28672, r=5632) with
 fp8 e4m3 factors and per-output-channel fp32 scales, bf16 activations, on a
@@ -49,23 +57,28 @@ def test_config4_stack_32_layers_full_shape(gpu):
     x0 = _np(x[idx])
     chain_orc, chain_f64 = x0.copy(), x0.astype(np.float64)
     cur, bufs = x, (torch.empty_like(x), torch.empty_like(x))
-    worst = 0.0
+    worst, worst_part = 0.0, 0.0
     for i, layer in enumerate(layers):
         out = ops.svd_mlp_block(cur, layer.gain, *layer.factors, eps=1e-5, workspace=ws, out=bufs[i % 2])
-        xin, yout = _np(cur[idx]), _np(out[idx])
+        xall = _np(cur)
+        xin, yout = xall[rows], _np(out[idx])
         f = [_np(a) for a in layer.factors]
         gain = layer.gain.cpu().numpy()
         ref = O.mlp_block_ref(xin, gain, f, eps=1e-5, dtype="bfloat16")
-        e_y, e_mlp = O.relative_l2(yout, ref), O.relative_l2(yout - xin, ref - xin)
-        worst = max(worst, e_mlp)
-        assert e_y < BF16_TOL and e_mlp < BF16_TOL, (i, layer.ranks, e_y, e_mlp)
+        hn = O.rmsnorm_ref(xall, gain, eps=1e-5, dtype="bfloat16")
+        mlp = _np(ops.svd_mlp(torch.from_numpy(hn).to(gpu).to(torch.bfloat16), *layer.factors, workspace=ws)[idx])
+        e_y = O.relative_l2(yout, ref)
+        e_mlp = O.relative_l2(mlp, O.svd_mlp_ref(hn[rows], *f, dtype="bfloat16"))
+        e_part = O.relative_l2(yout - xin, ref - xin)
+        worst, worst_part = max(worst, e_mlp), max(worst_part, e_part)
+        assert e_y < BF16_TOL and e_mlp < BF16_TOL and e_part < 2 * BF16_TOL, (i, layer.ranks, e_y, e_mlp, e_part)
         chain_orc = O.mlp_block_ref(chain_orc, gain, f, eps=1e-5, dtype="bfloat16")
         chain_f64 = O.mlp_block_f64(chain_f64, gain, f, eps=1e-5)
         cur = out
     got = _np(cur[idx])
     e_gpu = O.relative_l2(got, chain_f64.astype(np.float32))
     e_orc = O.relative_l2(chain_orc, chain_f64.astype(np.float32))
-    print(f"config 4: worst per-layer MLP rel_l2 {worst:.3e}; after {L} layers vs float64: "
+    print(f"config 4: worst per-layer MLP rel_l2 {worst:.3e} (block's y - x {worst_part:.3e}); after {L} layers vs float64: "
           f"GPU {e_gpu:.3e}, oracle bf16 chain {e_orc:.3e}, GPU vs oracle chain {O.relative_l2(got, chain_orc):.3e}")
     assert e_gpu <= 1.25 * e_orc, (e_gpu, e_orc)
 
