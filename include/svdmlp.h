@@ -176,6 +176,27 @@ int svdmlp_svd_mlp_block_ld(const void* x, const float* norm_w, float eps, const
                             int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * svdmlp_svd_mlp_ld without a workspace argument: the layer runs in a fixed
+ * scratch area that the library holds in device memory (64 MiB per device
+ * that the library runs on, until the process ends), so the call allocates
+ * nothing.  No counterpart in the reference; it is for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Shapes whose workspace
+ * (svdmlp_workspace_bytes) exceeds 64 MiB are rejected with SVDMLP_EINVAL
+ * (LLaMA3-8B: up to 64 tokens; prefill shapes need a workspace).  The first
+ * call on a device looks the scratch up and clears its sync area on `stream`
+ * (the current device's).  Every call on a device shares that device's
+ * scratch and leaves its contents behind: calls that overlap on one device
+ * (different streams, threads) race; serialise them.  svdmlp_workspace_status
+ * does not see this scratch; a timed-out call still writes NaN into y.
+ */
+int svdmlp_svd_mlp_noalloc(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                           const void* ud, const void* vd, const float* const* scales /* 6 or NULL */,
+                           const int64_t* ld /* 6 or NULL */, void* y, int64_t T, int64_t d, int64_t ff,
+                           int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                           void* stream);
+
+/*
  * Per-stage GPU timing (no counterpart in the reference, whose timing is host
  * wall clock around block_until_ready, test_speedup.py:739-749).  While
  * enabled, every stage launch of the calls above is bracketed by hipEvents

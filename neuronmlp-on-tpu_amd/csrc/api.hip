@@ -48,6 +48,9 @@ constexpr int64_t kDlMaxT = 128;
 constexpr int kTargetBlocks = 384;  // ~1.5 blocks per CU on 256 CUs
 
 thread_local std::string g_err;
+// Set while svdmlp_svd_mlp_noalloc runs on this thread: the stage profiler
+// then records no events (creating one may allocate).
+thread_local bool t_no_events = false;
 
 int fail(const char* fmt, ...) {
   char buf[512];
@@ -122,6 +125,7 @@ struct StageScope {
   hipStream_t st;
   hipEvent_t a = nullptr, b = nullptr;
   StageScope(int s, hipStream_t stream) : stage(s), st(stream) {
+    if (t_no_events) return;
     std::lock_guard<std::mutex> g(g_prof.mu);
     if (!g_prof.on) return;
     a = g_prof.get();
@@ -830,9 +834,65 @@ int validate_dims(int64_t T, int64_t a, int64_t b, int64_t r) {
   return SVDMLP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Fixed scratch of svdmlp_svd_mlp_noalloc: the workspace of calls that may not
+// allocate.  One copy per device, at its own address, held until the process
+// ends; host code uses only the address hipGetSymbolAddress returns for the
+// current device (the array's name is a host-side stand-in).
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// Device address of the current device's scratch.  The first call on a
+// device looks it up and zeroes its 4096-byte sync area on `st` (the grid
+// barrier and tile counters of the persistent decode kernels start at zero;
+// every later call leaves them valid for the next).
+int scratch_of_current_device(hipStream_t st, char** out) {
+  int dev = 0;
+  int rc = check(hipGetDevice(&dev), "current device");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kScratchDevices) return fail("device index %d beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if ((rc = check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "scratch symbol address"))) return rc;
+    if (!ptr) return fail("scratch symbol address: null");
+    if ((rc = check(launch_fill_zero(static_cast<float*>(ptr), 4096 / 4, st), "scratch sync area clear"))) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = static_cast<char*>(g_scratch_ptr[dev]);
+  return SVDMLP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int svdmlp_svd_mlp_noalloc(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                           const void* ud, const void* vd, const float* const* scales, const int64_t* ld, void* y,
+                           int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
+                           int32_t w_dtype, uint32_t flags, void* stream) {
+  g_err.clear();
+  int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
+  if (rc) return rc;
+  const size_t need = ws_layout(T, d, ff, std::max(r_gu, r_d)).total;
+  if (need > kScratchBytes)
+    return fail("svdmlp_svd_mlp_noalloc: this shape needs %zu bytes of workspace, more than the fixed scratch of "
+                "%zu bytes (T=%lld, d=%lld, ff=%lld, r=%lld); use svdmlp_svd_mlp_ld with a workspace",
+                need, kScratchBytes, (long long)T, (long long)d, (long long)ff, (long long)std::max(r_gu, r_d));
+  char* ws = nullptr;
+  if ((rc = scratch_of_current_device((hipStream_t)stream, &ws))) return rc;
+  struct NoEvents {
+    NoEvents() { t_no_events = true; }
+    ~NoEvents() { t_no_events = false; }
+  } guard;
+  return svdmlp_svd_mlp_ld(x, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_gu, r_d, act_dtype, w_dtype, flags,
+                           ws, kScratchBytes, stream);
+}
 
 int svdmlp_version(void) { return SVDMLP_VERSION; }
 

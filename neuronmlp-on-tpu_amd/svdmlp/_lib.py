@@ -40,6 +40,7 @@ EXPORTED = (
     "svdmlp_svd_mlp_block",
     "svdmlp_svd_mlp_ld",
     "svdmlp_svd_mlp_block_ld",
+    "svdmlp_svd_mlp_noalloc",
     "svdmlp_profile_enable",
     "svdmlp_profile_read",
     "svdmlp_stage_name",
@@ -86,6 +87,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.svdmlp_svd_mlp_block_ld.restype = ctypes.c_int
     lib.svdmlp_svd_mlp_block_ld.argtypes = ([_vp, _vp, ctypes.c_float] + [_vp] * 6 + [_vp, _vp, _vp] + [_i64] * 5
                                             + [_i32, _i32, _u32, _vp, _sz, _vp])
+    lib.svdmlp_svd_mlp_noalloc.restype = ctypes.c_int
+    lib.svdmlp_svd_mlp_noalloc.argtypes = [_vp] * 7 + [_vp, _vp, _vp] + [_i64] * 5 + [_i32, _i32, _u32, _vp]
     lib.svdmlp_profile_enable.restype = ctypes.c_int
     lib.svdmlp_profile_enable.argtypes = [ctypes.c_int]
     lib.svdmlp_profile_read.restype = ctypes.c_int
