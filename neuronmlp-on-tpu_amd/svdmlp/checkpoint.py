@@ -1,230 +1,257 @@
-"""SVD-MLP factors from a sharded Hugging Face safetensors checkpoint
-(models/hf_svd.py:1-196).
+"""SVD-MLP factors stored in a sharded Hugging Face safetensors checkpoint.
 
-The checkpoint stores each branch as two PyTorch ``Linear`` weights in
-``[out, in]`` order, and names the first projection ``v_proj`` and the second
-``u_proj``: ``gate_v_proj.weight`` is ``(r, d)`` and ``gate_u_proj.weight``
-``(ff, r)``.  The kernels take natural matmul operands, ``U (d_in, r)`` and
-``V (r, d_out)``, so each stored tensor is transposed and the v/u names swap:
-``Ug = gate_v_proj.T``, ``Vg = gate_u_proj.T`` and so on.  Factors come back
+The on-disk format is the reference's (models/hf_svd.py:13-20, 130-196) and
+is kept exactly, so its checkpoints load unchanged:
+
+* ``config.json`` gives ``hidden_size``, ``intermediate_size`` and
+  ``num_hidden_layers``; ``model.safetensors.index.json`` maps every tensor
+  name to its shard file (``weight_map``);
+* each MLP branch (gate, up, down) is two PyTorch ``Linear`` weights stored
+  ``(out, in)``: ``model.layers.{i}.mlp.{branch}_v_proj.weight`` is the first
+  projection, ``(r, d_in)``, and ``{branch}_u_proj.weight`` the second,
+  ``(d_out, r)``.
+
+The kernels take natural matmul operands, ``U (d_in, r)`` and ``V (r,
+d_out)``: the first projection is U transposed, the second V transposed
+(hence the v -> U, u -> V naming swap).  Everything below works on a table of
+the six factor slots, each knowing its branch, its projection and how its
+shapes follow from (rank, hidden, intermediate); layers are returned
 gate-first, ``(Ug, Vg, Uu, Vu, Ud, Vd)``, ready for ``svdmlp.svd_mlp``.
 
-Two device layouts are offered:
+Device layouts: ``"natural"`` (contiguous ``(in, out)``, one transpose on the
+device), ``"padded"`` (natural, V rows 64 elements longer in memory, the pitch
+the decode kernels stream fastest) and ``"linear"`` (transposed views of the
+stored tensors: the library reads the ``(out, in)`` storage in place).
 
-* ``"natural"`` (default): each factor is copied to the device and transposed
-  there once into a contiguous ``(in, out)`` tensor, the layout every fast path
-  (large-tile prefill, persistent decode layers) reads;
-* ``"linear"``: each factor is copied as stored and returned as a transposed
-  view; the library reads the ``(out, in)`` storage in place (no transpose
-  pass, no second copy), on its Linear-layout kernels.
-
-Validation and its exceptions follow the reference: missing config or index
--> ``FileNotFoundError``; index without ``weight_map`` -> ``ValueError``;
-missing factor keys -> ``KeyError``; missing shards -> ``FileNotFoundError``;
-factor shapes or dtypes that disagree with the config -> ``ValueError`` /
-``TypeError``.
+Errors keep the reference's exception types and message wording, so callers
+that match on them behave the same: missing config / index / shards
+(FileNotFoundError), an index without ``weight_map`` or a bad layer selection
+(ValueError), absent tensor names (KeyError), inconsistent shapes
+(ValueError) or dtypes (TypeError).
 """
 
 from __future__ import annotations
 
 import json
 from contextlib import ExitStack
+from dataclasses import dataclass
 from pathlib import Path
-from typing import Sequence
+from typing import Iterable, Sequence
 
-FACTOR_SUFFIXES = (
-    "gate_v_proj.weight",
-    "gate_u_proj.weight",
-    "up_v_proj.weight",
-    "up_u_proj.weight",
-    "down_v_proj.weight",
-    "down_u_proj.weight",
-)
-
-_SAFETENSORS_DTYPES = ("BF16", "F32", "F16")
+CONFIG_FILE = "config.json"
+INDEX_FILE = "model.safetensors.index.json"
+_ITEMSIZE = {"BF16": 2, "F16": 2, "F32": 4}
 
 
-def checkpoint_metadata(model_path: str | Path) -> tuple[dict, dict]:
-    """``config.json`` and ``model.safetensors.index.json`` of a checkpoint
-    directory, minimally validated (models/hf_svd.py:23-37)."""
-    model_path = Path(model_path)
-    config_path = model_path / "config.json"
-    index_path = model_path / "model.safetensors.index.json"
-    if not config_path.is_file():
-        raise FileNotFoundError(f"missing checkpoint config: {config_path}")
-    if not index_path.is_file():
-        raise FileNotFoundError(f"missing safetensors index: {index_path}")
-    config = json.loads(config_path.read_text(encoding="utf-8"))
-    index = json.loads(index_path.read_text(encoding="utf-8"))
-    if "weight_map" not in index:
-        raise ValueError(f"safetensors index has no weight_map: {index_path}")
-    return config, index
+@dataclass(frozen=True)
+class FactorSlot:
+    """One of a layer's six factors: ``branch`` gate / up / down, ``proj``
+    "v" (first projection; natural operand U) or "u" (second; natural V)."""
+
+    branch: str
+    proj: str
+
+    def key(self, layer: int) -> str:
+        return f"model.layers.{layer}.mlp.{self.branch}_{self.proj}_proj.weight"
+
+    def natural_shape(self, rank: int, hidden: int, intermediate: int) -> tuple[int, int]:
+        d_in, d_out = (intermediate, hidden) if self.branch == "down" else (hidden, intermediate)
+        return (d_in, rank) if self.proj == "v" else (rank, d_out)
+
+
+SLOTS = tuple(FactorSlot(b, p) for b in ("gate", "up", "down") for p in ("v", "u"))
+FACTOR_SUFFIXES = tuple(s.key(0).split(".mlp.", 1)[1] for s in SLOTS)
 
 
 def factor_keys(layer_index: int) -> tuple[str, ...]:
-    """The six tensor names of one layer's MLP (models/hf_svd.py:40-44)."""
+    """Tensor names of one layer's factors, in slot (gate-first) order."""
     if layer_index < 0:
         raise ValueError(f"layer index must be non-negative, got {layer_index}")
-    prefix = f"model.layers.{layer_index}.mlp."
-    return tuple(prefix + suffix for suffix in FACTOR_SUFFIXES)
+    return tuple(s.key(layer_index) for s in SLOTS)
 
 
 def validate_factor_shapes(factors: Sequence, *, hidden_size: int, intermediate_size: int) -> int:
-    """Check the natural-layout (transposed) shapes and a common dtype; return
-    the rank (models/hf_svd.py:47-73).  ``factors`` may be tensors or any
-    objects with ``shape`` and ``dtype``."""
-    if len(factors) != 6:
+    """Rank of six natural-layout factors (anything with ``shape`` and
+    ``dtype``) after checking every shape against the slot table and that one
+    dtype is shared (the contract of models/hf_svd.py:47-73)."""
+    if len(factors) != len(SLOTS):
         raise ValueError(f"expected six MLP factors, got {len(factors)}")
-    rank = int(factors[0].shape[1])
-    expected = (
-        (hidden_size, rank),
-        (rank, intermediate_size),
-        (hidden_size, rank),
-        (rank, intermediate_size),
-        (intermediate_size, rank),
-        (rank, hidden_size),
-    )
-    actual = tuple(tuple(int(v) for v in f.shape) for f in factors)
-    if actual != expected:
-        raise ValueError(f"invalid transposed MLP factor shapes; expected {expected}, got {actual}")
-    dtypes = {str(f.dtype) for f in factors}
-    if len(dtypes) != 1:
-        raise TypeError(f"MLP factor dtypes differ: {sorted(dtypes)}")
+    shapes = tuple(tuple(int(n) for n in f.shape) for f in factors)
+    rank = shapes[0][1] if len(shapes[0]) == 2 else -1
+    want = tuple(s.natural_shape(rank, hidden_size, intermediate_size) for s in SLOTS)
+    if shapes != want:
+        raise ValueError(f"invalid transposed MLP factor shapes; expected {want}, got {shapes}")
+    kinds = sorted({str(f.dtype) for f in factors})
+    if len(kinds) > 1:
+        raise TypeError(f"MLP factor dtypes differ: {kinds}")
     return rank
 
 
-def _selected(config: dict, layer_indices) -> tuple[int, ...]:
-    num_layers = int(config["num_hidden_layers"])
-    selected = tuple(range(num_layers)) if layer_indices is None else tuple(int(i) for i in layer_indices)
-    if not selected or len(set(selected)) != len(selected):
-        raise ValueError("select at least one layer, without duplicates")
-    if min(selected) < 0 or max(selected) >= num_layers:
-        raise ValueError(f"layer indices must be in [0, {num_layers})")
-    return selected
+class SvdCheckpoint:
+    """A checkpoint directory, parsed once: its MLP geometry and tensor map."""
+
+    def __init__(self, root: str | Path):
+        self.root = Path(root)
+        cfg_path, idx_path = self.root / CONFIG_FILE, self.root / INDEX_FILE
+        for path, what in ((cfg_path, "checkpoint config"), (idx_path, "safetensors index")):
+            if not path.is_file():
+                raise FileNotFoundError(f"missing {what}: {path}")
+        self.config = json.loads(cfg_path.read_text(encoding="utf-8"))
+        self.index = json.loads(idx_path.read_text(encoding="utf-8"))
+        if "weight_map" not in self.index:
+            raise ValueError(f"safetensors index has no weight_map: {idx_path}")
+        self.weight_map: dict = self.index["weight_map"]
+
+    @property
+    def hidden(self) -> int:
+        return int(self.config["hidden_size"])
+
+    @property
+    def intermediate(self) -> int:
+        return int(self.config["intermediate_size"])
+
+    @property
+    def num_layers(self) -> int:
+        return int(self.config["num_hidden_layers"])
+
+    def selection(self, layers: Iterable[int] | None) -> tuple[int, ...]:
+        """Validated layer list (``None``: every layer)."""
+        sel = tuple(range(self.num_layers)) if layers is None else tuple(int(i) for i in layers)
+        if not sel or len(set(sel)) != len(sel):
+            raise ValueError("select at least one layer, without duplicates")
+        if not all(0 <= i < self.num_layers for i in sel):
+            raise ValueError(f"layer indices must be in [0, {self.num_layers})")
+        return sel
+
+    def shards_for(self, layers: Sequence[int]) -> list[str]:
+        """Shard files holding the layers' factors, after checking that every
+        tensor name is mapped and every shard exists."""
+        keys = [k for i in layers for k in factor_keys(i)]
+        unmapped = [k for k in keys if k not in self.weight_map]
+        if unmapped:
+            raise KeyError(f"checkpoint is missing MLP factors: {unmapped}")
+        shards = sorted({self.weight_map[k] for k in keys})
+        gone = [s for s in shards if not (self.root / s).is_file()]
+        if gone:
+            raise FileNotFoundError("checkpoint shards required by the selected layers are missing: " + ", ".join(gone))
+        return shards
+
+    def _handles(self, stack: ExitStack, shards: Sequence[str]) -> dict:
+        from safetensors import safe_open
+
+        return {s: stack.enter_context(safe_open(str(self.root / s), framework="pt")) for s in shards}
+
+    def headers(self, layers: Sequence[int]) -> list[dict]:
+        """Per layer: rank, dtype, factor bytes and where each tensor lives,
+        from the shard headers alone (no payload is read)."""
+        rows = []
+        with ExitStack() as stack:
+            handles = self._handles(stack, self.shards_for(layers))
+            for i in layers:
+                tensors, natural = [], []
+                for slot in SLOTS:
+                    key = slot.key(i)
+                    view = handles[self.weight_map[key]].get_slice(key)
+                    stored, kind = tuple(view.get_shape()), view.get_dtype()
+                    if len(stored) != 2 or kind not in _ITEMSIZE or min(stored) <= 0:
+                        raise ValueError(f"unsupported MLP tensor {key}: {stored}, {kind}")
+                    natural.append(_Header((stored[1], stored[0]), kind))
+                    tensors.append({"key": key, "shape": list(stored), "dtype": kind, "shard": self.weight_map[key]})
+                rank = validate_factor_shapes(natural, hidden_size=self.hidden, intermediate_size=self.intermediate)
+                size = sum(h.shape[0] * h.shape[1] * _ITEMSIZE[h.dtype] for h in natural)
+                rows.append({"layer": i, "rank": rank, "dtype": tensors[0]["dtype"], "factor_bytes": size,
+                             "tensors": tensors})
+        return rows
+
+    def tensors(self, layers: Sequence[int], *, device, layout: str, dtype=None) -> tuple[tuple, ...]:
+        """The layers' factors on ``device`` in the requested layout."""
+        import torch
+
+        from .ops import pad_rows
+
+        place = {
+            "natural": lambda w, slot: w.t().contiguous(),
+            "padded": lambda w, slot: pad_rows(w.t()) if slot.proj == "u" else w.t().contiguous(),
+            "linear": lambda w, slot: w.t(),
+        }
+        if layout not in place:
+            raise ValueError(f"layout must be 'natural', 'padded' or 'linear', got {layout!r}")
+        dev = torch.device(device)
+        out = []
+        with ExitStack() as stack:
+            handles = self._handles(stack, self.shards_for(layers))
+            for i in layers:
+                layer = []
+                for slot in SLOTS:
+                    key = slot.key(i)
+                    w = handles[self.weight_map[key]].get_tensor(key).to(dev)   # stored (out, in)
+                    if dtype is not None:
+                        w = w.to(dtype)
+                    layer.append(place[layout](w, slot))
+                validate_factor_shapes(layer, hidden_size=self.hidden, intermediate_size=self.intermediate)
+                out.append(tuple(layer))
+        return tuple(out)
 
 
-def _required_shards(model_path: Path, weight_map: dict, keys) -> list[str]:
-    missing = [key for key in keys if key not in weight_map]
-    if missing:
-        raise KeyError(f"checkpoint is missing MLP factors: {missing}")
-    names = sorted({weight_map[key] for key in keys})
-    absent = [name for name in names if not (model_path / name).is_file()]
-    if absent:
-        raise FileNotFoundError("checkpoint shards required by the selected layers are missing: " + ", ".join(absent))
-    return names
+@dataclass(frozen=True)
+class _Header:
+    shape: tuple
+    dtype: str
 
 
-class _Shape:
-    def __init__(self, shape, dtype):
-        self.shape, self.dtype = shape, dtype
+def checkpoint_metadata(model_path: str | Path) -> tuple[dict, dict]:
+    """``(config, index)`` of a checkpoint directory (models/hf_svd.py:23-37)."""
+    ck = SvdCheckpoint(model_path)
+    return ck.config, ck.index
 
 
 def inspect_mlp_checkpoint(model_path: str | Path, layer_indices: Sequence[int] | None = None) -> dict:
-    """Validate shard headers without loading payloads (models/hf_svd.py:76-129):
-    per selected layer its rank, dtype, factor bytes and tensor locations."""
-    from safetensors import safe_open
-
-    model_path = Path(model_path)
-    config, index = checkpoint_metadata(model_path)
-    if config.get("hidden_act", "silu") != "silu" or config.get("mlp_bias", False):
+    """Header-only validation of the selected layers (models/hf_svd.py:76-129):
+    geometry, shards and, per layer, rank, dtype, factor bytes and tensors."""
+    ck = SvdCheckpoint(model_path)
+    if ck.config.get("hidden_act", "silu") != "silu" or ck.config.get("mlp_bias", False):
         raise ValueError("the fused kernel requires bias-free SwiGLU MLPs")
-    hidden, intermediate = int(config["hidden_size"]), int(config["intermediate_size"])
-    selected = _selected(config, layer_indices)
-    weight_map = index["weight_map"]
-    keys = tuple(key for layer in selected for key in factor_keys(layer))
-    names = _required_shards(model_path, weight_map, keys)
-    itemsize = {"BF16": 2, "F16": 2, "F32": 4}
-    layers = []
-    with ExitStack() as stack:
-        shards = {name: stack.enter_context(safe_open(str(model_path / name), framework="pt")) for name in names}
-        for layer in selected:
-            descriptors, info = [], []
-            for key in factor_keys(layer):
-                view = shards[weight_map[key]].get_slice(key)
-                shape, dtype = tuple(view.get_shape()), view.get_dtype()
-                if len(shape) != 2 or dtype not in _SAFETENSORS_DTYPES or min(shape) <= 0:
-                    raise ValueError(f"unsupported MLP tensor {key}: {shape}, {dtype}")
-                descriptors.append(_Shape(shape[::-1], dtype))
-                info.append({"key": key, "shape": list(shape), "dtype": dtype, "shard": weight_map[key]})
-            rank = validate_factor_shapes(descriptors, hidden_size=hidden, intermediate_size=intermediate)
-            nbytes = sum(d.shape[0] * d.shape[1] * itemsize[d.dtype] for d in descriptors)
-            layers.append({"layer": layer, "rank": rank, "dtype": info[0]["dtype"], "factor_bytes": nbytes,
-                           "tensors": info})
-    return {"model_path": str(model_path.resolve()), "num_hidden_layers": int(config["num_hidden_layers"]),
-            "hidden_size": hidden, "intermediate_size": intermediate, "selected_layers": list(selected),
-            "shards": names, "layers": layers}
+    layers = ck.selection(layer_indices)
+    return {"model_path": str(ck.root.resolve()), "num_hidden_layers": ck.num_layers, "hidden_size": ck.hidden,
+            "intermediate_size": ck.intermediate, "selected_layers": list(layers), "shards": ck.shards_for(layers),
+            "layers": ck.headers(layers)}
 
 
 def load_mlp_factors(model_path: str | Path, layer_indices: Sequence[int], *, device="cuda",
                      layout: str = "natural", dtype=None) -> tuple[tuple, ...]:
     """Selected layers' factors on ``device``, gate-first ``(Ug, Vg, Uu, Vu, Ud,
-    Vd)`` per layer (models/hf_svd.py:132-196).  ``layout`` is ``"natural"``
-    (contiguous ``(in, out)``, transposed on the device), ``"padded"`` (natural,
-    with the V factors' rows 64 elements longer in memory: the row pitch the
-    decode kernels stream fastest, see ``ops.pad_rows``) or ``"linear"``
-    (transposed views of the stored ``(out, in)`` tensors).  ``dtype``
-    optionally converts (e.g. ``torch.bfloat16``) on the device."""
-    import torch
-    from safetensors import safe_open
-
-    from .ops import pad_rows
-
-    if layout not in ("natural", "padded", "linear"):
-        raise ValueError(f"layout must be 'natural', 'padded' or 'linear', got {layout!r}")
-    model_path = Path(model_path)
-    config, index = checkpoint_metadata(model_path)
-    layer_indices = tuple(layer_indices)
-    if not layer_indices:
+    Vd)`` per layer (models/hf_svd.py:132-196); ``layout`` is "natural",
+    "padded" or "linear" (module docstring); ``dtype`` optionally converts
+    on the device."""
+    ck = SvdCheckpoint(model_path)
+    layers = tuple(layer_indices)
+    if not layers:
         raise ValueError("at least one layer must be selected")
-    weight_map = index["weight_map"]
-    keys = tuple(key for layer in layer_indices for key in factor_keys(layer))
-    names = _required_shards(model_path, weight_map, keys)
-    dev = torch.device(device)
-    layers = []
-    with ExitStack() as stack:
-        shards = {name: stack.enter_context(safe_open(str(model_path / name), framework="pt")) for name in names}
-        for layer in layer_indices:
-            factors = []
-            for i, key in enumerate(factor_keys(layer)):
-                stored = shards[weight_map[key]].get_tensor(key).to(dev)  # (out, in)
-                if dtype is not None:
-                    stored = stored.to(dtype)
-                if layout == "linear":
-                    factors.append(stored.t())
-                elif layout == "padded" and i % 2:   # Vg, Vu, Vd
-                    factors.append(pad_rows(stored.t()))
-                else:
-                    factors.append(stored.t().contiguous())
-                del stored
-            validate_factor_shapes(factors, hidden_size=int(config["hidden_size"]),
-                                   intermediate_size=int(config["intermediate_size"]))
-            layers.append(tuple(factors))
-    return tuple(layers)
+    return ck.tensors(layers, device=device, layout=layout, dtype=dtype)
 
 
 def save_mlp_checkpoint(model_path: str | Path, layers: Sequence[Sequence], *, hidden_size: int,
                         intermediate_size: int, shard_layers: int = 1, extra_config: dict | None = None) -> Path:
-    """Write gate-first natural-layout factors as a sharded checkpoint in the
-    format ``load_mlp_factors`` reads (stored transposed, v/u names swapped):
-    for synthetic test checkpoints and for exporting factors."""
+    """Write gate-first natural-layout factors in the format above (stored
+    transposed, v/u roles as the reference names them), ``shard_layers``
+    layers per shard: for synthetic test checkpoints and exported factors."""
     import torch
     from safetensors.torch import save_file
 
-    model_path = Path(model_path)
-    model_path.mkdir(parents=True, exist_ok=True)
+    root = Path(model_path)
+    root.mkdir(parents=True, exist_ok=True)
     weight_map = {}
-    for s0 in range(0, len(layers), shard_layers):
-        name = f"model-{s0 // shard_layers + 1:05d}.safetensors"
-        tensors = {}
-        for layer in range(s0, min(len(layers), s0 + shard_layers)):
-            validate_factor_shapes(layers[layer], hidden_size=hidden_size, intermediate_size=intermediate_size)
-            for key, f in zip(factor_keys(layer), layers[layer]):
-                tensors[key] = torch.as_tensor(f).detach().to("cpu").t().contiguous()
-                weight_map[key] = name
-        save_file(tensors, str(model_path / name))
+    for first in range(0, len(layers), shard_layers):
+        shard = f"model-{first // shard_layers + 1:05d}.safetensors"
+        payload = {}
+        for i in range(first, min(len(layers), first + shard_layers)):
+            validate_factor_shapes(layers[i], hidden_size=hidden_size, intermediate_size=intermediate_size)
+            for slot, f in zip(SLOTS, layers[i]):
+                payload[slot.key(i)] = torch.as_tensor(f).detach().to("cpu").t().contiguous()
+                weight_map[slot.key(i)] = shard
+        save_file(payload, str(root / shard))
     config = {"hidden_size": hidden_size, "intermediate_size": intermediate_size, "num_hidden_layers": len(layers),
-              "hidden_act": "silu", "mlp_bias": False}
-    config.update(extra_config or {})
-    (model_path / "config.json").write_text(json.dumps(config), encoding="utf-8")
-    (model_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}), encoding="utf-8")
-    return model_path
+              "hidden_act": "silu", "mlp_bias": False, **(extra_config or {})}
+    (root / CONFIG_FILE).write_text(json.dumps(config), encoding="utf-8")
+    (root / INDEX_FILE).write_text(json.dumps({"weight_map": weight_map}), encoding="utf-8")
+    return root
