@@ -54,6 +54,7 @@
 #pragma once
 
 #include "gemm_big.hpp"
+#include "sync_area.hpp"
 
 namespace svdmlp {
 
@@ -83,40 +84,6 @@ constexpr int kDlThreads = 512;
 // slice area holds kDlMaxGrid units.
 constexpr int kDlMaxGrid = 256;
 constexpr int kDlWStage = 8192;    // 32 k x 128 columns bf16
-// Default bound of a grid-barrier wait, in polls (~1 us each with the
-// device-scope load): seconds, far beyond any barrier of a resident grid.
-constexpr uint32_t kDlSpinLimit = 1u << 22;
-// Barrier words in the workspace's sync area, one 128-byte line each (in
-// uint64 units): kDlGroups group counters, then root, generation, and the
-// timeout line: word kDlFlag is nonzero once a bounded wait gave up (sticky
-// until the caller zeroes the area), word kDlSpin, if nonzero, replaces
-// kDlSpinLimit (failure tests set a tiny bound so that waits give up at once).
-constexpr int kDlGroups = 16;
-constexpr int kDlLine = 16;
-constexpr int kDlRoot = kDlGroups * kDlLine;
-constexpr int kDlGen = kDlRoot + kDlLine;
-constexpr int kDlFlag = kDlGen + kDlLine;
-constexpr int kDlSpin = kDlFlag + 1;
-// Block-done counter of the streaming-GEMV decode layer (monotone, like the
-// barrier counters: the last of every G arrivals finishes the launch); bit
-// kGvDoneBad is set with the timeout flag, so the last block learns of a
-// timeout from its own arrival.
-constexpr int kGvDone = kDlFlag + kDlLine;
-constexpr uint64_t kGvDoneBad = (uint64_t)1 << 63;
-// 32-bit arrival counters of the split-K tiles of phases 1, 3 and 4 (in
-// that order) fill the rest of the 4 KB area, kDlTileLines 128-byte lines.
-// Tile t's counter is word t / kDlTileLines of line t % kDlTileLines, so
-// neighbouring tiles, whose units finish together, hit different lines
-// (packed consecutively, ~100 blocks' atomics on 3 lines cost ~2 us per
-// layer).  The last arrival of a launch resets its tile's counter to zero.
-constexpr int kDlTileWords = kGvDone + kDlLine;
-constexpr int kDlTileLines = (512 - kDlTileWords) / kDlLine;
-constexpr int kDlMaxTiles = kDlTileLines * 32;
-constexpr int kDlSyncBytes = kDlTileWords * 8 + kDlMaxTiles * 4;
-__device__ __forceinline__ uint32_t* dl_tile_counter(uint64_t* sync, int t) {
-  return reinterpret_cast<uint32_t*>(sync + kDlTileWords) + (t % kDlTileLines) * 32 + t / kDlTileLines;
-}
-
 // Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
 // weight bytes per block barrier) and the ring holds NS stages, as far as
 // the activation tile, which shares the ring, leaves room.
@@ -149,12 +116,6 @@ __device__ __forceinline__ void dl_wait_vm() {
 // Block barrier that publishes LDS writes (ds, and DMA after the issuing
 // wave's vmcnt wait) without a global-memory fence.
 __device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// Bound of this launch's barrier waits: the workspace's override, if set.
-__device__ __forceinline__ uint32_t dl_spin_limit(uint64_t* sync) {
-  const uint64_t o = __hip_atomic_load(&sync[kDlSpin], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return o ? (uint32_t)o : kDlSpinLimit;
-}
 
 // Grid barrier k of this launch (gen0: generation at launch start).  Every
 // wave has completed its own global writes (vmcnt(0)) before calling.  If
@@ -192,7 +153,6 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
 // Buffer descriptor of the split-K slice area (kDlMaxGrid units of MT
 // 16-row blocks, 2048 floats each), the cache-policy bits of a device-scope
 // (sc1) buffer access, and an offset past every record.
-constexpr int kDlSc1 = 16;
 constexpr uint32_t kDlPastSlices = 0xfffffff0u;
 template <int MT>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dl_slice_rsrc(float* slices) {

@@ -71,9 +71,27 @@ def synthetic_factors(rng, H: int, I: int, R: int):
             random_matrix(I, R), random_matrix(R, H))
 
 
+def _time_ms(torch, fn, args, warmup: int, repeats: int) -> float:
+    """Median hipEvent time of single calls (each call waited for, as
+    test_speedup.py:739-749 times a call), after warmup calls."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup + 1):
+        fn(*args)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeats):
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
+        fn(*args)
+        end.record(stream)
+        end.synchronize()
+        times.append(begin.elapsed_time(end))
+    times.sort()
+    return times[len(times) // 2] if len(times) % 2 else 0.5 * (times[len(times) // 2 - 1] + times[len(times) // 2])
+
+
 def run(args) -> list[dict]:
     from . import compat
-    from .checkpoint_speedup import _time_ms
 
     if args.warmup < 0 or args.repeats <= 0:
         raise ValueError("warmup must be >= 0 and repeats must be > 0")
