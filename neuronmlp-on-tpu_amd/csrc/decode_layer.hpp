@@ -121,7 +121,9 @@ __device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcn
 // wave has completed its own global writes (vmcnt(0)) before calling.  If
 // the wait gives up, thread 0 sets the timeout flag (and the GEMV layer's
 // done bit), waits for both to complete, and sets *bad (LDS) for the block;
-// *bad is never cleared within a launch.
+// *bad is never cleared within a launch.  (Polling the root counter itself,
+// one atomic hop shorter, was ~2.4 us slower per layer: the polls then share
+// a line with the group completions' atomics.)
 __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k, uint32_t spin, int* bad) {
   dl_block_sync();
   if (threadIdx.x == 0) {
@@ -352,10 +354,11 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
 //  * otherwise the unit stores its rows < T as slice u (16 bytes per lane
 //    and block mt, in register order) and, once every wave's stores have
 //    completed, counts its arrival on the tile's counter; the block that
-//    completes the count resets the counter and sums the splits' slices in
-//    split order, 0 + s_0 + s_1 + ..., its own from registers (the values
-//    it stored), so the result does not depend on which unit came last;
-//    then it rounds to dst.
+//    completes the count resets the counter and sums every split's slice,
+//    its own included, in split order, 0 + s_0 + s_1 + ..., so the result
+//    does not depend on which unit came last; then it rounds to dst.  (Its
+//    own slice from registers, selected into the sum, cost ~0.4 us more per
+//    layer than the extra load.)
 // `out_y`: dst is the layer output; it receives NaN instead if this block
 // gave up a barrier wait (`bad`) or, after the last arrival, the timeout
 // flag is set.
@@ -391,8 +394,10 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
     if (!*flag) return;
     // issued with the first slices, after every split's arrival was seen
     const uint64_t tflag = out_y ? __hip_atomic_load(&sync[kDlFlag], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-    const int split = u / nt, tile = u - split * nt;
-    constexpr int SB = MT >= 8 ? 2 : 8;  // slices in flight (registers: SB * MT * 4)
+    const int tile = u % nt;
+    // slices in flight (registers: SB * MT * 4); at MT 4, 8 in flight cost
+    // ~4 us per layer at 64 tokens against 4 (scalar-register spills)
+    constexpr int SB = MT >= 8 ? 2 : (MT >= 4 ? 4 : 8);
     f32x4 sum[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) sum[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -403,26 +408,21 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
         const int s = s0 + i;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const bool live = s < splits && s != split && 16 * mt + c.lr < c.T;
+          const bool live = s < splits && 16 * mt + c.lr < c.T;
           const uint32_t off =
               live ? (uint32_t)((((tile + s * nt) * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
           v[i][mt] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kDlSc1);
         }
       }
 #pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const int s = s0 + i;
-        if (s < splits) {
-          const bool own = s == split;
+      for (int i = 0; i < SB; ++i)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            sum[mt].x += own ? acc[mt].x : __uint_as_float(v[i][mt].x);
-            sum[mt].y += own ? acc[mt].y : __uint_as_float(v[i][mt].y);
-            sum[mt].z += own ? acc[mt].z : __uint_as_float(v[i][mt].z);
-            sum[mt].w += own ? acc[mt].w : __uint_as_float(v[i][mt].w);
-          }
+        for (int mt = 0; mt < MT; ++mt) {
+          sum[mt].x += __uint_as_float(v[i][mt].x);
+          sum[mt].y += __uint_as_float(v[i][mt].y);
+          sum[mt].z += __uint_as_float(v[i][mt].z);
+          sum[mt].w += __uint_as_float(v[i][mt].w);
         }
-      }
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = sum[mt];
