@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
     for (int u = 0; u < D; ++u) ring[u] = gv_issue<RW>(P1, ic, lrow, lcol);
   }
   dl_wait_vm<D>();  // the zero stores, issued before the D loads, are done
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, &s_bad);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, nullptr, &s_bad);
 
 #pragma unroll 1
   for (int ph = 1; ph <= 4; ++ph) {
@@ -386,7 +386,7 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
     if (after_flush >= 1)
       gv_wait_after<0>(after_flush - 1);
     ic = nc;
-    if (ph < 4) dl_grid_sync(p.sync, gen0, ++nbar, spin, &s_bad);
+    if (ph < 4) dl_grid_sync(p.sync, gen0, ++nbar, spin, nullptr, &s_bad);
   }
   // drain the run-out loads (no records) before the registers are released
 #pragma unroll

@@ -117,14 +117,19 @@ __device__ __forceinline__ void dl_wait_vm() {
 // wave's vmcnt wait) without a global-memory fence.
 __device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Grid barrier k of this launch (gen0: generation at launch start).  Every
-// wave has completed its own global writes (vmcnt(0)) before calling.  If
-// the wait gives up, thread 0 sets the timeout flag (and the GEMV layer's
+// Grid barrier k of this launch (gen0: generation at launch start).  The
+// bound of the wait (dl_spin_limit) comes from spin_lds when non-null, else
+// spin_reg: where it lives changes the register allocation of the whole
+// layer kernel (8B layer: the 1-tile instance is 0.5 us faster with it in a
+// register, the 4-tile instance ~4 us faster with it in LDS).  Every wave
+// has completed its own global writes (vmcnt(0)) before calling.  If the
+// wait gives up, thread 0 sets the timeout flag (and the GEMV layer's
 // done bit), waits for both to complete, and sets *bad (LDS) for the block;
 // *bad is never cleared within a launch.  (Polling the root counter itself,
 // one atomic hop shorter, was ~2.4 us slower per layer: the polls then share
 // a line with the group completions' atomics.)
-__device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k, uint32_t spin, int* bad) {
+__device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k, uint32_t spin_reg,
+                                             const uint32_t* spin_lds, int* bad) {
   dl_block_sync();
   if (threadIdx.x == 0) {
     const uint32_t G = gridDim.x, b = blockIdx.x;
@@ -137,6 +142,7 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
       if ((r + 1) % ngroups == 0)
         __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    const uint32_t spin = spin_lds ? *spin_lds : spin_reg;
     uint32_t polls = 0;
     while ((int64_t)(__hip_atomic_load(&sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - gen0 - k) < 0) {
       __builtin_amdgcn_s_sleep(1);
@@ -215,6 +221,7 @@ struct DlLds {
   static constexpr int DUMMY_OFF = A_OFF + NS * A_SLOT;
   static constexpr int FLAG_OFF = DUMMY_OFF + 1024;  // int: "this block finishes the tile"
   static constexpr int BAD_OFF = FLAG_OFF + 4;       // int: "a barrier wait of this block gave up"
+  static constexpr int SPIN_OFF = FLAG_OFF + 8;      // uint32: bound of the grid-barrier waits (MT >= 4)
   static constexpr int BYTES = FLAG_OFF + 16;
   static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
@@ -453,7 +460,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   c.T = p.T;
   int* const flag = reinterpret_cast<int*>(lds + L::FLAG_OFF);
   int* const bad = reinterpret_cast<int*>(lds + L::BAD_OFF);
-  if (threadIdx.x == 0) *bad = 0;  // published by the block barriers ahead of its first read
+  uint32_t* const spin_lds = MT >= 4 ? reinterpret_cast<uint32_t*>(lds + L::SPIN_OFF) : nullptr;
+  uint32_t spin = 0;
+  if constexpr (MT < 4) spin = dl_spin_limit(p.sync);
+  if (threadIdx.x == 0) {  // published by the block barriers ahead of their first reads
+    *bad = 0;
+    if constexpr (MT >= 4) *spin_lds = dl_spin_limit(p.sync);
+  }
   const int G = gridDim.x, b = blockIdx.x;
   const int T = p.T;
   constexpr int NS = L::NS;
@@ -461,7 +474,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // Generation at launch start: it cannot advance before every block has
   // arrived at barrier 1, which each block does only after this read.
   const uint64_t gen0 = __hip_atomic_load(&p.sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t spin = dl_spin_limit(p.sync);
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
@@ -551,7 +563,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(2);
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, bad);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
 
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
   for (int u = b; u < units[2]; u += G) {
@@ -583,7 +595,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(3);
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, bad);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
 
   // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
   for (int u = b; u < units[3]; u += G) {
@@ -596,7 +608,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(4);
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, bad);
+  dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
   for (int u = b; u < units[4]; u += G) {
