@@ -45,8 +45,9 @@ def _args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    # the clocks take some tens of milliseconds of load to settle: with 5
-    # warmup steps the 8B layer timed ~375 us, after ~60 steps ~343 us
+    # the clocks take some tens of milliseconds of load to settle; the prefill
+    # line is timed after the other sections (see main), and the first W + K
+    # steps of the run are reported beside it as cold_start
     p.add_argument("--warmup", type=int, default=100)
     p.add_argument("--tokens", type=int, default=1024)
     p.add_argument("--layers", type=int, default=4, help="synthetic layers the steps rotate over")
@@ -115,22 +116,29 @@ def _stage_work(T):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "prefill_8b_T1024_traffic.md"
+MFMA_PROFILE = ROOT / "profiles" / "prefill_8b_T1024_mfma.md"
 TRAFFIC_LAYOUT = "padded"   # the weights layout the PMC summaries were taken with
 DECODE_TRAFFIC_PROFILE = ROOT / "profiles" / "decode_8b_traffic.md"
 
 
-def _profiled_traffic(stage, path=TRAFFIC_PROFILE):
-    """HBM bytes per launch of a stage from a committed rocprofv3 PMC summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel of known size),
-    or None when the summary has no line for it."""
+def _profiled(key, stage, path):
+    """A per-stage figure from a committed rocprofv3 summary: the value of its
+    machine-readable line ``<key> <stage> <value>``, or None."""
     try:
         for line in path.read_text().splitlines():
             parts = line.split()
-            if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == stage:
-                return int(parts[2])
+            if len(parts) == 3 and parts[0] == key and parts[1] == stage:
+                return float(parts[2])
     except OSError:
         pass
     return None
+
+
+def _profiled_traffic(stage, path=TRAFFIC_PROFILE):
+    """HBM bytes per launch of a stage (FETCH_SIZE + WRITE_SIZE, calibrated
+    against a copy kernel of known size), or None."""
+    v = _profiled("traffic_bytes", stage, path)
+    return int(v) if v is not None else None
 
 
 def _time_steps(torch, fn, steps, warmup, stream):
@@ -183,58 +191,123 @@ def _cpu_baseline(layer0, x, T, seconds):
     }, y
 
 
-def _bench_stack(torch, dev, stream, args):
-    """BASELINE config 4: the 32-layer LLaMA3-8B MLP stack, x <- x +
-    svd_mlp(RMSNorm(x) * gain) per layer, T=4096, per-branch ranks drawn from
-    {2048, ..., 3072}, eps 1e-5, gains ~ U(0.9, 1.1)."""
-    import oracle as O
+def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
+    """the 8B layer at decode token counts (GPU only)."""
+    import svdmlp
+    from svdmlp import _lib
+
+    dec = {}
+    for Td in args.decode_tokens:
+        xd = x[:Td].contiguous()
+        wsd = svdmlp.svd_mlp_workspace(xd, r=R, ff=FF)
+        outd = torch.empty(Td, D, dtype=torch.bfloat16, device=dev)
+
+        def dstep(i, xd=xd, wsd=wsd, outd=outd):
+            svdmlp.svd_mlp(xd, *layers[i % len(layers)], workspace=wsd, out=outd)
+
+        msd, _ = _time_steps(torch, dstep, args.decode_steps, max(10, args.warmup), stream)
+        with _lib.StageProfile() as prof:
+            _time_steps(torch, dstep, min(args.decode_steps, 50), 0, stream)
+        nbytes = factor_bytes + 2 * Td * D * 2
+        gbs = nbytes / (msd * 1e-3) / 1e9
+        # measured HBM bytes of the MFMA decode layer's launch (16-row token tiles: 1, 2, 4 or 8 of them)
+        mt = 1 if Td <= 16 else (2 if Td <= 32 else (4 if Td <= 64 else 8))
+        traffic = (_profiled_traffic(f"decode_layer_mt{mt}", DECODE_TRAFFIC_PROFILE)
+                   if args.weights_layout == TRAFFIC_LAYOUT and Td <= 128 else None)
+        dec[f"T={Td}"] = {
+            "us_per_layer": round(msd * 1e3, 2),
+            "GB/s": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+            "traffic_GB/s": round(traffic / (msd * 1e-3) / 1e9, 1) if traffic else None,
+            "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),
+            "stages_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.result.items()},
+        }
+        if svdmlp.workspace_status(wsd):
+            raise RuntimeError(f"decode T={Td}: a grid-barrier wait gave up (the device was shared?)")
+    return dec
+
+
+def _stack_inputs(torch, dev, args):
     from svdmlp import stack
 
-    T = args.stack_tokens
     layers = stack.make_stack(args.stack_layers, D, FF, seed=args.seed + 4, device=dev)
     gx = torch.Generator(device=dev)
     gx.manual_seed(args.seed + 4000)
-    x = torch.randn(T, D, generator=gx, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    x = torch.randn(args.stack_tokens, D, generator=gx, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    return layers, x
+
+
+def _time_stack(torch, dev, stream, args, layers, x):
+    """BASELINE config 4: the 32-layer LLaMA3-8B MLP stack, x <- x +
+    svd_mlp(RMSNorm(x) * gain) per layer, T=4096, per-branch ranks drawn from
+    {2048, ..., 3072}, eps 1e-5, gains ~ U(0.9, 1.1) (GPU only)."""
+    from svdmlp import stack
+
+    T = x.shape[0]
     ws = stack.stack_workspace(x, layers)
     bufs = (torch.empty_like(x), torch.empty_like(x))
     ms, _ = _time_steps(torch, lambda i: stack.run_stack(x, layers, eps=1e-5, workspace=ws, buffers=bufs),
                         args.stack_steps, 1, stream)
     flops = stack.stack_flops(T, D, FF, layers)
     padded = sum(2 * T * (2 * l.factors[0].shape[1] * (D + FF) + l.ranks[2] * (FF + D)) for l in layers)
-    rows = min(args.parity_rows, T)
-    y1 = stack.run_stack(x, layers[:1], eps=1e-5, workspace=ws, buffers=bufs)[:rows].float().cpu().numpy()
-    f1 = [a.float().cpu().numpy() for a in layers[0].factors]
-    ref1 = O.mlp_block_ref(x[:rows].float().cpu().numpy(), layers[0].gain.cpu().numpy(), f1, eps=1e-5,
-                           dtype="bfloat16")
-    y = stack.run_stack(x, layers, eps=1e-5, workspace=ws, buffers=bufs)
-    got = y[:rows].float().cpu().numpy()
-    ref = x[:rows].float().cpu().numpy()
-    x0 = ref.copy()
-    for l in layers:   # rows are independent through the whole stack
-        f = [a.float().cpu().numpy() for a in l.factors]
-        ref = O.mlp_block_ref(ref, l.gain.cpu().numpy(), f, eps=1e-5, dtype="bfloat16")
     tflops = flops / (ms * 1e-3) / 1e12
-    return {
+    return ws, {
         "workload": f"LLaMA3-8B MLP stack, {len(layers)} layers of RMSNorm + SVD-MLP + residual, non-uniform ranks",
         "T": T, "layers": len(layers), "ms_per_stack": round(ms, 3),
         "us_per_layer": round(ms * 1e3 / len(layers), 1), "TFLOP/s": round(tflops, 2),
         "pct_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
         "flop_per_stack": flops, "padded_flop_fraction": round(padded / flops - 1, 4),
         "ranks_first_layers": [l.ranks for l in layers[:4]],
-        "parity_rows": rows,
-        "parity_rel_l2_first_layer": round(O.relative_l2(y1, ref1), 6),
-        "parity_rel_l2_after_all_layers": round(O.relative_l2(got, ref), 6),
-        "parity_note": "both sides round to bf16 at the same points; accumulation-order differences compound "
-                       "through the RMSNorm/residual chain over the layers",
     }
 
 
-def _bench_fp8(torch, dev, stream, args):
-    """BASELINE config 5: the LLaMA3-70B-shape layer (T=2048, d=8192,
-    ff=28672, r=5632) with fp8 e4m3fn factors and per-output-channel fp32
-    scales (amax/448), bf16 activations, fp32 accumulation."""
+def _stack_parity(torch, args, layers, x, ws):
+    """Rows are independent through the whole stack: on a row subset, each
+    layer's block output against the oracle's block fed with the GPU's own
+    input rows, and the whole chain against the unrounded float64 chain, for
+    the GPU and for the oracle's own bf16 chain (two correct bf16 chains drift
+    apart through the residual stream; a measured comparison, not a
+    tolerance)."""
+    import numpy as np
+
     import oracle as O
-    import svdmlp
+    from svdmlp import ops
+
+    rows = min(args.parity_rows, x.shape[0])
+    idx = torch.arange(rows, device=x.device)
+    bufs = (torch.empty_like(x), torch.empty_like(x))
+    cur = x
+    chain = x[idx].float().cpu().numpy()
+    chain64 = chain.astype(np.float64)
+    worst = 0.0
+    first = None
+    for i, l in enumerate(layers):
+        out = ops.svd_mlp_block(cur, l.gain, *l.factors, eps=1e-5, workspace=ws, out=bufs[i % 2])
+        xin, yout = cur[idx].float().cpu().numpy(), out[idx].float().cpu().numpy()
+        f = [a.float().cpu().numpy() for a in l.factors]
+        gain = l.gain.cpu().numpy()
+        err = O.relative_l2(yout, O.mlp_block_ref(xin, gain, f, eps=1e-5, dtype="bfloat16"))
+        worst = max(worst, err)
+        first = err if first is None else first
+        chain = O.mlp_block_ref(chain, gain, f, eps=1e-5, dtype="bfloat16")
+        chain64 = O.mlp_block_f64(chain64, gain, f, eps=1e-5)
+        cur = out
+    got = cur[idx].float().cpu().numpy()
+    exact = chain64.astype(np.float32)
+    return {
+        "parity_rows": rows,
+        "parity_rel_l2_first_layer": round(first, 6),
+        "parity_rel_l2_worst_layer": round(worst, 6),
+        "after_all_layers_rel_l2_gpu_vs_float64": round(O.relative_l2(got, exact), 6),
+        "after_all_layers_rel_l2_oracle_bf16_vs_float64": round(O.relative_l2(chain, exact), 6),
+        "after_all_layers_rel_l2_gpu_vs_oracle_bf16": round(O.relative_l2(got, chain), 6),
+        "parity_note": "per layer: the GPU block vs the oracle block on the GPU's input rows; after all layers: "
+                       "both bf16 chains against the unrounded float64 chain",
+    }
+
+
+def _fp8_inputs(torch, dev, args):
     from svdmlp import fp8
 
     T, d, ff, r = args.fp8_tokens, 8192, 28672, 5632
@@ -247,25 +320,44 @@ def _bench_fp8(torch, dev, stream, args):
 
     fs = [q(d, r), q(r, ff), q(d, r), q(r, ff), q(ff, r), q(r, d)]
     x = torch.randn(T, d, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    return fs, x
+
+
+def _time_fp8(torch, dev, stream, args, fs, x):
+    """BASELINE config 5: the LLaMA3-70B-shape layer (T=2048, d=8192,
+    ff=28672, r=5632) with fp8 e4m3fn factors and per-output-channel fp32
+    scales (amax/448), bf16 activations, fp32 accumulation (GPU only)."""
+    import svdmlp
+
+    T, d = x.shape
+    ff, r = fs[1].data.shape[1], fs[0].data.shape[1]
     ws = svdmlp.svd_mlp_workspace(x, r=r, ff=ff, w_code=2)
     out = torch.empty(T, d, dtype=torch.bfloat16, device=dev)
     ms, _ = _time_steps(torch, lambda i: svdmlp.svd_mlp(x, *fs, workspace=ws, out=out), args.fp8_steps, 1, stream)
     flops = 2.0 * T * 3 * r * (d + ff)
-    y = svdmlp.svd_mlp(x, *fs, workspace=ws, out=out)
-    rows = min(args.parity_rows, T)
-    deq = [(f.data.float() * f.scale[None, :]).cpu().numpy() for f in fs]
-    ref = O.svd_mlp_ref(x[:rows].float().cpu().numpy(), *deq, dtype="bfloat16")
     tflops = flops / (ms * 1e-3) / 1e12
     fbytes = sum(f.data.numel() + 4 * f.scale.numel() for f in fs)
-    return {
+    return out, {
         "workload": "LLaMA3-70B-shape SVD-MLP layer, fp8 e4m3 factors with per-column scales, bf16 activations",
         "T": T, "d": d, "ff": ff, "r": r, "us_per_layer": round(ms * 1e3, 1), "TFLOP/s": round(tflops, 2),
         "pct_fp8_mfma_peak": round(100 * tflops / 5000.0, 2),
         "pct_bf16_mfma_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
-        "compute": "factors widened exactly to bf16 in registers, bf16 MFMA (activations stay bf16)",
-        "factor_bytes": fbytes, "parity_rows": rows,
-        "parity_rel_l2_vs_oracle": round(O.relative_l2(y[:rows].float().cpu().numpy(), ref), 6),
+        "compute": "factors widened exactly to bf16 in registers, bf16 MFMA (activations stay bf16: e4m3 "
+                   "activations would exceed the 3e-2 tolerance, tests/test_fp8_budget.py)",
+        "factor_bytes": fbytes,
     }
+
+
+def _fp8_parity(args, fs, x, y):
+    import numpy as np
+
+    import oracle as O
+
+    rows = min(args.parity_rows, x.shape[0])
+    table = O.e4m3_decode(np.arange(256, dtype=np.uint8))
+    deq = [table[f.data.view(__import__("torch").uint8).cpu().numpy()] * f.scale.cpu().numpy()[None, :] for f in fs]
+    ref = O.svd_mlp_ref(x[:rows].float().cpu().numpy(), *deq, dtype="bfloat16")
+    return {"parity_rows": rows, "parity_rel_l2_vs_oracle": round(O.relative_l2(y[:rows].float().cpu().numpy(), ref), 6)}
 
 
 def main(argv=None) -> int:
@@ -301,14 +393,28 @@ def main(argv=None) -> int:
         del src, dst
     factor_bytes = 2 * (2 * R * (D + FF) + R * (FF + D))
     record: dict = {}
+    prefill = args.only in (None, "prefill")
+    ws = svdmlp.svd_mlp_workspace(x, r=R, ff=FF)
+    out = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
 
-    if args.only in (None, "prefill"):
-        ws = svdmlp.svd_mlp_workspace(x, r=R, ff=FF)
-        out = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    def step(i):
+        svdmlp.svd_mlp(x, *layers[i % len(layers)], workspace=ws, out=out)
 
-        def step(i):
-            svdmlp.svd_mlp(x, *layers[i % len(layers)], workspace=ws, out=out)
+    # The prefill line is timed after the other GPU sections, with the clocks
+    # at their steady state under load; the same W + K steps as the first GPU
+    # work of the run (the GPU ramping up from idle) are reported beside it.
+    cold = _time_steps(torch, step, args.steps, args.warmup, stream)[0] if prefill else None
 
+    if args.only in (None, "decode"):
+        record["decode"] = _bench_decode(torch, dev, stream, args, layers, x, factor_bytes)
+    if args.only in (None, "stack"):
+        s_layers, s_x = _stack_inputs(torch, dev, args)
+        s_ws, record["stack"] = _time_stack(torch, dev, stream, args, s_layers, s_x)
+    if args.only in (None, "fp8"):
+        f_fs, f_x = _fp8_inputs(torch, dev, args)
+        f_out, record["fp8_70b"] = _time_fp8(torch, dev, stream, args, f_fs, f_x)
+
+    if prefill:
         ms, wall = _time_steps(torch, step, args.steps, args.warmup, stream)
         with _lib.StageProfile() as prof:
             ms_prof, _ = _time_steps(torch, step, args.steps, 0, stream)
@@ -322,6 +428,9 @@ def main(argv=None) -> int:
         dom_flops, dom_bytes, dom_desc = stage_work.get(dom, (None, None, None))
         achieved = dom_flops / (dom_ms * 1e-3) / 1e12 if dom_ms else None
         tflops = flops / (ms * 1e-3) / 1e12
+        profiled = (T, args.weights_layout) == (1024, TRAFFIC_LAYOUT)
+        busy = _profiled("mfma_busy", dom, MFMA_PROFILE) if profiled and dom else None
+        clock = _profiled("shader_clock_ghz", dom, MFMA_PROFILE) if profiled and dom else None
         record.update({
             "metric": METRIC,
             "value": round(tflops, 2),
@@ -341,6 +450,8 @@ def main(argv=None) -> int:
                        "layers_rotated": len(layers), "flop_per_step": flops,
                        "weights_layout": args.weights_layout},
             "wall_s_timed": round(wall, 4),
+            "cold_start": {"ms_per_step": round(cold, 4), "us_per_layer": round(cold * 1e3, 1),
+                           "note": "the same warmup and timed steps as the first GPU work of the run"},
             "roofline": {
                 "kernel": f"{dom}: {dom_desc}" if dom else None,
                 "bound": "mfma",
@@ -348,9 +459,13 @@ def main(argv=None) -> int:
                 "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4) if achieved else None,
-                "traffic": _profiled_traffic(dom) if (T, args.weights_layout) == (1024, TRAFFIC_LAYOUT) else None,
+                "traffic": _profiled_traffic(dom) if profiled else None,
                 "traffic_source": "profiles/prefill_8b_T1024_traffic.md: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
                                   "per dispatch, calibrated on a 256 MiB copy",
+                "mfma_busy": busy,
+                "shader_clock_ghz": clock,
+                "mfma_source": "profiles/prefill_8b_T1024_mfma.md: rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES, "
+                               "SQ_BUSY_CYCLES; MFMA-busy share of the SIMD cycles at the measured shader clock",
                 "algorithmic_flop_per_launch": dom_flops,
                 "algorithmic_bytes_per_launch": dom_bytes,
                 "avg_launch_us": round(dom_ms * 1e3, 2) if dom_ms else None,
@@ -358,55 +473,27 @@ def main(argv=None) -> int:
             "stages_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
             "ms_per_step_with_stage_events": round(ms_prof, 4),
         })
-        # in-bench parity on a row sample (oracle is the checker only)
-        if not args.no_cpu_baseline:
-            base, y_ref = _cpu_baseline(layers[0], x, T, args.cpu_seconds)
-            y = svdmlp.svd_mlp(x, *layers[0], workspace=ws, out=out)
-            import oracle as O
 
-            got = y[: y_ref.shape[0]].float().cpu().numpy()
-            record["parity_rel_l2_vs_oracle"] = round(O.relative_l2(got, y_ref), 6)
-            record["cpu_baseline"] = base
+    # CPU work last (the oracle is the checker only; nothing below is timed
+    # on the GPU)
+    if prefill and not args.no_cpu_baseline:
+        base, y_ref = _cpu_baseline(layers[0], x, T, args.cpu_seconds)
+        y = svdmlp.svd_mlp(x, *layers[0], workspace=ws, out=out)
+        import oracle as O
 
-    if args.only in (None, "decode"):
-        dec = {}
-        for Td in args.decode_tokens:
-            xd = x[:Td].contiguous()
-            wsd = svdmlp.svd_mlp_workspace(xd, r=R, ff=FF)
-            outd = torch.empty(Td, D, dtype=torch.bfloat16, device=dev)
-
-            def dstep(i, xd=xd, wsd=wsd, outd=outd):
-                svdmlp.svd_mlp(xd, *layers[i % len(layers)], workspace=wsd, out=outd)
-
-            msd, _ = _time_steps(torch, dstep, args.decode_steps, max(10, args.warmup), stream)
-            with _lib.StageProfile() as prof:
-                _time_steps(torch, dstep, min(args.decode_steps, 50), 0, stream)
-            nbytes = factor_bytes + 2 * Td * D * 2
-            gbs = nbytes / (msd * 1e-3) / 1e9
-            # measured HBM bytes of the MFMA decode layer's launch (16-row token tiles: 1, 2, 4 or 8 of them)
-            mt = 1 if Td <= 16 else (2 if Td <= 32 else (4 if Td <= 64 else 8))
-            traffic = (_profiled_traffic(f"decode_layer_mt{mt}", DECODE_TRAFFIC_PROFILE)
-                       if args.weights_layout == TRAFFIC_LAYOUT and Td <= 128 else None)
-            dec[f"T={Td}"] = {
-                "us_per_layer": round(msd * 1e3, 2),
-                "GB/s": round(gbs, 1),
-                "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-                "traffic": traffic,
-                "traffic_GB/s": round(traffic / (msd * 1e-3) / 1e9, 1) if traffic else None,
-                "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),
-                "stages_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.result.items()},
-            }
-        record["decode"] = dec
-        if args.only == "decode":
-            t1 = dec.get("T=1") or next(iter(dec.values()))
-            record.update({"metric": METRIC, "value": t1["GB/s"], "unit": "GB/s", "n_gpus": 1,
-                           "steps": args.decode_steps, "warmup": max(10, args.warmup), "ms_per_step": t1["us_per_layer"] / 1e3,
-                           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-                           "data": "synthetic", "config": {"workload": "LLaMA3-8B SVD-MLP layer, decode"}})
+        got = y[: y_ref.shape[0]].float().cpu().numpy()
+        record["parity_rel_l2_vs_oracle"] = round(O.relative_l2(got, y_ref), 6)
+        record["cpu_baseline"] = base
     if args.only in (None, "stack"):
-        record["stack"] = _bench_stack(torch, dev, stream, args)
+        record["stack"].update(_stack_parity(torch, args, s_layers, s_x, s_ws))
     if args.only in (None, "fp8"):
-        record["fp8_70b"] = _bench_fp8(torch, dev, stream, args)
+        record["fp8_70b"].update(_fp8_parity(args, f_fs, f_x, f_out))
+    if args.only == "decode":
+        t1 = record["decode"].get("T=1") or next(iter(record["decode"].values()))
+        record.update({"metric": METRIC, "value": t1["GB/s"], "unit": "GB/s", "n_gpus": 1,
+                       "steps": args.decode_steps, "warmup": max(10, args.warmup), "ms_per_step": t1["us_per_layer"] / 1e3,
+                       "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+                       "data": "synthetic", "config": {"workload": "LLaMA3-8B SVD-MLP layer, decode"}})
     print(json.dumps(record), flush=True)
     return 0
 
