@@ -1,6 +1,7 @@
 // RMSNorm prologue and residual epilogue of the MLP block
 // y = x + svd_mlp(rmsnorm(x) * gain)  (models/modeling_llama.py:253-262,
-// bench/e2e_block.py:268-278).  Both are single HBM passes over (T, d).
+// bench/e2e_block.py:268-278).  Both are single HBM passes over (T, d),
+// moved in 16-byte pieces (8 bf16 or 4 fp32 per lane access).
 #include <algorithm>
 
 #include "dispatch.hpp"
@@ -11,13 +12,52 @@ namespace {
 
 // One 256-thread block per row: mean of squares in fp32, then
 // y = act(gain * (x * (1 / sqrt(mean + eps)))), the order of LlamaRMSNorm.
-template <bool BF16>
+// VEC: d is a multiple of 8 (bf16) / 4 (fp32) and the rows are 16-byte
+// aligned, so each thread moves whole 16-byte pieces; the row is read once
+// into registers (up to PER pieces per thread) and written from them.
+template <bool BF16, bool VEC>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, const float* gain, void* y, int64_t d,
                                                       float eps) {
-  __shared__ float part[8];
+  __shared__ float part[4];
   const int64_t row = blockIdx.x;
+  constexpr int E = BF16 ? 8 : 4;  // elements per 16-byte piece
+  constexpr int PER = 4;           // pieces per thread kept in registers (rows up to 256 * 4 * E)
   float ss = 0.f;
-  if constexpr (BF16) {
+  u32x4 keep[PER];
+  const int64_t pieces = d / E;
+  if constexpr (VEC) {
+    const u32x4* xr = reinterpret_cast<const u32x4*>(static_cast<const char*>(x) + row * d * (BF16 ? 2 : 4));
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t i = threadIdx.x + 256 * q;
+      keep[q] = i < pieces ? xr[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    for (int64_t i = threadIdx.x + 256 * PER; i < pieces; i += 256) {  // rows longer than the register copy
+      const u32x4 v = xr[i];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if constexpr (BF16) {
+          const float a = bf16_bits_to_f32(v[w] & 0xffffu), b = bf16_bits_to_f32(v[w] >> 16);
+          ss += a * a + b * b;
+        } else {
+          const float a = __uint_as_float(v[w]);
+          ss += a * a;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if constexpr (BF16) {
+          const float a = bf16_bits_to_f32(keep[q][w] & 0xffffu), b = bf16_bits_to_f32(keep[q][w] >> 16);
+          ss += a * a + b * b;
+        } else {
+          const float a = __uint_as_float(keep[q][w]);
+          ss += a * a;
+        }
+      }
+  } else if constexpr (BF16) {
     const uint16_t* xr = static_cast<const uint16_t*>(x) + row * d;
     for (int64_t j = threadIdx.x; j < d; j += 256) {
       const float v = bf16_bits_to_f32(xr[j]);
@@ -32,7 +72,35 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, const float
   __syncthreads();
   const float tot = part[0] + part[1] + part[2] + part[3];
   const float rstd = 1.0f / sqrtf(tot / (float)d + eps);
-  if constexpr (BF16) {
+  if constexpr (VEC) {
+    const char* xb = static_cast<const char*>(x) + row * d * (BF16 ? 2 : 4);
+    u32x4* yr = reinterpret_cast<u32x4*>(static_cast<char*>(y) + row * d * (BF16 ? 2 : 4));
+    auto norm = [&](u32x4 v, int64_t i) {
+      const f32x4* g = reinterpret_cast<const f32x4*>(gain + i * E);
+      u32x4 o;
+      if constexpr (BF16) {
+        const f32x4 g0 = g[0], g1 = g[1];
+        const float gl[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          o[w] = pack_bf16x2(gl[2 * w] * (bf16_bits_to_f32(v[w] & 0xffffu) * rstd),
+                             gl[2 * w + 1] * (bf16_bits_to_f32(v[w] >> 16) * rstd));
+      } else {
+        const f32x4 g0 = g[0];
+        const float gl[4] = {g0.x, g0.y, g0.z, g0.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) o[w] = __float_as_uint(gl[w] * (__uint_as_float(v[w]) * rstd));
+      }
+      return o;
+    };
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t i = threadIdx.x + 256 * q;
+      if (i < pieces) yr[i] = norm(keep[q], i);
+    }
+    for (int64_t i = threadIdx.x + 256 * PER; i < pieces; i += 256)
+      yr[i] = norm(reinterpret_cast<const u32x4*>(xb)[i], i);
+  } else if constexpr (BF16) {
     const uint16_t* xr = static_cast<const uint16_t*>(x) + row * d;
     uint16_t* yr = static_cast<uint16_t*>(y) + row * d;
     for (int64_t j = threadIdx.x; j < d; j += 256)
@@ -44,40 +112,75 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, const float
   }
 }
 
-// y = act(x + y), the residual add rounded to the activation dtype.
-template <bool BF16>
+// y = act(x + y), the residual add rounded to the activation dtype; VEC: n is
+// a multiple of the 16-byte piece and both buffers are 16-byte aligned.
+template <bool BF16, bool VEC>
 __global__ void residual_add_kernel(const void* x, void* y, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    if constexpr (BF16) {
-      const uint16_t* xs = static_cast<const uint16_t*>(x);
-      uint16_t* ys = static_cast<uint16_t*>(y);
-      ys[i] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(xs[i]) + bf16_bits_to_f32(ys[i]));
-    } else {
-      static_cast<float*>(y)[i] += static_cast<const float*>(x)[i];
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if constexpr (VEC) {
+    const u32x4* xs = static_cast<const u32x4*>(x);
+    u32x4* ys = static_cast<u32x4*>(y);
+    const int64_t pieces = n / (BF16 ? 8 : 4);
+    for (int64_t i = t0; i < pieces; i += stride) {
+      const u32x4 a = xs[i], b = ys[i];
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if constexpr (BF16)
+          o[w] = pack_bf16x2(bf16_bits_to_f32(a[w] & 0xffffu) + bf16_bits_to_f32(b[w] & 0xffffu),
+                             bf16_bits_to_f32(a[w] >> 16) + bf16_bits_to_f32(b[w] >> 16));
+        else
+          o[w] = __float_as_uint(__uint_as_float(a[w]) + __uint_as_float(b[w]));
+      }
+      ys[i] = o;
+    }
+  } else {
+    for (int64_t i = t0; i < n; i += stride) {
+      if constexpr (BF16) {
+        const uint16_t* xs = static_cast<const uint16_t*>(x);
+        uint16_t* ys = static_cast<uint16_t*>(y);
+        ys[i] = (uint16_t)f32_to_bf16_bits(bf16_bits_to_f32(xs[i]) + bf16_bits_to_f32(ys[i]));
+      } else {
+        static_cast<float*>(y)[i] += static_cast<const float*>(x)[i];
+      }
     }
   }
 }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
 hipError_t launch_rmsnorm(const void* x, const float* gain, void* y, int64_t T, int64_t d, float eps, bool bf16,
                           hipStream_t st) {
   if (T <= 0) return hipSuccess;
-  if (bf16)
-    hipLaunchKernelGGL(rmsnorm_kernel<true>, dim3((unsigned)T), dim3(256), 0, st, x, gain, y, d, eps);
+  const bool vec = d % (bf16 ? 8 : 4) == 0 && aligned16(x) && aligned16(y) && aligned16(gain);
+  const dim3 grid((unsigned)T), block(256);
+  if (bf16 && vec)
+    hipLaunchKernelGGL((rmsnorm_kernel<true, true>), grid, block, 0, st, x, gain, y, d, eps);
+  else if (bf16)
+    hipLaunchKernelGGL((rmsnorm_kernel<true, false>), grid, block, 0, st, x, gain, y, d, eps);
+  else if (vec)
+    hipLaunchKernelGGL((rmsnorm_kernel<false, true>), grid, block, 0, st, x, gain, y, d, eps);
   else
-    hipLaunchKernelGGL(rmsnorm_kernel<false>, dim3((unsigned)T), dim3(256), 0, st, x, gain, y, d, eps);
+    hipLaunchKernelGGL((rmsnorm_kernel<false, false>), grid, block, 0, st, x, gain, y, d, eps);
   return hipGetLastError();
 }
 
 hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hipStream_t st) {
   if (n <= 0) return hipSuccess;
-  const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
-  if (bf16)
-    hipLaunchKernelGGL(residual_add_kernel<true>, dim3(blocks), dim3(256), 0, st, x, y, n);
+  const bool vec = n % (bf16 ? 8 : 4) == 0 && aligned16(x) && aligned16(y);
+  const int64_t work = vec ? n / (bf16 ? 8 : 4) : n;
+  const unsigned blocks = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
+  if (bf16 && vec)
+    hipLaunchKernelGGL((residual_add_kernel<true, true>), dim3(blocks), dim3(256), 0, st, x, y, n);
+  else if (bf16)
+    hipLaunchKernelGGL((residual_add_kernel<true, false>), dim3(blocks), dim3(256), 0, st, x, y, n);
+  else if (vec)
+    hipLaunchKernelGGL((residual_add_kernel<false, true>), dim3(blocks), dim3(256), 0, st, x, y, n);
   else
-    hipLaunchKernelGGL(residual_add_kernel<false>, dim3(blocks), dim3(256), 0, st, x, y, n);
+    hipLaunchKernelGGL((residual_add_kernel<false, false>), dim3(blocks), dim3(256), 0, st, x, y, n);
   return hipGetLastError();
 }
 

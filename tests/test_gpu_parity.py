@@ -480,6 +480,22 @@ def test_mlp_block(gpu, T):
     assert _rel(y - xb, ref - xb) < BF16_TOL
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 256), (torch.bfloat16, 260), (torch.float32, 258)])
+def test_mlp_block_fp32_and_odd_widths(gpu, dtype, d):
+    """The block's RMSNorm and residual kernels in fp32 and on widths that
+    are no multiple of the 16-byte piece (their element-wise form)."""
+    shape = inputs.LayerShape(d, 392, 72)
+    x, f = inputs.make_layer(shape, T=37, seed=d)
+    gain = np.random.default_rng(d).uniform(0.9, 1.1, size=d).astype(np.float32)
+    name = "bfloat16" if dtype == torch.bfloat16 else "float32"
+    xr, *fr = _rounded((x, *f), dtype) if dtype == torch.bfloat16 else (x, *f)
+    t = [_to(a, dtype, gpu) for a in (xr, *fr)]
+    y = _np(ops.svd_mlp_block(t[0], torch.from_numpy(gain).to(gpu), *t[1:], eps=1e-5))
+    ref = O.mlp_block_ref(xr, gain, fr, eps=1e-5, dtype=name)
+    tol = BF16_TOL if dtype == torch.bfloat16 else 1e-4
+    assert _rel(y, ref) < tol and _rel(y - xr, ref - xr) < tol
+
+
 def test_mlp_stack_nonuniform_ranks(gpu):
     """Three blocks with independently drawn gate/up/down ranks (gate and up
     zero-padded to a common rank) against the oracle, layer after layer."""
