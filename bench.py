@@ -250,7 +250,9 @@ def _time_stack(torch, dev, stream, args, layers, x):
     ms, _ = _time_steps(torch, lambda i: stack.run_stack(x, layers, eps=1e-5, workspace=ws, buffers=bufs),
                         args.stack_steps, 1, stream)
     flops = stack.stack_flops(T, D, FF, layers)
-    padded = sum(2 * T * (2 * l.factors[0].shape[1] * (D + FF) + l.ranks[2] * (FF + D)) for l in layers)
+    # FLOPs at the ranks the kernels run (each branch at its drawn rank: 0 padding)
+    padded = sum(2 * T * ((l.factors[0].shape[1] + l.factors[2].shape[1]) * (D + FF) + l.factors[4].shape[1] * (FF + D))
+                 for l in layers)
     tflops = flops / (ms * 1e-3) / 1e12
     return ws, {
         "workload": f"LLaMA3-8B MLP stack, {len(layers)} layers of RMSNorm + SVD-MLP + residual, non-uniform ranks",

@@ -62,6 +62,7 @@ extern "C" {
 #define SVDMLP_OK 0
 #define SVDMLP_EINVAL (-1)
 #define SVDMLP_EHIP (-2)
+#define SVDMLP_EUNSUP (-3) /* valid arguments that no kernel of this build takes (see svdmlp_svd_mlp_ranks) */
 
 /* Library version (SVDMLP_VERSION of the build). */
 int svdmlp_version(void);
@@ -174,6 +175,33 @@ int svdmlp_svd_mlp_block_ld(const void* x, const float* norm_w, float eps, const
                             const float* const* scales /* 6 or NULL */, const int64_t* ld /* 6 or NULL */, void* y,
                             int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype,
                             int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * svdmlp_svd_mlp_ld and svdmlp_svd_mlp_block_ld with a gate rank r_g and an
+ * up rank r_u of their own: ug (d, r_g), vg (r_g, ff), uu (d, r_u),
+ * vu (r_u, ff).  kernels/reference.py:54-72 (fused_gate_up_ref) places no
+ * constraint between the two ranks; the reference's TPU launcher rejects
+ * them ("gate/up factors must have matching shapes", test_speedup.py:
+ * 532-533), so its non-uniform models zero-pad the smaller branch.  Here
+ * each branch runs at its own rank on the large-tile path (more than 128
+ * tokens, bf16 activations, bf16 or fp8 weights, 16-byte aligned, d, ff
+ * and ranks multiples of 32); with padded rows, gate and up may have pitches
+ * of their own.  Other shapes with r_g != r_u return SVDMLP_EUNSUP (pad the
+ * smaller branch with zero U columns and V rows, which changes nothing in
+ * the result, and call with one rank).  The workspace is sized with
+ * r = max(r_g, r_u, r_d).  r_g == r_u is svdmlp_svd_mlp_ld.
+ */
+int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                         const void* ud, const void* vd, const float* const* scales /* 6 or NULL */,
+                         const int64_t* ld /* 6 or NULL */, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_g,
+                         int64_t r_u, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                         void* workspace, size_t ws_bytes, void* stream);
+int svdmlp_svd_mlp_block_ranks(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
+                               const void* uu, const void* vu, const void* ud, const void* vd,
+                               const float* const* scales /* 6 or NULL */, const int64_t* ld /* 6 or NULL */,
+                               void* y, int64_t T, int64_t d, int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d,
+                               int32_t act_dtype, int32_t w_dtype, uint32_t flags, void* workspace,
+                               size_t ws_bytes, void* stream);
 
 /*
  * svdmlp_svd_mlp_ld without a workspace argument: the layer runs in a fixed

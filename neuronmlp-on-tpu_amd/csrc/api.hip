@@ -439,11 +439,19 @@ int big_nw(int fn, int epi, bool b_kc) { return (fn == 8 && epi == BEPI_STORE &&
 // Tile shapes whose fragment-order split-K slices the reduction kernel takes.
 bool big_frag_reduce_ok(int fn, int nw) { return (nw == 8 && (fn == 8 || fn == 4)) || (nw == 4 && fn == 8); }
 
+// Batch entry 1 of a large-tile launch whose two entries differ in width
+// (gate and up ranks): its output columns, B row pitch, output row pitch
+// and B bytes.  Its column tiles follow entry 0's in one grid.
+struct Entry1 {
+  int N;
+  int64_t ldb, ldo, b_bytes;
+};
+
 int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
-             int gfrag = 0, int out_frag = 0) {
+             int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr) {
   BigParams p{};
   p.gfrag = gfrag;
   p.out_frag = out_frag;
@@ -456,19 +464,29 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   p.b[0] = b0;
   p.b[1] = b1 ? b1 : b0;
   p.a_bytes[0] = p.a_bytes[1] = (uint32_t)a_bytes;
-  p.b_bytes[0] = p.b_bytes[1] = (uint32_t)b_bytes;
+  p.b_bytes[0] = (uint32_t)b_bytes;
+  p.b_bytes[1] = (uint32_t)(e1 ? e1->b_bytes : b_bytes);
   p.lda = lda;
-  p.ldb = ldb;
+  p.ldb[0] = ldb;
+  p.ldb[1] = e1 ? e1->ldb : ldb;
   p.out = out;
-  p.ldo = ldo;
+  p.ldo[0] = ldo;
+  p.ldo[1] = e1 ? e1->ldo : ldo;
   p.out_bstride = out_bstride;
   p.out_sstride = out_sstride;
   p.gmem = gmem;
   p.M = M;
-  p.N = N;
+  p.N[0] = N;
+  p.N[1] = e1 ? e1->N : N;
   p.K = K;
   p.mtiles = (M + 255) / 256;
   p.ntiles = (N + 32 * fn - 1) / (32 * fn);
+  if (e1) {  // both entries' column tiles in one grid of z = 1
+    if (batch != 2) return fail("large-tile GEMM: a second entry of its own width needs a batch of two");
+    p.nt0 = p.ntiles;
+    p.ntiles += (e1->N + 32 * fn - 1) / (32 * fn);
+    batch = 1;
+  }
   p.k_split = k_split;
   const int splits = (K + k_split - 1) / k_split;
   const BigDesc d{fn, b_kc, epi, out_f32, fp8, big_nw(fn, epi, b_kc)};
@@ -492,11 +510,15 @@ namespace {
 // The constants are measured on MI355X: a 32-k step costs ~41 cycles per
 // MFMA of the wave tile (64 x 32*fn), prologue + epilogue ~20k cycles, and
 // a slice byte ~0.00045 cycles each way (~4 TB/s at ~1.8 GHz).
-int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch) {
+// N1 >= 0: a second batch entry N1 columns wide (its own column tiles);
+// otherwise `batch` entries of N columns.
+int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch, int64_t N1 = -1) {
   const int64_t cus = tune().split;
-  const int64_t tiles = ((T + 255) / 256) * ((N + 32 * fn - 1) / (32 * fn)) * batch;
+  const int64_t bn = 32 * fn;
+  const int64_t ntl = N1 >= 0 ? (N + bn - 1) / bn + (N1 + bn - 1) / bn : ((N + bn - 1) / bn) * batch;
+  const int64_t tiles = ((T + 255) / 256) * ntl;
   const double c_step = 41.0 * 4 * fn, c_block = 20000.0;
-  const double c_slice = 0.0009 * (double)batch * (double)T * (double)N * 4.0;
+  const double c_slice = 0.0009 * (double)T * (double)(N1 >= 0 ? N + N1 : batch * N) * 4.0;
   int64_t best_ks = K;
   double best = -1.0;
   const int64_t max_s = std::max<int64_t>(1, std::min<int64_t>(64, K / 128));
@@ -525,9 +547,50 @@ int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
 struct FactorLd {
   int64_t u, v, ud, vd;
   bool dense;
+  int64_t uu = 0, vu = 0;  // up-branch pitches when they differ from u, v (distinct gate and up ranks)
 };
 
 FactorLd dense_ld(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d) { return FactorLd{r_gu, ff, r_d, d, true}; }
+
+// XU_g, XU_u = A . Ug, A . Uu of ranks r and r1 != r (one launch, the two
+// entries' column tiles side by side) into bf16 ws.xu_bf16: (T, r) then
+// (T, r1).  Split-K as in big_xu when the fragment-order slices fit the
+// workspace's slice area, else one split.
+int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
+            int T, int K, int r, int r1, char* ws, const Ws& L, const float* const* su, int64_t ldu, int64_t ldu1) {
+  const int fn = tune().s1;
+  const int nw = big_nw(fn, BEPI_STORE, u_lin);
+  uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
+  const int64_t ldb0 = u_lin ? K : (ldu ? ldu : r), ldb1 = u_lin ? K : (ldu1 ? ldu1 : r1);
+  const int64_t b0 = (int64_t)(u_lin ? r : K) * ldb0 * wbytes(c), b1 = (int64_t)(u_lin ? r1 : K) * ldb1 * wbytes(c);
+  const float* s0 = su ? su[0] : nullptr;
+  const float* s1 = su ? su[1] : nullptr;
+  const int64_t bn = 32 * fn, tp = (T + 255) / 256 * 256;
+  const int64_t per0 = tp * ((r + bn - 1) / bn * bn), per1 = tp * ((r1 + bn - 1) / bn * bn);
+  int ks = plan_ksplit(T, K, r, fn, 2, r1);
+  int splits = (K + ks - 1) / ks;
+  if (splits > 1 && (!big_frag_reduce_ok(fn, nw) || (int64_t)splits * (per0 + per1) * 4 > (int64_t)(L.norm - L.part))) {
+    ks = K;
+    splits = 1;
+  }
+  const Entry1 e1{r1, ldb1, r1, b1};
+  if (splits == 1)
+    return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, K, xu, r,
+                    (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, &e1);
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, ks, part, r,
+                    per0, nullptr, true, per0 + per1, s0, s1, 0, 1, &e1);
+  if (rc) return rc;
+  StageScope fin(ST_FINALIZE, c.st);
+  const int mt = (int)(tp / 256);
+  rc = check(launch_reduce_frag_bf16(part, splits, per0 + per1, 0, xu, r, 0, T, r, mt, (int)(per0 / tp / bn), fn, nw,
+                                     1, c.st),
+             "split-K reduce");
+  if (rc) return rc;
+  return check(launch_reduce_frag_bf16(part + per0, splits, per0 + per1, 0, xu + (int64_t)T * r, r1, 0, T, r1, mt,
+                                       (int)(per1 / tp / bn), fn, nw, 1, c.st),
+               "split-K reduce");
+}
 
 // XU_b = A . U_b (b < batch) into bf16 ws.xu_bf16, batch stride T*r.  With
 // too few output tiles for the chip, K is split: each split writes an fp32
@@ -570,17 +633,21 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
 
 // out = SiLU(XUg . Vg) * (XUu . Vu): a g pass (bf16 g to the workspace) and a
 // u pass whose epilogue applies SiLU(g) * u.
+// The up branch's rank r_u may differ from the gate branch's r (0: the same).
 int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, const void* vg, const void* vu,
                bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, float* part, int64_t part_cap,
-               const float* s_vg = nullptr, const float* s_vu = nullptr, int64_t ldv = 0) {
+               const float* s_vg = nullptr, const float* s_vu = nullptr, int64_t ldv = 0, int r_u = 0,
+               int64_t ldv_u = 0) {
+  if (r_u <= 0) r_u = r;
   int fn = tune().s2fn;
   // 256 x 224 tiles (fn 7) leave most CUs idle at one or two 256-row tiles
   // of tokens; 256 x 128 tiles (fn 4) double the block count there (8B
   // layer: T=256 268 -> 245 us, T=512 298 -> 288 us; from three row tiles on
   // fn 7 is faster: T=768 349 vs 428 us).
   if (fn == 0) fn = (T <= 512 && ff % 128 == 0) ? 4 : ((ff % 224 == 0) ? 7 : 8);
-  const int64_t ldb = v_lin ? r : (ldv ? ldv : ff);
+  const int64_t ldb = v_lin ? r : (ldv ? ldv : ff), ldb_u = v_lin ? r_u : (ldv_u ? ldv_u : ldb);
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? ff : r) * ldb * wbytes(c);
+  const int64_t xuu_bytes = (int64_t)T * r_u * 2, vu_bytes = (int64_t)(v_lin ? ff : r_u) * ldb_u * wbytes(c);
   // One row tile of 256 x 128 tiles: each block streams its whole V column
   // panel, so the passes run at the panel's stream rate per block (8B layer,
   // T=256: 62 us for the g pass); two K splits put twice the blocks on the
@@ -593,10 +660,11 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   // T=384: 221 -> 233 us).
   const int sfn = T <= 256 ? 4 : 8;
   const int64_t per = (int64_t)((T + 255) / 256 * 256) * ((ff + 32 * sfn - 1) / (32 * sfn) * (32 * sfn));
-  if ((T <= 256 || (T > 448 && T <= 512 && ff % 256 == 0)) && fn == 4 && r >= 64 && tune().gusplit &&
+  if ((T <= 256 || (T > 448 && T <= 512 && ff % 256 == 0)) && fn == 4 && r >= 64 && r_u >= 64 && tune().gusplit &&
       2 * per * 4 <= part_cap) {
     fn = sfn;
     const int ks = (r / 2 + 31) / 32 * 32, splits = (r + ks - 1) / ks;
+    const int ks_u = (r_u / 2 + 31) / 32 * 32, splits_u = (r_u + ks_u - 1) / ks_u;
     int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
                       BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
     if (rc) return rc;
@@ -604,12 +672,12 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
       StageScope fin(ST_FINALIZE, c.st);
       if ((rc = check(launch_reduce_bf16(part, splits, per, gbuf, per, c.st), "split-K reduce"))) return rc;
     }
-    rc = big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
-                  BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
+    rc = big_gemm(c, ST_GU_XUV, xu_u, nullptr, r_u, xuu_bytes, vu, nullptr, ldb_u, vu_bytes, v_lin, T, ff, r_u, 1, fn,
+                  BEPI_STORE, ks_u, part, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
     const int mt = (T + 255) / 256;
-    return check(launch_reduce_frag_bf16(part, splits, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff, T,
+    return check(launch_reduce_frag_bf16(part, splits_u, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff, T,
                                          ff, mt, (int)(per / (256 * mt) / (32 * fn)), fn, big_nw(fn, BEPI_STORE, v_lin), 1,
                                          c.st, gbuf),
                  "split-K SwiGLU reduce");
@@ -617,8 +685,8 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,
                     1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
   if (rc) return rc;
-  return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r, xu_bytes, vu, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1,
-                  fn, BEPI_SWIGLU_MEM, r, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1);
+  return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r_u, xuu_bytes, vu, nullptr, ldb_u, vu_bytes, v_lin, T, ff, r_u, 1,
+                  fn, BEPI_SWIGLU_MEM, r_u, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1);
 }
 
 // y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
@@ -911,22 +979,31 @@ int svdmlp_svd_mlp_block_ld(const void* x, const float* norm_w, float eps, const
                             const float* const* scales, const int64_t* ld, void* y, int64_t T, int64_t d, int64_t ff,
                             int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
                             void* workspace, size_t ws_bytes, void* stream) {
+  return svdmlp_svd_mlp_block_ranks(x, norm_w, eps, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_gu, r_gu, r_d,
+                                    act_dtype, w_dtype, flags, workspace, ws_bytes, stream);
+}
+
+int svdmlp_svd_mlp_block_ranks(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
+                               const void* uu, const void* vu, const void* ud, const void* vd,
+                               const float* const* scales, const int64_t* ld, void* y, int64_t T, int64_t d,
+                               int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d, int32_t act_dtype, int32_t w_dtype,
+                               uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
   g_err.clear();
-  int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
+  int rc = validate_dims(T, d, ff, std::min(std::min(r_g, r_u), r_d));
   if (rc) return rc;
   if ((rc = check_types(act_dtype, w_dtype))) return rc;
   if (!x || !norm_w || !y || !workspace) return fail("null pointer argument");
   if (x == y) return fail("x and y must not alias (y receives the MLP output before the residual add)");
   if (!(eps > 0.0f)) return fail("eps must be positive, got %g", (double)eps);
-  const int64_t r = std::max(r_gu, r_d);
+  const int64_t r = std::max(std::max(r_g, r_u), r_d);
   const Ws L = ws_layout(T, d, ff, r);
   if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
   const bool bf16 = act_dtype == SVDMLP_BF16;
   hipStream_t st = (hipStream_t)stream;
   void* h = static_cast<char*>(workspace) + L.norm;
   if ((rc = check(launch_rmsnorm(x, norm_w, h, T, d, eps, bf16, st), "RMSNorm"))) return rc;
-  if ((rc = svdmlp_svd_mlp_ld(h, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_gu, r_d, act_dtype, w_dtype,
-                              flags, workspace, ws_bytes, stream)))
+  if ((rc = svdmlp_svd_mlp_ranks(h, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_g, r_u, r_d, act_dtype,
+                                 w_dtype, flags, workspace, ws_bytes, stream)))
     return rc;
   return check(launch_residual_add(x, y, T * d, bf16, st), "residual add");
 }
@@ -1143,8 +1220,16 @@ int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void*
                       const void* vd, const float* const* scales, const int64_t* ld_in, void* y, int64_t T, int64_t d,
                       int64_t ff, int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
                       void* workspace, size_t ws_bytes, void* stream) {
+  return svdmlp_svd_mlp_ranks(x, ug, vg, uu, vu, ud, vd, scales, ld_in, y, T, d, ff, r_gu, r_gu, r_d, act_dtype,
+                              w_dtype, flags, workspace, ws_bytes, stream);
+}
+
+int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                         const void* ud, const void* vd, const float* const* scales, const int64_t* ld_in, void* y,
+                         int64_t T, int64_t d, int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d, int32_t act_dtype,
+                         int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
   g_err.clear();
-  int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
+  int rc = validate_dims(T, d, ff, std::min(std::min(r_g, r_u), r_d));
   if (rc) return rc;
   if ((rc = check_types(act_dtype, w_dtype))) return rc;
   if (!x || !ug || !vg || !uu || !vu || !ud || !vd || !y || !workspace) return fail("null pointer argument");
@@ -1156,17 +1241,22 @@ int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void*
   }
   if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR)) return fail("unsupported flags 0x%x", flags);
   if (fp8 && flags) return fail("fp8 weights must use the natural layout");
-  const int64_t r = std::max(r_gu, r_d);
+  // one rank for both branches below; two ranks only on the large-tile path
+  const bool two = r_g != r_u;
+  const int64_t r_gu = r_g;
+  const int64_t r = std::max(std::max(r_g, r_u), r_d);
   const Ws L = ws_layout(T, d, ff, r);
   if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
   const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
   const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR;
-  bool vec = d % 8 == 0 && ff % 8 == 0 && r_gu % 8 == 0 && r_d % 8 == 0;
+  bool vec = d % 8 == 0 && ff % 8 == 0 && r_g % 8 == 0 && r_u % 8 == 0 && r_d % 8 == 0;
   for (const void* q : {x, ug, vg, uu, vu, ud, vd, (const void*)y, (const void*)workspace}) vec = vec && aligned16(q);
   if (fp8 && !vec) return fail("fp8 weights need d, ff and ranks to be multiples of 8 and 16-byte aligned buffers");
   FactorLd ld = dense_ld(d, ff, r_gu, r_d);
+  ld.uu = r_u;
+  ld.vu = ff;
   if (ld_in) {
-    const int64_t rows[6] = {r_gu, ff, r_gu, ff, r_d, d};  // row length of ug, vg, uu, vu, ud, vd
+    const int64_t rows[6] = {r_g, ff, r_u, ff, r_d, d};  // row length of ug, vg, uu, vu, ud, vd
     int64_t got[6];
     for (int i = 0; i < 6; ++i) {
       got[i] = ld_in[i] ? ld_in[i] : rows[i];
@@ -1180,14 +1270,48 @@ int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void*
         return fail("factors with padded rows need bf16 natural-layout factors, 16-byte aligned");
       for (int i = 0; i < 6; ++i)
         if (got[i] % 8) return fail("leading dimensions must be multiples of 8 elements (16-byte rows)");
-      if (got[0] != got[2] || got[1] != got[3]) return fail("gate and up factors must share their leading dimensions");
-      ld = FactorLd{got[0], got[1], got[4], got[5], false};
+      if (!two && (got[0] != got[2] || got[1] != got[3]))
+        return fail("gate and up factors must share their leading dimensions");
+      ld = FactorLd{got[0], got[1], got[4], got[5], false, got[2], got[3]};
     }
   }
   char* ws = static_cast<char*>(workspace);
   const float* S[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (fp8)
     for (int i = 0; i < 6; ++i) S[i] = scales[i];
+
+  if (two) {
+    // The large-tile path runs each branch at its own rank: X.Ug and X.Uu
+    // in one launch (their column tiles side by side), then the g pass over
+    // r_g and the u pass over r_u.
+    const bool big2 = T > kDecodeMaxT &&
+                      big_ok(c, vec, {T * d * 2, d * ld.u * 2, d * ld.uu * 2, r_g * ld.v * 2, r_u * ld.vu * 2,
+                                      T * ff * 2, ff * ld.ud * 2, r_d * ld.vd * 2},
+                             {d, r_g, r_u, ff, r_d});
+    if (!big2) {
+      fail("distinct gate and up ranks (%lld, %lld) run on the large-tile path only (bf16 activations, bf16 or fp8 "
+           "weights, more than %lld tokens, 16-byte aligned, d, ff and ranks multiples of 32); pad the smaller "
+           "branch with zero U columns and V rows for this shape",
+           (long long)r_g, (long long)r_u, (long long)kDecodeMaxT);
+      return SVDMLP_EUNSUP;
+    }
+    const void* us[2] = {ug, uu};
+    const float* sus[2] = {S[0], S[2]};
+    if ((rc = big_xu2(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, (int)T, (int)d, (int)r_g, (int)r_u, ws, L, sus,
+                      ld.u, ld.uu)))
+      return rc;
+    const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
+    uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
+    uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
+    if ((rc = big_swiglu(c, xu, xu + T * r_g, vg, vu, v_lin, (int)T, (int)r_g, (int)ff, gbuf, hbuf,
+                         reinterpret_cast<float*>(ws + L.part), (int64_t)(L.norm - L.part), S[1], S[3], ld.v,
+                         (int)r_u, ld.vu)))
+      return rc;
+    const void* ud1[1] = {ud};
+    const float* sud[1] = {S[4]};
+    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) return rc;
+    return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);
+  }
 
   // With padded V rows the MFMA decode layer is the faster one at every T
   // (8B layer at T=1: 75.5 us against 78 us): the streaming-GEMV layer reads

@@ -152,20 +152,26 @@ __device__ __forceinline__ int bnat_swz(int k) { return k & 3; }
 enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2, BEPI_STORE_FRAG = 3 };
 
 struct BigParams {
-  const void* a[2];  // per batch entry (blockIdx.z)
+  const void* a[2];  // per batch entry
   const void* b[2];
   uint32_t a_bytes[2], b_bytes[2];
-  int64_t lda, ldb;  // elements
+  int64_t lda;        // elements
+  int64_t ldb[2];     // per batch entry, elements
   void* out;
-  int64_t ldo;
-  int64_t out_bstride;   // elements between batch outputs
+  int64_t ldo[2];     // per batch entry, elements
+  int64_t out_bstride;   // elements from batch entry 0's output to entry 1's
   int64_t out_sstride;   // elements between split-K partial slices (fp32 output)
   const uint16_t* gmem;  // BEPI_SWIGLU_MEM: bf16 gate values, same layout as out
   const float* scale[2]; // fp8 B: one fp32 scale per output column, per batch entry
   int gfrag;             // BEPI_SWIGLU_MEM: gmem holds g in fragment order (BEPI_STORE_FRAG)
   int out_frag;          // fp32 output (split-K slices) in fragment order, padded tiles included
-  int M, N, K;
+  int M, K;
+  int N[2];    // output columns per batch entry
   int mtiles, ntiles;
+  // 0: the batch entry is blockIdx.z and both entries have ntiles column
+  // tiles; > 0: the grid's z is 1, entry 0 has the first nt0 of the ntiles
+  // column tiles and entry 1 the rest (entries of different widths).
+  int nt0;
   int k_split;
 };
 
@@ -219,10 +225,17 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   int vb = xcd_remap(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), nblk);
   const int m0 = (vb % p.mtiles) * BM;
   vb /= p.mtiles;
-  const int n0 = (vb % p.ntiles) * BN;
+  int nt = vb % p.ntiles;
   vb /= p.ntiles;
   const int split = vb % gridDim.y;
-  const int zb = vb / gridDim.y;
+  int zb = vb / gridDim.y;
+  if (p.nt0 > 0 && nt >= p.nt0) {
+    zb = 1;
+    nt -= p.nt0;
+  }
+  const int n0 = nt * BN;
+  const int N = p.N[zb];
+  const int64_t ldb = p.ldb[zb], ldo = p.ldo[zb];
   const int kbeg = split * p.k_split;
   const int kend = min(p.K, kbeg + p.k_split);
   const int nk = (kend - kbeg + BK - 1) / BK;
@@ -235,7 +248,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 
   const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
   const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
-  const uint32_t lda2 = (uint32_t)p.lda * 2u, ldb2 = (uint32_t)p.ldb * 2u;
+  const uint32_t lda2 = (uint32_t)p.lda * 2u, ldb2 = (uint32_t)ldb * 2u;
   const uint32_t lbase = lds_addr(lds);
 
   // ---- per-lane DMA geometry (constant along K) ----
@@ -265,7 +278,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 #pragma unroll
     for (int i = 0; i < C::B_UNITS; ++i) {
       const int row = row0 + 16 * NW * i;
-      b_voff[i] = (row < BN && n0 + row < p.N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
+      b_voff[i] = (row < BN && n0 + row < N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
     }
   } else if constexpr (C::FP8_B) {
     // fp8 natural: instruction i fills k-rows 4*(wave + NW*i) + lane/16
@@ -275,7 +288,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     for (int i = 0; i < C::B_UNITS; ++i) {
       const int kk = 4 * (wave + NW * i) + (lane >> 4);
       const int col = 16 * ((lane & 15) ^ (kk & 7));
-      b_voff[i] = (col < BN && n0 + col < p.N) ? (uint32_t)kk * (uint32_t)p.ldb + (uint32_t)(n0 + col) : kOOB;
+      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * (uint32_t)ldb + (uint32_t)(n0 + col) : kOOB;
     }
   } else {
     const int kk = 2 * wave + (lane >> 5);
@@ -283,7 +296,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
 #pragma unroll
     for (int i = 0; i < C::B_UNITS; ++i)
-      b_voff[i] = (col < BN && n0 + col < p.N) ? (uint32_t)(kk + 2 * NW * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)(kk + 2 * NW * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
   }
 
   // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
@@ -294,7 +307,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
     } else {
       const int i = d - C::A_UNITS;
-      const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)p.ldb : (uint32_t)k0 * ldb2);
+      const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)ldb : (uint32_t)k0 * ldb2);
       dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + NW * i) * 1024);
     }
   };
@@ -465,8 +478,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         // them issue before the first store: a load under a branch left a
         // vmcnt(0) per fragment, which also waited for every earlier h store.
         const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
-        const bool in = m < p.M && n < p.N;
-        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (in ? (int64_t)m * p.ldo + n : 0)));
+        const bool in = m < p.M && n < N;
+        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (in ? (int64_t)m * ldo + n : 0)));
         gv[i][j] = in ? g : u32x2{0u, 0u};
       }
     }
@@ -478,17 +491,17 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int n = n0 + wn0 + 16 * j + 4 * lg;
-      if (!FRAG && !ffrag && n >= p.N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+      if (!FRAG && !ffrag && n >= N) continue;  // N % 8 == 0: n < N implies n + 3 < N
       f32x4 v = acc[i][j];
       if constexpr (C::FP8_B)
-        if (n < p.N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
+        if (n < N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
       const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
       if constexpr (FRAG) {
         *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + fo) =
             u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
         continue;
       }
-      const int64_t o = (int64_t)m * p.ldo + n;
+      const int64_t o = (int64_t)m * ldo + n;
       if constexpr (C::EPI == BEPI_ATOMIC) {
         float* op = reinterpret_cast<float*>(outp) + o;
         unsafeAtomicAdd(op + 0, v.x);

@@ -27,6 +27,7 @@ SVDMLP_X_T = 0x8
 SVDMLP_OK = 0
 SVDMLP_EINVAL = -1
 SVDMLP_EHIP = -2
+SVDMLP_EUNSUP = -3
 
 # Every symbol include/svdmlp.h declares.
 EXPORTED = (
@@ -40,6 +41,8 @@ EXPORTED = (
     "svdmlp_svd_mlp_block",
     "svdmlp_svd_mlp_ld",
     "svdmlp_svd_mlp_block_ld",
+    "svdmlp_svd_mlp_ranks",
+    "svdmlp_svd_mlp_block_ranks",
     "svdmlp_svd_mlp_noalloc",
     "svdmlp_profile_enable",
     "svdmlp_profile_read",
@@ -87,6 +90,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.svdmlp_svd_mlp_block_ld.restype = ctypes.c_int
     lib.svdmlp_svd_mlp_block_ld.argtypes = ([_vp, _vp, ctypes.c_float] + [_vp] * 6 + [_vp, _vp, _vp] + [_i64] * 5
                                             + [_i32, _i32, _u32, _vp, _sz, _vp])
+    lib.svdmlp_svd_mlp_ranks.restype = ctypes.c_int
+    lib.svdmlp_svd_mlp_ranks.argtypes = [_vp] * 7 + [_vp, _vp, _vp] + [_i64] * 6 + [_i32, _i32, _u32, _vp, _sz, _vp]
+    lib.svdmlp_svd_mlp_block_ranks.restype = ctypes.c_int
+    lib.svdmlp_svd_mlp_block_ranks.argtypes = ([_vp, _vp, ctypes.c_float] + [_vp] * 6 + [_vp, _vp, _vp]
+                                               + [_i64] * 6 + [_i32, _i32, _u32, _vp, _sz, _vp])
     lib.svdmlp_svd_mlp_noalloc.restype = ctypes.c_int
     lib.svdmlp_svd_mlp_noalloc.argtypes = [_vp] * 7 + [_vp, _vp, _vp] + [_i64] * 5 + [_i32, _i32, _u32, _vp]
     lib.svdmlp_profile_enable.restype = ctypes.c_int

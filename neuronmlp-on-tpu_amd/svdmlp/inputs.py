@@ -73,21 +73,6 @@ def make_layer(shape: LayerShape, T: int, seed: int = 0):
     return make_x(rng, T, shape.d), factors
 
 
-def stack_ranks(num_layers: int, seed: int = 0, choices=(2048, 2304, 2560, 2816, 3072)):
-    """per-layer (r_gate_up, r_down) drawn seeded from the
-    rank set, independently per branch.  Gate and up share a rank because
-    the fused kernel requires matching gate/up shapes (test_speedup.py:532)."""
-    rng = np.random.default_rng(seed)
-    picks = rng.choice(np.asarray(choices), size=(num_layers, 2))
-    return [(int(a), int(b)) for a, b in picks]
-
-
-def stack_gains(num_layers: int, d: int, seed: int = 0) -> np.ndarray:
-    """RMSNorm gains ~ U(0.9, 1.1), float32, shape (num_layers, d)."""
-    rng = np.random.default_rng(seed + 1)
-    return rng.uniform(0.9, 1.1, size=(num_layers, d)).astype(np.float32)
-
-
 def to_torch(a: np.ndarray, dtype: torch.dtype, device="cuda") -> torch.Tensor:
     """float32 numpy -> torch tensor of ``dtype`` (RNE for bfloat16)."""
     t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32))

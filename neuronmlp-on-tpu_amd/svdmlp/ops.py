@@ -321,7 +321,7 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
     key = _plan_key(x, factors)
     plan = _PLANS.get(key) if key is not None else None
     if plan is not None:
-        ptrs, flags, w_code, ld_arr, (d, ff, r_gu, r_d), dev = plan
+        ptrs, flags, w_code, ld_arr, (d, ff, r_g, r_u, r_d), dev = plan
         T = int(x.shape[0])
         x = _activation(x)
         if out is None:
@@ -329,15 +329,17 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
         elif out.shape != (T, d) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
             raise ValueError("out must be a contiguous (T, d) tensor of x.dtype on x.device")
         if workspace is None:
-            workspace = _shared_workspace(dev, T, d, ff, max(r_gu, r_d), w_code)
-        return x, ptrs, None, flags, w_code, None, ld_arr, out, workspace, (T, d, ff, r_gu, r_d), dev
+            workspace = _shared_workspace(dev, T, d, ff, max(r_g, r_u, r_d), w_code)
+        return x, ptrs, None, flags, w_code, None, ld_arr, out, workspace, (T, d, ff, r_g, r_u, r_d), dev
     validate_arrays(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
     T, d = _shape(x)
-    if u_gate.shape[0] != d or v_gate.shape[0] != u_gate.shape[1]:
+    if u_gate.shape[0] != d or v_gate.shape[0] != u_gate.shape[1] or v_up.shape[0] != u_up.shape[1]:
         raise ValueError("X, U, V contraction dimensions do not match")
-    if _shape(u_up) != _shape(u_gate) or _shape(v_up) != _shape(v_gate):
+    # the gate and up ranks may differ (kernels/reference.py:54-72 allows it)
+    if u_up.shape[0] != u_gate.shape[0] or v_up.shape[1] != v_gate.shape[1]:
         raise ValueError("gate/up factors must have matching shapes")
-    r_gu, ff = _shape(v_gate)
+    r_g, ff = _shape(v_gate)
+    r_u = int(v_up.shape[0])
     if u_down.shape[0] != ff or v_down.shape[0] != u_down.shape[1] or v_down.shape[1] != d:
         raise ValueError("X, U, V contraction dimensions do not match")
     r_d = int(u_down.shape[1])
@@ -349,14 +351,16 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
     _uniform(vs, all(f.linear for f in vs))
     flags = _layout_flags(us, vs)
     w_code = _w_code(x, (u_gate,))
-    # padded rows: bf16 natural layout only, one pitch for gate and up
+    # padded rows: bf16 natural layout only, one pitch for gate and up when
+    # their ranks are equal (the decode kernels read both with one pitch)
     if x.dtype != torch.bfloat16 or w_code == _lib.SVDMLP_FP8_E4M3 or flags:
         for f in fs:
             f.dense()
-    for a, b in ((fs[0], fs[2]), (fs[1], fs[3])):
-        if a.ld != b.ld:
-            a.dense()
-            b.dense()
+    if r_g == r_u:
+        for a, b in ((fs[0], fs[2]), (fs[1], fs[3])):
+            if a.ld != b.ld:
+                a.dense()
+                b.dense()
     ld_arr = (ctypes.c_int64 * 6)(*[f.ld for f in fs]) if any(f.ld for f in fs) else None
     scale_arr = None
     if w_code == _lib.SVDMLP_FP8_E4M3:
@@ -366,13 +370,13 @@ def _prepare_layer(x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out
     elif out.shape != (T, d) or out.dtype != x.dtype or not out.is_contiguous() or out.device != dev:
         raise ValueError("out must be a contiguous (T, d) tensor of x.dtype on x.device")
     if workspace is None:
-        workspace = _shared_workspace(dev, T, d, ff, max(r_gu, r_d), w_code)
-    dims = (T, d, ff, r_gu, r_d)
+        workspace = _shared_workspace(dev, T, d, ff, max(r_g, r_u, r_d), w_code)
+    dims = (T, d, ff, r_g, r_u, r_d)
     ptrs = tuple(f.ptr for f in fs)
     if key is not None and scale_arr is None and all(p == f.data_ptr() for p, f in zip(ptrs, factors)):
         if len(_PLANS) > 64:
             _PLANS.clear()
-        _PLANS[key] = (ptrs, flags, w_code, ld_arr, (d, ff, r_gu, r_d), dev)
+        _PLANS[key] = (ptrs, flags, w_code, ld_arr, (d, ff, r_g, r_u, r_d), dev)
     return x, ptrs, fs, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev
 
 
@@ -384,22 +388,55 @@ def _on_device(dev, call):
         return call()
 
 
+def pad_rank(u, v, r: int):
+    """U (d_in, r0) and V (r0, d_out) zero-padded to rank r: r - r0 more U
+    columns and V rows of zeros, which add exactly nothing to U . V.  fp8
+    factors pad their data with zeros (and the U scales with ones)."""
+    r0 = int(u.shape[1])
+    if r0 == r:
+        return u, v
+    if isinstance(u, QuantizedFactor):
+        ud = torch.zeros((u.shape[0], r), dtype=u.data.dtype, device=u.device)
+        ud[:, :r0] = u.data
+        us = torch.ones(r, dtype=torch.float32, device=u.device)
+        us[:r0] = u.scale
+        vd = torch.zeros((r, v.shape[1]), dtype=v.data.dtype, device=v.device)
+        vd[:r0] = v.data
+        return QuantizedFactor(ud, us), QuantizedFactor(vd, v.scale)
+    up = torch.zeros((u.shape[0], r), dtype=u.dtype, device=u.device)
+    vp = torch.zeros((r, v.shape[1]), dtype=v.dtype, device=v.device)
+    up[:, :r0] = u
+    vp[:r0] = v
+    return up, vp
+
+
+def _pad_branches(u_gate, v_gate, u_up, v_up):
+    r = max(int(u_gate.shape[1]), int(u_up.shape[1]))
+    return (*pad_rank(u_gate, v_gate, r), *pad_rank(u_up, v_up, r))
+
+
 def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
             out: torch.Tensor | None = None) -> torch.Tensor:
     """Full SVD SwiGLU block, fused_xuv(fused_gate_up(x)) with h rounded to
-    x.dtype in between (kernels/reference.py:85-93).  Gate/up rank and down
-    rank may differ.  ``workspace``/``out`` may be supplied to avoid
-    per-call allocation (see :func:`svd_mlp_workspace`)."""
+    x.dtype in between (kernels/reference.py:85-93).  The gate, up and down
+    ranks may all differ: the large-tile path (more than 128 tokens) runs
+    each branch at its own rank; other shapes zero-pad the smaller of the
+    gate and up branches, which does not change the result.
+    ``workspace``/``out`` may be supplied to avoid per-call allocation (see
+    :func:`svd_mlp_workspace`, with r the largest rank)."""
     lib = _lib.load()
     x, ptrs, holders, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
         x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
-    _on_device(dev, lambda: _lib.check(lib.svdmlp_svd_mlp_ld(
+    rc = _on_device(dev, lambda: lib.svdmlp_svd_mlp_ranks(
         x.data_ptr(), *ptrs,
         ctypes.addressof(scale_arr) if scale_arr is not None else None,
         ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
         *dims, _ACT_CODES[x.dtype], w_code, flags,
-        workspace.data_ptr(), workspace.numel(), _stream(dev))))
+        workspace.data_ptr(), workspace.numel(), _stream(dev)))
     del holders
+    if rc == _lib.SVDMLP_EUNSUP:
+        return svd_mlp(x, *_pad_branches(u_gate, v_gate, u_up, v_up), u_down, v_down, workspace=workspace, out=out)
+    _lib.check(rc)
     return out
 
 
@@ -421,13 +458,17 @@ def svd_mlp_block(x, norm_weight, u_gate, v_gate, u_up, v_up, u_down, v_down, *,
     eps = float(eps)
     if not eps > 0:
         raise ValueError(f"eps must be positive, got {eps}")
-    _on_device(dev, lambda: _lib.check(lib.svdmlp_svd_mlp_block_ld(
+    rc = _on_device(dev, lambda: lib.svdmlp_svd_mlp_block_ranks(
         x.data_ptr(), gain.data_ptr(), eps, *ptrs,
         ctypes.addressof(scale_arr) if scale_arr is not None else None,
         ctypes.addressof(ld_arr) if ld_arr is not None else None, out.data_ptr(),
         *dims, _ACT_CODES[x.dtype], w_code, flags,
-        workspace.data_ptr(), workspace.numel(), _stream(dev))))
+        workspace.data_ptr(), workspace.numel(), _stream(dev)))
     del holders, gain
+    if rc == _lib.SVDMLP_EUNSUP:
+        return svd_mlp_block(x, norm_weight, *_pad_branches(u_gate, v_gate, u_up, v_up), u_down, v_down, eps=eps,
+                             workspace=workspace, out=out)
+    _lib.check(rc)
     return out
 
 

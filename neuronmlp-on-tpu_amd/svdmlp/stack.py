@@ -3,12 +3,10 @@ the model loop of bench/e2e_block.py:264-278 / 343-355 with LlamaRMSNorm
 (models/modeling_llama.py:245-262), on libsvdmlp.
 
 Non-uniform compression draws each layer's gate, up and down ranks
-independently from ``RANK_CHOICES`` with a seeded generator.  The library's
-fused gate/up takes one rank for both branches (as the reference's fused
-kernel, test_speedup.py:532-533), so when the gate and up ranks of a layer
-differ both branches are zero-padded to the larger one: extra U columns and V
-rows of zeros, which add exactly nothing to the result.  FLOP counts use the
-drawn (unpadded) ranks.
+independently from ``RANK_CHOICES`` with a seeded generator.  Each branch
+runs at its own rank (the library's two-rank entry points; the reference's
+TPU launcher takes one rank for gate and up, test_speedup.py:532-533, so it
+would zero-pad the smaller branch).
 """
 
 from __future__ import annotations
@@ -27,7 +25,7 @@ RANK_CHOICES = (2048, 2304, 2560, 2816, 3072)
 @dataclass
 class StackLayer:
     gain: torch.Tensor   # (d,) float32 RMSNorm gain
-    factors: tuple       # (ug, vg, uu, vu, ud, vd), gate/up padded to a common rank
+    factors: tuple       # (ug, vg, uu, vu, ud, vd) at the drawn ranks
     ranks: tuple         # drawn (r_gate, r_up, r_down)
 
 
@@ -36,18 +34,6 @@ def draw_ranks(n_layers: int, seed: int, choices=RANK_CHOICES) -> list[tuple[int
     rng = np.random.default_rng(seed)
     picks = rng.choice(np.asarray(choices), size=(n_layers, 3))
     return [tuple(int(v) for v in row) for row in picks]
-
-
-def pad_rank(u: torch.Tensor, v: torch.Tensor, r: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Zero-pad U (d_in, r0) to r columns and V (r0, d_out) to r rows."""
-    r0 = u.shape[1]
-    if r0 == r:
-        return u, v
-    up = torch.zeros((u.shape[0], r), dtype=u.dtype, device=u.device)
-    vp = torch.zeros((r, v.shape[1]), dtype=v.dtype, device=v.device)
-    up[:, :r0] = u
-    vp[:r0] = v
-    return up, vp
 
 
 def make_stack(n_layers: int, d: int, ff: int, *, seed: int, device, dtype=torch.bfloat16,
@@ -67,9 +53,6 @@ def make_stack(n_layers: int, d: int, ff: int, *, seed: int, device, dtype=torch
         ug, vg = rnd(d, rg), rnd(rg, ff)
         uu, vu = rnd(d, ru), rnd(ru, ff)
         ud, vd = rnd(ff, rd), rnd(rd, d)
-        r = max(rg, ru)
-        ug, vg = pad_rank(ug, vg, r)
-        uu, vu = pad_rank(uu, vu, r)
         gain = torch.rand(d, generator=g, device=device, dtype=torch.float32) * 0.2 + 0.9
         layers.append(StackLayer(gain, (ug, vg, uu, vu, ud, vd), (rg, ru, rd)))
     return layers
@@ -85,7 +68,7 @@ def stack_flops(T: int, d: int, ff: int, layers) -> float:
 def stack_workspace(x: torch.Tensor, layers) -> torch.Tensor:
     """One workspace for every layer of the stack (sized for the largest rank)."""
     ff = layers[0].factors[1].shape[1]
-    r = max(max(l.factors[0].shape[1], l.factors[4].shape[1]) for l in layers)
+    r = max(max(l.ranks) for l in layers)
     return ops.svd_mlp_workspace(x, r=r, ff=ff)
 
 

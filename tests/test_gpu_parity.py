@@ -497,8 +497,9 @@ def test_mlp_block_fp32_and_odd_widths(gpu, dtype, d):
 
 
 def test_mlp_stack_nonuniform_ranks(gpu):
-    """Three blocks with independently drawn gate/up/down ranks (gate and up
-    zero-padded to a common rank) against the oracle, layer after layer."""
+    """Three blocks with independently drawn gate/up/down ranks against the
+    oracle, layer after layer (T=96: decode shapes, where the host mirror
+    zero-pads the smaller of the gate and up branches)."""
     from svdmlp import stack
 
     d, ff, T = 1024, 2048, 96
@@ -513,6 +514,96 @@ def test_mlp_stack_nonuniform_ranks(gpu):
     x0 = x.float().cpu().numpy()
     assert _rel(y, ref) < BF16_TOL
     assert _rel(y - x0, ref - x0) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------
+# distinct gate and up ranks (svdmlp_svd_mlp_ranks)
+# ---------------------------------------------------------------------------
+
+def _two_rank_layer(d, ff, r_g, r_u, r_d, T, seed):
+    """bf16-valued x and factors with a gate rank and an up rank of their own."""
+    rng = np.random.default_rng(seed)
+    f = [inputs.random_matrix(rng, a, b) for a, b in ((d, r_g), (r_g, ff), (d, r_u), (r_u, ff), (ff, r_d), (r_d, d))]
+    return _rounded((inputs.make_x(rng, T, d), *f), torch.bfloat16)
+
+
+# T=8 and 96: decode shapes, where the host mirror zero-pads the smaller
+# branch; T=200: split gate/up XU.V passes (one row tile, K split in two per
+# branch); T=300: fragment-order g pass + SwiGLU pass at each branch's rank;
+# T=1024: split-K X.U with both branches' column tiles in one launch; ranks
+# that are no multiple of the 256-wide tile leave ragged last tiles per branch.
+@pytest.mark.parametrize("T,ranks", [(8, (512, 256, 384)), (96, (384, 640, 256)), (200, (512, 256, 384)),
+                                     (300, (256, 512, 384)), (1024, (384, 640, 512))])
+def test_distinct_gate_up_ranks(gpu, T, ranks):
+    r_g, r_u, r_d = ranks
+    d, ff = 1024, 2048
+    xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 900 + T)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
+    got = _np(ops.svd_mlp(*t))
+    err = _rel(got, ref)
+    print(f"two ranks T={T} r_g={r_g} r_u={r_u} r_d={r_d} rel_l2={err:.3e}")
+    assert err < BF16_TOL
+    # the same layer with the smaller branch zero-padded to one rank
+    padded = _np(ops.svd_mlp(t[0], *ops._pad_branches(*t[1:5]), *t[5:]))
+    assert _rel(got, padded) < 5e-3
+
+
+def test_distinct_gate_up_ranks_fp8(gpu):
+    T, d, ff, r_g, r_u, r_d = 300, 1024, 2048, 512, 256, 384
+    xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 950)
+    q = [fp8.quantize_per_channel(torch.from_numpy(a)) for a in fb]
+    deq = [O.e4m3_decode(qq.data.view(torch.uint8).numpy()) * qq.scale.numpy() for qq in q]
+    qg = [ops.QuantizedFactor(qq.data.to(gpu), qq.scale.to(gpu)) for qq in q]
+    got = _np(ops.svd_mlp(_to(xb, torch.bfloat16, gpu), *qg))
+    assert _rel(got, O.svd_mlp_ref(xb, *deq, dtype="bfloat16")) < FP8_TOL
+    # fp8 at a decode shape: zero-padded fp8 branches (zero data, unit scales)
+    xs = xb[:8]
+    got = _np(ops.svd_mlp(_to(xs, torch.bfloat16, gpu), *qg))
+    assert _rel(got, O.svd_mlp_ref(xs, *deq, dtype="bfloat16")) < FP8_TOL
+
+
+def test_distinct_gate_up_ranks_block_and_row_pitches(gpu):
+    """The block with two ranks, and gate / up factors with padded rows of
+    different pitches (each branch read with its own on the large-tile path)."""
+    T, d, ff, r_g, r_u, r_d = 300, 1024, 2048, 384, 256, 512
+    xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 960)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    gain = np.random.default_rng(4).uniform(0.9, 1.1, size=d).astype(np.float32)
+    g = torch.from_numpy(gain).to(gpu)
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    y = _np(ops.svd_mlp_block(t[0], g, *t[1:], eps=1e-5))
+    assert _rel(y, ref) < BF16_TOL and _rel(y - xb, ref - xb) < BF16_TOL
+    padded = [ops.pad_rows(a, p) for a, p in zip(t[1:], (8, 64, 72, 128, 24, 40))]
+    assert all(ops.padded_rows(a) for a in padded)
+    y = _np(ops.svd_mlp_block(t[0], g, *padded, eps=1e-5))
+    assert _rel(y, ref) < BF16_TOL and _rel(y - xb, ref - xb) < BF16_TOL
+
+
+def test_distinct_gate_up_ranks_abi(gpu):
+    """svdmlp_svd_mlp_ranks runs two ranks on the large-tile path and returns
+    SVDMLP_EUNSUP, with a message, where only one rank is taken."""
+    import ctypes
+
+    from svdmlp import _lib
+
+    lib = _lib.load()
+    d, ff, r_g, r_u, r_d = 1024, 2048, 512, 256, 384
+    ws = None
+    for T, want in ((8, _lib.SVDMLP_EUNSUP), (300, _lib.SVDMLP_OK)):
+        xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 970)
+        t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+        y = torch.zeros((T, d), dtype=torch.bfloat16, device=gpu)
+        ws = ops.svd_mlp_workspace(t[0], r=max(r_g, r_u, r_d), ff=ff)
+        bf = _lib.SVDMLP_BF16
+        rc = lib.svdmlp_svd_mlp_ranks(t[0].data_ptr(), *(a.data_ptr() for a in t[1:]), None, None, y.data_ptr(),
+                                      T, d, ff, r_g, r_u, r_d, bf, bf, 0, ws.data_ptr(), ws.numel(),
+                                      torch.cuda.current_stream(gpu).cuda_stream)
+        assert rc == want
+        if want == _lib.SVDMLP_EUNSUP:
+            assert "large-tile path only" in lib.svdmlp_last_error().decode()
+        else:
+            assert _rel(_np(y), O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
 
 
 # ---------------------------------------------------------------------------

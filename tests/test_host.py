@@ -158,14 +158,6 @@ def test_generator_order_and_scale():
     assert abs(big[1].std() - 1 / np.sqrt(512)) < 1e-3  # N(0, 1/r)
 
 
-def test_stack_ranks_are_seeded_and_in_set():
-    a = inputs.stack_ranks(32, seed=3)
-    assert a == inputs.stack_ranks(32, seed=3)
-    assert len(a) == 32 and all(r in (2048, 2304, 2560, 2816, 3072) for pair in a for r in pair)
-    g = inputs.stack_gains(4, 128)
-    assert g.shape == (4, 128) and g.min() >= 0.9 and g.max() <= 1.1
-
-
 def test_quantizer_matches_oracle_codec():
     from svdmlp import fp8
 
@@ -196,12 +188,12 @@ def test_stack_rank_padding_is_exact():
     the oracle's float64-free fp32 math on CPU tensors)."""
     import torch
 
-    from svdmlp import stack
+    from svdmlp import ops
 
     g = torch.Generator().manual_seed(0)
     x = torch.randn(5, 16, generator=g)
     u, v = torch.randn(16, 6, generator=g), torch.randn(6, 12, generator=g)
-    up, vp = stack.pad_rank(u, v, 10)
+    up, vp = ops.pad_rank(u, v, 10)
     assert up.shape == (16, 10) and vp.shape == (10, 12)
     assert torch.equal(up[:, 6:], torch.zeros(16, 4)) and torch.equal(vp[6:], torch.zeros(4, 12))
     np.testing.assert_allclose(O.fused_xuv_ref(x.numpy(), up.numpy(), vp.numpy()),
