@@ -52,7 +52,7 @@ def _args(argv=None):
     p.add_argument("--tokens", type=int, default=1024)
     p.add_argument("--layers", type=int, default=4, help="synthetic layers the steps rotate over")
     p.add_argument("--decode-steps", type=int, default=200)
-    p.add_argument("--decode-tokens", type=int, nargs="*", default=[1, 8, 32, 64])
+    p.add_argument("--decode-tokens", type=int, nargs="*", default=[1, 2, 8, 32, 64])
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=("prefill", "decode", "stack", "fp8"), default=None,
@@ -210,9 +210,12 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
             _time_steps(torch, dstep, min(args.decode_steps, 50), 0, stream)
         nbytes = factor_bytes + 2 * Td * D * 2
         gbs = nbytes / (msd * 1e-3) / 1e9
-        # measured HBM bytes of the MFMA decode layer's launch (16-row token tiles: 1, 2, 4 or 8 of them)
+        # measured HBM bytes of the decode layer's launch: the contracted layer at
+        # 1-3 tokens (its slices grow with T), else the MFMA layer by 16-row token tiles
         mt = 1 if Td <= 16 else (2 if Td <= 32 else (4 if Td <= 64 else 8))
-        traffic = (_profiled_traffic(f"decode_layer_mt{mt}", DECODE_TRAFFIC_PROFILE)
+        kernel = "decode_layer_contracted" if "decode_layer_contracted" in prof.result else "decode_layer"
+        key = f"decode_layer_contracted_T{Td}" if kernel == "decode_layer_contracted" else f"decode_layer_mt{mt}"
+        traffic = (_profiled_traffic(key, DECODE_TRAFFIC_PROFILE)
                    if args.weights_layout == TRAFFIC_LAYOUT and Td <= 128 else None)
         dec[f"T={Td}"] = {
             "us_per_layer": round(msd * 1e3, 2),
@@ -222,6 +225,7 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
             "traffic_GB/s": round(traffic / (msd * 1e-3) / 1e9, 1) if traffic else None,
             "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),
             "stages_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.result.items()},
+            "kernel": kernel,
         }
         if svdmlp.workspace_status(wsd):
             raise RuntimeError(f"decode T={Td}: a grid-barrier wait gave up (the device was shared?)")

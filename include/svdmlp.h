@@ -57,6 +57,16 @@ extern "C" {
 #define SVDMLP_V_LINEAR 0x2u /* V stored (d_out, r) instead of (r, d_out) */
 #define SVDMLP_OUT_T 0x4u    /* gate_up: write h transposed, (ff, T) */
 #define SVDMLP_X_T 0x8u      /* xuv: input given transposed, (d_in, T) */
+/* svd_mlp entry points: the contracted layer (models/modeling_llama.py:865-886,
+ * _contracted_mlp: Gate/Up/SwiGLU fused through Down-U, so that h never leaves
+ * the kernel and only (T, r_d) partials of XU_d cross blocks).  Taken by the
+ * persistent decode layer at 1-4 tokens (bf16, natural layout, ff a multiple
+ * of 64, gate/up rank >= 320, a block for each 64-column strip of h and each
+ * 128-column tile of XU_d: ff/64 + r_d/128 <= CU count); other shapes run as
+ * without the flag (same result: at prefill a (rows x r_d) partial per h
+ * strip would move far more bytes than h itself).  Without the flag it is
+ * taken at 1-3 tokens, where it is the fastest layer. */
+#define SVDMLP_CONTRACT 0x10u
 
 /* status codes */
 #define SVDMLP_OK 0

@@ -87,12 +87,13 @@ enum Stage : int {
   ST_GU_XUV_G,
   ST_DEC_LAYER,
   ST_DEC_GEMV,
+  ST_DEC_CONTRACT,
   ST_COUNT
 };
 const char* const kStageNames[ST_COUNT] = {
     "zero_fill",        "gate_up_xu",       "gate_up_xuv_swiglu", "down_xu",           "down_xuv",
     "decode_gate_up_xu", "decode_gate_up_xuv", "decode_down_xu",   "decode_down_xuv", "finalize",
-    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer"};
+    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer",  "decode_layer_contracted"};
 
 struct Profiler {
   std::mutex mu;
@@ -151,6 +152,16 @@ struct StageScope {
 
 size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
 
+// Token counts the contracted decode layer (SVDMLP_CONTRACT) takes: its
+// partial XU_d slices grow with T (8B layer: 2.5 MB per token).  Up to
+// kDlContractAutoT tokens it is the default wherever it runs (8B layer,
+// padded V rows: T=1 74.5 -> 71.0 us, T=2 74.5 -> 72.5, T=3 74.5 -> 74.0,
+// T=4 74.6 -> 75.2; dense factors, against the streaming-GEMV layer at
+// T <= 2 and the three-barrier layer at 3: 77.6 -> 74.5, 80.7 -> 77.0,
+// 81.8 -> 77.4).
+constexpr int64_t kDlContractMaxT = 4;
+constexpr int64_t kDlContractAutoT = 3;
+
 struct Ws {
   size_t sync;     // 4 KB of grid-barrier words (zero before first use)
   size_t xu_bf16;  // [2][T][r] bf16 (gate, up) rank-r intermediate
@@ -162,6 +173,9 @@ struct Ws {
   size_t norm;     // [T][d] RMSNorm output of the MLP block (4 bytes/elem worst case)
   size_t g;        // bf16 gate values of the large-tile g pass, fragment order over padded tiles
   size_t slices;   // split-K partial sums of the MFMA decode layer (decode only)
+  size_t need;     // bytes every call needs (the regions above)
+  size_t cslices;  // partial XU_d tiles of the contracted decode layer (T <= kDlContractMaxT), last: a
+                   // workspace without them runs the other decode layers
   size_t total;
 };
 
@@ -235,6 +249,12 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   off += dec ? 0 : a256(((T + 255) / 256 * 256) * std::max((big + 223) / 224 * 224, (big + 255) / 256 * 256) * 2);
   w.slices = off;
   off += T <= kDlMaxT ? a256((int64_t)kDlMaxGrid * decode_layer_mt((int)T) * 2048 * 4) : 0;
+  w.need = off;
+  // the contracted layer's slices: one per (XU_d tile, h strip), T rows each
+  w.cslices = off;
+  off += (T <= kDlContractMaxT && ff % 64 == 0 && ff / 64 + r / 128 <= kDlMaxGrid)
+             ? a256(dl_contract_bytes(r / 128, ff / 64, T))
+             : 0;
   w.total = off;
   return w;
 }
@@ -382,6 +402,7 @@ struct Tune {
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
   int nw = 8;          // waves per block of the fn-8 X.U and XU.V stages (8, or 4: faster in isolation, not in the layer)
+  bool contract = true; // contracted decode layer by default at T <= kDlContractAutoT
 };
 
 const Tune& tune() {
@@ -405,6 +426,7 @@ const Tune& tune() {
         if (k == "split") r.split = v;
         if (k == "big") r.big = v != 0;
         if (k == "dlayer") r.dlayer = v != 0;
+        if (k == "contract") r.contract = v != 0;
         if (k == "gusplit") r.gusplit = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
@@ -798,11 +820,20 @@ int dl_plan(int64_t K, int64_t tiles, int grid, int* units) {
   return (int)ks;
 }
 
+// The contracted instance takes the layer when asked for (SVDMLP_CONTRACT) at
+// T <= kDlContractMaxT with a block for every h strip and XU_d tile.
+bool decode_contract_ok(int64_t T, int64_t ff, int64_t r_gu, int64_t r_d, const Ws& L, size_t ws_bytes) {
+  // the gate/up run-out prefetches the down half's first 5 ring stages of 64 k
+  if (T > kDlContractMaxT || L.total == L.cslices || ws_bytes < L.total || r_gu < 320) return false;
+  const int grid = decode_layer_contract_grid();
+  return grid > 0 && ff / 64 + r_d / 128 <= grid;
+}
+
 int decode_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
                  const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
-                 char* ws, const Ws& L, const FactorLd& ld) {
+                 char* ws, const Ws& L, const FactorLd& ld, bool contract = false) {
   const int mt = decode_layer_mt((int)T);
-  const int grid = decode_layer_grid(mt);
+  const int grid = contract ? decode_layer_contract_grid() : decode_layer_grid(mt);
   DecLayerParams p{};
   p.x = x;
   p.ug = ug;
@@ -816,6 +847,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.xd16 = reinterpret_cast<uint16_t*>(ws + L.gu32);
   p.h = reinterpret_cast<uint16_t*>(ws + L.h);
   p.slices = reinterpret_cast<float*>(ws + L.slices);
+  p.cslices = contract ? reinterpret_cast<float*>(ws + L.cslices) : nullptr;
   p.sync = reinterpret_cast<uint64_t*>(ws + L.sync);
   p.T = (int)T;
   p.d = (int)d;
@@ -834,8 +866,8 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.ld_ud = (int)ld.ud;
   p.ld_vd = (int)ld.vd;
   const char* why = nullptr;
-  StageScope ss(ST_DEC_LAYER, c.st);
-  return check(launch_decode_layer(p, mt, grid, c.st, &why), "decode layer", why);
+  StageScope ss(contract ? ST_DEC_CONTRACT : ST_DEC_LAYER, c.st);
+  return check(launch_decode_layer(p, mt, grid, c.st, &why, contract), "decode layer", why);
 }
 
 // Streaming-GEMV layer (1 <= T <= min(kGvMaxT, gvmax)): bf16, natural
@@ -947,7 +979,7 @@ int svdmlp_svd_mlp_noalloc(const void* x, const void* ug, const void* vg, const 
   g_err.clear();
   int rc = validate_dims(T, d, ff, std::min(r_gu, r_d));
   if (rc) return rc;
-  const size_t need = ws_layout(T, d, ff, std::max(r_gu, r_d)).total;
+  const size_t need = ws_layout(T, d, ff, std::max(r_gu, r_d)).need;
   if (need > kScratchBytes)
     return fail("svdmlp_svd_mlp_noalloc: this shape needs %zu bytes of workspace, more than the fixed scratch of "
                 "%zu bytes (T=%lld, d=%lld, ff=%lld, r=%lld); use svdmlp_svd_mlp_ld with a workspace",
@@ -997,7 +1029,7 @@ int svdmlp_svd_mlp_block_ranks(const void* x, const float* norm_w, float eps, co
   if (!(eps > 0.0f)) return fail("eps must be positive, got %g", (double)eps);
   const int64_t r = std::max(std::max(r_g, r_u), r_d);
   const Ws L = ws_layout(T, d, ff, r);
-  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
   const bool bf16 = act_dtype == SVDMLP_BF16;
   hipStream_t st = (hipStream_t)stream;
   void* h = static_cast<char*>(workspace) + L.norm;
@@ -1080,7 +1112,7 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
   if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_OUT_T)) return fail("unsupported flags 0x%x", flags);
   if (fp8 && (flags & (SVDMLP_U_LINEAR | SVDMLP_V_LINEAR))) return fail("fp8 weights must use the natural layout");
   const Ws L = ws_layout(T, d, ff, r);
-  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
   const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
   const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR, out_t = flags & SVDMLP_OUT_T;
   bool vec = d % 8 == 0 && ff % 8 == 0 && r % 8 == 0 && (!out_t || T % 8 == 0);
@@ -1152,7 +1184,7 @@ int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, co
   if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_X_T)) return fail("unsupported flags 0x%x", flags);
   if (fp8 && (flags & (SVDMLP_U_LINEAR | SVDMLP_V_LINEAR))) return fail("fp8 weights must use the natural layout");
   const Ws L = ws_layout(T, din, dout, r);
-  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
   const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
   const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR, x_t = flags & SVDMLP_X_T;
   bool vec = din % 8 == 0 && dout % 8 == 0 && r % 8 == 0 && (!x_t || T % 8 == 0);
@@ -1239,14 +1271,16 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
     for (int i = 0; i < 6; ++i)
       if (!scales[i]) return fail("fp8 weights need per-column scales");
   }
-  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR)) return fail("unsupported flags 0x%x", flags);
+  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_CONTRACT)) return fail("unsupported flags 0x%x", flags);
+  const bool contract = (flags & SVDMLP_CONTRACT) || (T <= kDlContractAutoT && tune().contract);
+  flags &= ~SVDMLP_CONTRACT;
   if (fp8 && flags) return fail("fp8 weights must use the natural layout");
   // one rank for both branches below; two ranks only on the large-tile path
   const bool two = r_g != r_u;
   const int64_t r_gu = r_g;
   const int64_t r = std::max(std::max(r_g, r_u), r_d);
   const Ws L = ws_layout(T, d, ff, r);
-  if (ws_bytes < L.total) return fail("workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+  if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
   const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
   const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR;
   bool vec = d % 8 == 0 && ff % 8 == 0 && r_g % 8 == 0 && r_u % 8 == 0 && r_d % 8 == 0;
@@ -1316,7 +1350,12 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
   // With padded V rows the MFMA decode layer is the faster one at every T
   // (8B layer at T=1: 75.5 us against 78 us): the streaming-GEMV layer reads
   // whole 1 KB row pieces, which the padding does not spread over channels.
+  // The contracted instance first wherever it applies (asked for, or at
+  // T <= kDlContractAutoT), then the streaming-GEMV layer, then the
+  // three-barrier MFMA layer.
   const bool mfma_layer = decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld);
+  if (mfma_layer && contract && decode_contract_ok(T, ff, r_gu, r_d, L, ws_bytes))
+    return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld, true);
   if (!(mfma_layer && !ld.dense) && gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld))
     return gemv_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld);
   if (mfma_layer)

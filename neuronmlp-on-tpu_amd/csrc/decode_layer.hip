@@ -15,17 +15,17 @@ namespace svdmlp {
 
 namespace {
 
-template <int MT>
+template <int MT, bool CONTRACT = false>
 hipError_t coop(const DecLayerParams& p, int grid, hipStream_t st) {
-  hipLaunchKernelGGL(decode_layer_kernel<MT>, dim3(grid), dim3(kDlThreads), 0, st, p);
+  hipLaunchKernelGGL((decode_layer_kernel<MT, CONTRACT>), dim3(grid), dim3(kDlThreads), 0, st, p);
   return hipGetLastError();
 }
 
-template <int MT>
+template <int MT, bool CONTRACT = false>
 int blocks_per_cu() {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&decode_layer_kernel<MT>),
-                                                   kDlThreads, 0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, reinterpret_cast<const void*>(&decode_layer_kernel<MT, CONTRACT>), kDlThreads, 0) != hipSuccess)
     return 0;
   return n;
 }
@@ -43,13 +43,31 @@ int decode_layer_grid(int mt) {
   return per >= 1 ? std::min(cus, kDlMaxGrid) : 0;
 }
 
-hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why) {
+int decode_layer_contract_grid() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return blocks_per_cu<1, true>() >= 1 ? std::min(cus, kDlMaxGrid) : 0;
+}
+
+hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why,
+                               bool contract) {
   if (grid <= 0) {
     *why = "decode layer: the kernel cannot be resident on this device";
     return hipErrorInvalidValue;
   }
   hipError_t e;
-  if (mt == 1)
+  if (contract) {
+    // one unit per h strip plus one combining block per XU_d tile
+    // ... and a gate/up rank of at least NS - 1 ring stages, whose run-out
+    // brings in the down half's first stages
+    if (mt != 1 || p.units2 + p.r_d / 128 > grid || !p.cslices ||
+        p.r_gu < 32 * DlDepth<1>::KC * (DlDepth<1>::NS - 1)) {
+      *why = "contracted decode layer: one 16-row tile, a block per h strip and per XU_d tile, gate/up rank >= 320";
+      return hipErrorInvalidValue;
+    }
+    e = coop<1, true>(p, grid, st);
+  } else if (mt == 1)
     e = coop<1>(p, grid, st);
   else if (mt == 2)
     e = coop<2>(p, grid, st);

@@ -71,6 +71,7 @@ struct DecLayerParams {
   uint16_t* h;     // (T, ff) bf16
   uint16_t* xd16;  // (T, r_d) bf16 down rank intermediate
   float* slices;   // split-K partial sums, MT * 2048 floats per unit (kDlMaxGrid units)
+  float* cslices;  // contracted layer: partial XU_d tiles, (r_d / 128, units2, T, 128) fp32
   uint64_t* sync;  // barrier words, one per 128-byte line (kDl*), then split-K tile counters
   int T, d, ff, r_gu, r_d;
   int ks1, ks3, ks4;                   // K per split, phases 1, 3, 4 (multiples of 32)
@@ -301,13 +302,23 @@ __device__ __forceinline__ void dl_wait_head(int j) {
   }
 }
 
+// No weight DMAs in the run-out steps (stages past the unit's K): the
+// default of dl_run, whose dl_dma_w then fetches nothing.
+struct DlNoRunOut {
+  static constexpr bool kActive = false;
+  __device__ void operator()(int, int) const {}
+};
+
 // Runs one unit: returns the accumulators (lane: D[n = 4*lg + t][m = lr] of
 // each 16-row block mt).  `prefetched`: waves 1..7 already issued their
 // weight DMAs of stages 0..NS-2 (before the grid barrier); wave 0 issues
 // its own here, ahead of the activation DMAs, keeping every wave's order
-// W(0..NS-2), A(0..NS-2), then (W, A) per step.
-template <int MT, bool DUAL>
-__device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool prefetched, f32x4 (&acc)[MT]) {
+// W(0..NS-2), A(0..NS-2), then (W, A) per step.  `run_out(i, slot)`, when
+// active, issues the weight DMAs (KC per wave) of what follows the unit in
+// place of the empty stages past its K: stage nk + i goes to `slot`.
+template <int MT, bool DUAL, class RunOut = DlNoRunOut>
+__device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool prefetched, f32x4 (&acc)[MT],
+                                       const RunOut& run_out = RunOut{}) {
   using S = DlShape<MT, DUAL>;
   using L = DlLds<MT>;
   constexpr int NS = L::NS, KC = L::KC;
@@ -332,7 +343,10 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
       dl_wait_vm<(NS - 2) * S::P>();
     dl_block_sync();
     const int sn = j + NS - 1, slot_n = sn % NS;
-    dl_dma_w<MT, DUAL>(c, U, sn, slot_n);
+    if (RunOut::kActive && sn >= nk)
+      run_out(sn - nk, slot_n);
+    else
+      dl_dma_w<MT, DUAL>(c, U, sn, slot_n);
     dl_dma_a<MT, DUAL>(c, U, sn, slot_n);
 
     const int slot = j % NS;
@@ -446,7 +460,235 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
   }
 }
 
+// ---------------------------------------------------------------------------
+// Contracted layer (phases 2 and 3 fused): unit u computes its 64-column
+// strip of h as in phase 2 and keeps it in LDS as the A operand of
+// XU_d += h[:, strip] . Ud[strip, :], so h never leaves the block; the
+// (T, r_d) partial of every unit goes to the workspace as one fp32 slice per
+// 128-column tile, and one otherwise idle block per tile sums the units'
+// slices in unit order into bf16 XU_d while the units still stream.
+// ---------------------------------------------------------------------------
+
+// LDS byte offset of the h tile (two 32-k chunks of 16 * MT rows of 64
+// bytes, A-operand layout) within the activation region, after the 4 KB *
+// MT exchange area of the SwiGLU epilogue.
 template <int MT>
+struct DlH {
+  static constexpr int XCH = 4 * MT * 64 * 16;
+  static constexpr int OFF = XCH;
+  static constexpr int CHUNK = MT * 16 * 64;
+  static_assert(OFF + 2 * CHUNK <= DlLds<MT>::NS * DlLds<MT>::A_SLOT, "h tile fits the activation region");
+};
+
+// h = bf16(SiLU(g) * u) of the unit's strip into LDS (waves 0..3 hold g,
+// waves 4..7 u, for the same lanes' (m, n)).  Column n = 16 * wave + 4 * lg
+// + t of the strip is k = n of the down projection: chunk n / 32, 16-byte
+// piece (n % 32) / 8 at slot piece ^ a_swz(m) of row m.
+template <int MT>
+__device__ __forceinline__ void dl_contract_h(const DlCtx& c, char* lds, const f32x4 (&acc)[MT]) {
+  using L = DlLds<MT>;
+  using H = DlH<MT>;
+  f32x4* xch = reinterpret_cast<f32x4*>(lds + L::A_OFF);
+  if (c.wave >= 4) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xch[((c.wave - 4) * MT + mt) * 64 + c.lane] = acc[mt];
+  }
+  dl_block_sync();
+  if (c.wave < 4) {
+    char* hl = lds + L::A_OFF + H::OFF + (c.wave >> 1) * H::CHUNK;
+    const int piece = 2 * (c.wave & 1) + (c.lg >> 1);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + c.lr;
+      const f32x4 uv = xch[(c.wave * MT + mt) * 64 + c.lane], g = acc[mt];
+      *reinterpret_cast<u32x2*>(hl + m * 64 + ((piece ^ a_swz(m)) << 4) + (c.lg & 1) * 8) =
+          u32x2{dl_pack_bf16x2(silu_f32(g.x) * uv.x, silu_f32(g.y) * uv.y),
+                dl_pack_bf16x2(silu_f32(g.z) * uv.z, silu_f32(g.w) * uv.w)};
+    }
+  }
+  dl_block_sync();
+}
+
+// Byte size of the contracted slices: nt tiles x units x T rows x 128 fp32.
+__host__ __device__ constexpr int64_t dl_contract_bytes(int64_t nt, int64_t units, int64_t T) {
+  return nt * units * T * 128 * 4;
+}
+
+// Weight DMAs (KC = 2 per wave) of stage j of unit u's down half -- tile j:
+// 128 columns of Ud's rows 64u .. 64u+63 -- into ring slot `slot`, with
+// dl_dma_w's lane geometry (non-DUAL: row 8 * (wave % 4) + lane / 8 of each
+// 32-k chunk); stages past the last tile fetch nothing and keep the count.
+template <int MT>
+__device__ __forceinline__ void dl_contract_dma(const DlCtx& c, const void* ud, int ld_ud, int ff, int u, int NT,
+                                                int j, int slot) {
+  using L = DlLds<MT>;
+  static_assert(L::KC == 2, "one 64-k strip per ring stage");
+  const int sub = c.wave >> 2, lu = c.wave & 3;
+  const int row = 8 * lu + (c.lane >> 3);
+  const int col = 64 * sub + 16 * (((c.lane & 7) >> 1) ^ (row & 3)) + 8 * (c.lane & 1);
+  const uint32_t ldb2 = (uint32_t)ld_ud * 2u;
+  const uint32_t voff = (uint32_t)row * ldb2 + (uint32_t)col * 2u;
+  const bool live = j < NT;  // uniform
+  const i32x4 rs = make_rsrc_sgpr(ud, live ? (uint32_t)((int64_t)ff * ld_ud * 2) : 0u);
+  const uint32_t k_base = (uint32_t)(64 * u) * ldb2;
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+    dma16(rs, voff, live ? k_base + (uint32_t)(32 * kc) * ldb2 + (uint32_t)(128 * j) * 2u : 0u,
+          c.lbase + L::W_OFF + slot * L::W_SLOT + kc * kDlWStage + sub * 4096 + lu * 1024);
+}
+
+// dl_run's run-out hook of a contracted unit: stage nk + i is the down
+// half's stage i.
+template <int MT>
+struct DlContractRunOut {
+  static constexpr bool kActive = true;
+  DlCtx c;
+  const void* ud;
+  int ld_ud, ff, u, nt;
+  __device__ __forceinline__ void operator()(int i, int slot) const {
+    dl_contract_dma<MT>(c, ud, ld_ud, ff, u, nt, i, slot);
+  }
+};
+
+// The down half of unit u: stage j of the ring (slot (s0 + j) % NS) is tile
+// j, multiplied by the h fragments held in registers; the tile's partial is
+// stored as slice (j, u) (rows < T, one 16-byte device-scope store per lane
+// and 16-row block).  Stages 0..NS-2 were issued during the gate/up run-out
+// and have landed (that run ends with a full drain).  Per wave and stage:
+// MT stores, then the weight DMAs of stage j + NS - 1, so waiting for stage
+// j (NS - 2 stages of MT + 2 operations issued after it) also completes the
+// stores of tile j - NS + 1, whose arrival is counted then; the last NS - 1
+// tiles arrive after a final drain.  The counter of tile j is cnt0 + j.
+template <int MT>
+__device__ __forceinline__ void dl_contract_down(const DlCtx& c, const DecLayerParams& p, char* lds, int u, int U2,
+                                                 int NT, int cnt0, int s0) {
+  using L = DlLds<MT>;
+  using H = DlH<MT>;
+  constexpr int NS = L::NS, P = MT + 2;
+  const int sub = c.wave >> 2, lu = c.wave & 3;
+  // h fragments: chunk kc, rows 16 * mt + lr
+  u32x4 fa[2][MT];
+#pragma unroll
+  for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + c.lr;
+      fa[kc][mt] = lds_read_b128(c.l0 + L::A_OFF + H::OFF + kc * H::CHUNK + m * 64 + ((c.lg ^ a_swz(m)) << 4));
+    }
+  const int k_lo = 8 * c.lg + (c.lr >> 2);
+  const int b_off = L::W_OFF + sub * 4096 + k_lo * 128 + ((lu ^ (k_lo & 3)) << 5) + ((c.lr & 3) << 3);
+  const int colo = 64 * sub + 16 * lu + 4 * c.lg;
+  const __amdgpu_buffer_rsrc_t rs_sl =
+      __builtin_amdgcn_make_buffer_rsrc(p.cslices, 0, (int)dl_contract_bytes(NT, U2, c.T), 0x00020000);
+
+  for (int j = 0; j < NT; ++j) {
+    dl_wait_vm<(NS - 2) * P>();
+    dl_block_sync();
+    if (j >= NS - 1 && threadIdx.x == 0)
+      __hip_atomic_fetch_add(dl_tile_counter(p.sync, cnt0 + j - (NS - 1)), 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    const int slot = (s0 + j) % NS;
+    f32x4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const lds_cptr wb = c.l0 + slot * L::W_SLOT + kc * kDlWStage + b_off;
+      const u32x2 lo = lds_read_tr(wb), hi = lds_read_tr(wb + 512);
+      const u32x4 fb = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_chunk(fb, fa[kc][mt], acc[mt], __bf16{});
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = 16 * mt + c.lr;
+      const uint32_t off =
+          m < c.T ? (uint32_t)(((((int64_t)j * U2 + u) * c.T + m) * 128 + colo) * 4) : kDlPastSlices;
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y),
+                                                   __float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)},
+                                             rs_sl, off, 0, kDlSc1);
+    }
+    dl_contract_dma<MT>(c, p.ud, p.ld_ud, p.ff, u, NT, j + NS - 1, (s0 + j + NS - 1) % NS);
+  }
+  dl_wait_vm<0>();
+  dl_block_sync();
+  if (threadIdx.x < NS - 1) {
+    const int t = NT - (NS - 1) + (int)threadIdx.x;
+    if (t >= 0)
+      __hip_atomic_fetch_add(dl_tile_counter(p.sync, cnt0 + t), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Tile j of XU_d from the U2 units' slices: the block waits (bounded, as at
+// a grid barrier) until all U2 units have counted their slice of the tile,
+// resets the counter, and sums in a fixed order: with R the power of two
+// >= T and G = 16 / R, thread i takes float4 column q = i % 32 of row
+// m = (i / 32) / G and units g, g + G, g + 2G, ... (g = (i / 32) % G), 16
+// loads in flight, then the G partial sums of each (m, q) are added in g
+// order through LDS; XU_d is rounded to bf16 once.
+template <int MT>
+__device__ __forceinline__ void dl_contract_combine(const DlCtx& c, const DecLayerParams& p, char* lds, int j, int U2,
+                                                    int cnt0, uint32_t spin_reg, const uint32_t* spin_lds, int* bad) {
+  using L = DlLds<MT>;
+  static_assert(kDlThreads == 512, "16 groups of 32 threads");
+  if (threadIdx.x == 0) {
+    uint32_t* cnt = dl_tile_counter(p.sync, cnt0 + j);
+    const uint32_t spin = spin_lds ? *spin_lds : spin_reg;
+    uint32_t polls = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)U2) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++polls >= spin) {
+        __hip_atomic_fetch_or(&p.sync[kDlFlag], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_or(&p.sync[kGvDone], kGvDoneBad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        dl_wait_vm<0>();
+        *bad = 1;
+        break;
+      }
+    }
+    // every arrival of this launch is in (or the wait gave up): back to zero
+    // for the next launch (a late arrival after a give-up leaves it nonzero,
+    // as the timeout flag does; the caller resets the area)
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  dl_block_sync();
+  const int R = c.T <= 1 ? 1 : (c.T <= 2 ? 2 : (c.T <= 4 ? 4 : (c.T <= 8 ? 8 : 16)));
+  const int G = 16 / R;
+  const int q = threadIdx.x & 31, grp = threadIdx.x >> 5, m = grp / G, g = grp % G;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(p.cslices, 0, (int)dl_contract_bytes(p.r_d / 128, U2, c.T), 0x00020000);
+  f32x4* red = reinterpret_cast<f32x4*>(lds + L::A_OFF);  // 16 x 32 partial sums
+  f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (m < c.T) {
+    constexpr int B = 16;  // loads in flight per thread
+    for (int u0 = g; u0 < U2; u0 += B * G) {
+      u32x4 v[B];
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const int uu = u0 + G * i;
+        const uint32_t off =
+            uu < U2 ? (uint32_t)(((((int64_t)j * U2 + uu) * c.T + m) * 128 + 4 * q) * 4) : kDlPastSlices;
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kDlSc1);
+      }
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        sum.x += __uint_as_float(v[i].x);
+        sum.y += __uint_as_float(v[i].y);
+        sum.z += __uint_as_float(v[i].z);
+        sum.w += __uint_as_float(v[i].w);
+      }
+    }
+  }
+  red[grp * 32 + q] = sum;
+  dl_block_sync();
+  if (g == 0 && m < c.T) {
+    f32x4 tot = red[grp * 32 + q];
+    for (int gg = 1; gg < G; ++gg) tot += red[(grp + gg) * 32 + q];
+    dl_store8(p.xd16 + (int64_t)m * p.r_d + 128 * j + 4 * q,
+              u32x2{dl_pack_bf16x2(tot.x, tot.y), dl_pack_bf16x2(tot.z, tot.w)});
+  }
+}
+
+template <int MT, bool CONTRACT = false>
 __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerParams p) {
   using L = DlLds<MT>;
   __shared__ __attribute__((aligned(1024))) char lds[L::BYTES];
@@ -565,6 +807,29 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   prefetch(2);
   dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
 
+  if constexpr (CONTRACT) {
+    // ---- phases 2 and 3 contracted: unit b < units2 keeps its h strip in
+    // LDS and stores partial XU_d tiles; blocks units2 .. units2 + nt3 - 1
+    // each sum one tile (the launcher checks that the grid holds both) ----
+    const int U2 = units[2];
+    if (b < U2) {
+      DlUnit U;
+      unit_of(2, b, U);
+      f32x4 acc[MT];
+      // the down half's first NS - 1 stages stream in during the gate/up
+      // run-out (the launcher checks that the gate/up rank has >= NS - 1 stages)
+      const DlContractRunOut<MT> run_out{c, p.ud, p.ld_ud, p.ff, b, nt3};
+      dl_run<MT, true>(c, U, true, acc, run_out);
+      const int nk = (U.ke - U.kb + 32 * L::KC - 1) / (32 * L::KC);
+      dl_contract_h<MT>(c, lds, acc);
+      dl_contract_down<MT>(c, p, lds, b, U2, nt3, nt1, nk % NS);
+    } else if (b < U2 + nt3) {
+      dl_contract_combine<MT>(c, p, lds, b - U2, U2, nt1, spin, spin_lds, bad);
+    }
+    dl_wait_vm<0>();
+    prefetch(4);
+    dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
+  } else {
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
   for (int u = b; u < units[2]; u += G) {
     DlUnit U;
@@ -609,6 +874,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   dl_wait_vm<0>();
   prefetch(4);
   dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
+  }
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
   for (int u = b; u < units[4]; u += G) {

@@ -63,7 +63,11 @@ hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hip
 // block per CU, else 0.
 int decode_layer_mt(int T);
 int decode_layer_grid(int mt);
-hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why);
+// contract: the contracted instance (phases 2 and 3 fused, h kept in LDS),
+// grid = decode_layer_contract_grid().
+int decode_layer_contract_grid();
+hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why,
+                               bool contract = false);
 // Streaming-GEMV decode layer (T <= 2): rows per wave load rw (1 or 2),
 // grid = CU count when the kernel fits one block per CU, else 0.
 struct GvParams;

@@ -24,6 +24,7 @@ SVDMLP_U_LINEAR = 0x1
 SVDMLP_V_LINEAR = 0x2
 SVDMLP_OUT_T = 0x4
 SVDMLP_X_T = 0x8
+SVDMLP_CONTRACT = 0x10
 SVDMLP_OK = 0
 SVDMLP_EINVAL = -1
 SVDMLP_EHIP = -2

@@ -416,17 +416,21 @@ def _pad_branches(u_gate, v_gate, u_up, v_up):
 
 
 def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
-            out: torch.Tensor | None = None) -> torch.Tensor:
+            out: torch.Tensor | None = None, contracted: bool = False) -> torch.Tensor:
     """Full SVD SwiGLU block, fused_xuv(fused_gate_up(x)) with h rounded to
     x.dtype in between (kernels/reference.py:85-93).  The gate, up and down
     ranks may all differ: the large-tile path (more than 128 tokens) runs
     each branch at its own rank; other shapes zero-pad the smaller of the
     gate and up branches, which does not change the result.
     ``workspace``/``out`` may be supplied to avoid per-call allocation (see
-    :func:`svd_mlp_workspace`, with r the largest rank)."""
+    :func:`svd_mlp_workspace`, with r the largest rank).  ``contracted``
+    asks for the contracted layer (SVDMLP_CONTRACT: h kept inside the
+    kernel, taken at 1-4 tokens; other shapes run as without it)."""
     lib = _lib.load()
     x, ptrs, holders, flags, w_code, scale_arr, ld_arr, out, workspace, dims, dev = _prepare_layer(
         x, u_gate, v_gate, u_up, v_up, u_down, v_down, workspace, out)
+    if contracted:
+        flags |= _lib.SVDMLP_CONTRACT
     rc = _on_device(dev, lambda: lib.svdmlp_svd_mlp_ranks(
         x.data_ptr(), *ptrs,
         ctypes.addressof(scale_arr) if scale_arr is not None else None,
@@ -435,7 +439,8 @@ def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.T
         workspace.data_ptr(), workspace.numel(), _stream(dev)))
     del holders
     if rc == _lib.SVDMLP_EUNSUP:
-        return svd_mlp(x, *_pad_branches(u_gate, v_gate, u_up, v_up), u_down, v_down, workspace=workspace, out=out)
+        return svd_mlp(x, *_pad_branches(u_gate, v_gate, u_up, v_up), u_down, v_down, workspace=workspace, out=out,
+                       contracted=contracted)
     _lib.check(rc)
     return out
 

@@ -22,15 +22,17 @@ does, and return freshly allocated outputs.
   accumulation, fp32 inputs fp32 MFMA (at least the precision of either
   reference mode).
 * ``interpret=True`` (the Pallas CPU emulator) has no counterpart and raises.
-* ``contracted_svd_mlp`` is the variant whose HBM boundary is the rank-r
-  Down-XU instead of h.  It returns the same y as ``svd_mlp``.  On MI355X the
-  decode path already runs the whole layer in one persistent launch (h never
-  crosses a kernel boundary); for prefill the two-kernel boundary is kept,
-  because carrying h through the Down-U product on a GPU either keeps a
-  (rows x r) fp32 accumulator per block (16 rows x 2816 already fill a CU's
-  registers, so every block would stream all of Vg, Vu and Ud) or recomputes
-  h once per rank tile, both far costlier than h's round trip (~10 us of HBM
-  time for the 8B layer at 1024 tokens).
+* ``contracted_svd_mlp`` is the variant whose boundary is the rank-r Down-XU
+  instead of h (models/modeling_llama.py:865-886).  At 1-4 tokens it runs the
+  contracted decode layer (SVDMLP_CONTRACT): every block computes a 64-column
+  strip of h, keeps it in LDS and multiplies it by the matching rows of Ud,
+  so h never leaves the block and only fp32 (T, r_d) partials of XU_d cross
+  blocks, summed in a fixed order.  Other shapes run the two-kernel layer
+  (same y): for prefill, carrying h through the Down-U product on a GPU
+  either writes a (rows x r_d) fp32 partial per h strip (64 strips of 224
+  columns at 8B, ~740 MB at 1024 tokens, against h's 29 MB) or recomputes h
+  once per rank tile; at 5-128 tokens the partials outgrow h's round trip
+  inside the persistent layer.
 * ``dense_mlp`` is the uncompressed SwiGLU of the dense comparison arm
   (kernels/reference.py:96-106); it runs on the vendor library (hipBLASLt via
   torch) at the input dtype with the SiLU product in fp32.
@@ -86,10 +88,12 @@ def xuv_matmul(x, u, v, *, mixed_precision=True, interpret=False) -> torch.Tenso
 
 def contracted_svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, gate_up_blocks=None,
                        mixed_precision=True, interpret=False) -> torch.Tensor:
-    """The contracted variant's interface (same y as :func:`svd_mlp`)."""
+    """The contracted variant: h kept inside the kernel, (T, r_d) partials of
+    Down-XU as the only cross-block data (same y as :func:`svd_mlp` up to
+    fp32 summation order)."""
     _check_blocks(gate_up_blocks, "gate_up_blocks")
     _check_interpret(interpret)
-    return ops.svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down)
+    return ops.svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, contracted=True)
 
 
 def dense_mlp(x, w_gate, w_up, w_down, *, mixed_precision=True, interpret=False) -> torch.Tensor:

@@ -20,6 +20,15 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = 1e-2
 FP8_TOL = 3e-2
 GEMV_LAYER_MAX_T = 2   # kGvMaxT in csrc/decode_gemv.hpp
+CONTRACT_AUTO_T = 3    # kDlContractAutoT in csrc/api.hip: the contracted decode layer by default
+
+
+def _contracted(shape, T):
+    """Whether a bf16 natural-layout call runs the contracted decode layer by
+    default: 1-3 tokens, d and ranks multiples of 128, ff of 64, gate/up rank
+    >= 320, a block per h strip and per XU_d tile (256 CUs)."""
+    return (T <= CONTRACT_AUTO_T and shape.d % 128 == 0 and shape.r % 128 == 0 and shape.rd % 128 == 0
+            and shape.ff % 64 == 0 and shape.r >= 320 and shape.ff // 64 + shape.rd // 128 <= 256)
 
 
 def _to(a, dtype, dev):
@@ -223,12 +232,13 @@ def _tile_counters(ws):
     (inputs.LayerShape(16640, 1024, 128), (8, 64)),                     # 130 output tiles: phase 4 unsplit
 ])
 def test_decode_layer_workspace_reuse(gpu, shape, Ts):
-    """The persistent decode kernels (the streaming-GEMV layer up to 2
-    tokens, the MFMA layer above; one launch each, grid barriers and split-K
-    tile counters in the workspace's first 4096 bytes) over one reused
-    workspace: results match the oracle, every call advances the shared
-    barrier generation by its barriers, no barrier times out and every tile
-    counter is back at zero."""
+    """The persistent decode kernels (the contracted layer at 1-3 tokens, the
+    streaming-GEMV layer up to 2 tokens where the former does not run, the
+    MFMA layer above; one launch each, grid barriers and split-K tile
+    counters in the workspace's first 4096 bytes) over one reused workspace:
+    results match the oracle, every call advances the shared barrier
+    generation by its barriers, no barrier times out and every tile counter
+    is back at zero."""
     x, f = inputs.make_layer(shape, T=max(Ts), seed=31)
     xb, *fb = _rounded((x, *f), torch.bfloat16)
     t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
@@ -238,7 +248,8 @@ def test_decode_layer_workspace_reuse(gpu, shape, Ts):
         y = _np(ops.svd_mlp(t[0][:T].contiguous(), *t[1:], workspace=ws))
         err = _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16"))
         assert err < BF16_TOL, (T, err)
-        gen += 4 if T <= GEMV_LAYER_MAX_T else 3   # GEMV layer: 4 barriers, MFMA layer: 3
+        # contracted layer: 2 barriers, GEMV layer: 4, MFMA layer: 3
+        gen += 2 if _contracted(shape, T) else (4 if T <= GEMV_LAYER_MAX_T else 3)
         assert _barrier_state(ws) == (gen, 0), T
         assert not any(_tile_counters(ws)), T
 
@@ -350,10 +361,13 @@ def test_replay_is_bitwise_identical(gpu, layer8b, T, padded):
     assert _rel(_np(ys[0])[: min(T, 16)], O.svd_mlp_ref(_np(xt)[: min(T, 16)], *f, dtype="bfloat16")) < BF16_TOL
 
 
-@pytest.mark.parametrize("shape,T", [(inputs.LayerShape(1024, 2048, 512), 8),     # MFMA decode layer
-                                     (inputs.LayerShape(1024, 2048, 512), 1),     # streaming-GEMV layer
-                                     (inputs.LayerShape(1040, 2064, 400, 272), 2)])  # GEMV, ragged strips
-def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T):
+@pytest.mark.parametrize("shape,T,contracted", [
+    (inputs.LayerShape(1024, 2048, 512), 8, False),        # MFMA decode layer
+    (inputs.LayerShape(1040, 2064, 400, 272), 1, False),   # streaming-GEMV layer
+    (inputs.LayerShape(1040, 2064, 400, 272), 2, False),   # GEMV, ragged strips
+    (inputs.LayerShape(1024, 2048, 512), 4, True),         # contracted layer (asked for): tile-combine waits too
+    (inputs.LayerShape(1024, 2048, 512), 1, False)])       # contracted layer (the default at 1-3 tokens)
+def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T, contracted):
     """A persistent decode launch whose grid-barrier waits give up (forced
     from the host with a bound of one poll, so every block still runs to its
     end) writes NaN into y, reports the timeout through the workspace
@@ -363,17 +377,66 @@ def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T):
     t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
     ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
     ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
-    assert _rel(_np(ops.svd_mlp(*t, workspace=ws)), ref) < BF16_TOL
+    assert _rel(_np(ops.svd_mlp(*t, workspace=ws, contracted=contracted)), ref) < BF16_TOL
     assert ops.workspace_status(ws) is False
     _set_spin_bound(ws, 1)
-    y = _np(ops.svd_mlp(*t, workspace=ws))
+    y = _np(ops.svd_mlp(*t, workspace=ws, contracted=contracted))
     assert np.isnan(y).all(), f"{np.isnan(y).mean():.3f} of y is NaN"
     assert ops.workspace_status(ws) is True
     assert ops.workspace_status(ws, reset=True) is True   # reports, then zeroes the sync area
     assert ops.workspace_status(ws) is False and _barrier_state(ws) == (0, 0)
     for _ in range(2):
-        assert _rel(_np(ops.svd_mlp(*t, workspace=ws)), ref) < BF16_TOL
+        assert _rel(_np(ops.svd_mlp(*t, workspace=ws, contracted=contracted)), ref) < BF16_TOL
     assert ops.workspace_status(ws) is False
+
+
+# ---------------------------------------------------------------------------
+# the contracted layer (SVDMLP_CONTRACT; models/modeling_llama.py:865-886)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+def test_contracted_decode_layer_8b(gpu, layer8b, T):
+    """The contracted decode layer (each block's h strip kept in LDS and
+    multiplied by its Ud rows; the (T, r_d) partials of XU_d summed in unit
+    order by dedicated blocks) against the oracle, bitwise on replay, with
+    dense and row-padded factors: one launch with two grid barriers per call,
+    every tile counter back at zero."""
+    shape, f, ft = layer8b
+    xt = _to(_x(T, shape.d, 600 + T), torch.bfloat16, gpu)
+    ref = O.svd_mlp_ref(_np(xt), *f, dtype="bfloat16")
+    for fs in (ft, [ops.pad_rows(a, 64) if i % 2 else a for i, a in enumerate(ft)]):
+        ws = ops.svd_mlp_workspace(xt, r=shape.r, ff=shape.ff)
+        ys = [ops.svd_mlp(xt, *fs, workspace=ws, contracted=True).clone() for _ in range(3)]
+        assert _barrier_state(ws) == (6, 0) and not any(_tile_counters(ws))
+        for y in ys[1:]:
+            assert torch.equal(y.view(torch.int16), ys[0].view(torch.int16))
+        err = _rel(_np(ys[0]), ref)
+        print(f"contracted 8B T={T} rel_l2={err:.3e}")
+        assert err < BF16_TOL
+        assert _rel(_np(ys[0]), _np(ops.svd_mlp(xt, *fs, workspace=ws))) < 5e-3
+
+
+@pytest.mark.parametrize("shape,T", [
+    (inputs.LayerShape(1024, 2048, 512, 384), 1),   # 3 XU_d tiles: fewer than the ring depth
+    (inputs.LayerShape(1024, 2048, 512, 384), 4),
+    (inputs.LayerShape(3072, 8192, 1792), 2),       # the reference runner's default (3B) shape
+    (inputs.LayerShape(1024, 2048, 512, 384), 8),   # beyond 4 tokens: the three-barrier layer
+    (inputs.LayerShape(1024, 2048, 512, 384), 300)])
+def test_contracted_svd_mlp_entry(gpu, shape, T):
+    """pallas_ops.contracted_svd_mlp: the contracted layer at 1-4 tokens, the
+    same y from the other paths elsewhere."""
+    from svdmlp import pallas_ops
+
+    x, f = inputs.make_layer(shape, T=T, seed=610 + T)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
+    y = _np(ops.svd_mlp(*t, workspace=ws, contracted=True))
+    if T <= 128:
+        assert _barrier_state(ws)[0] == (2 if T <= 4 else 3) and not any(_tile_counters(ws))
+    ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
+    assert _rel(y, ref) < BF16_TOL
+    assert _rel(_np(pallas_ops.contracted_svd_mlp(*t)), ref) < BF16_TOL
 
 
 # ---------------------------------------------------------------------------
@@ -675,11 +738,11 @@ def test_padded_factor_rows(gpu, T):
     ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
     err = _rel(_np(ops.svd_mlp(t[0], *padded, workspace=ws)), ref)
     assert err < BF16_TOL, err
-    if T <= 128:   # one MFMA decode-layer launch: 3 barriers, counters back at zero
-        assert _barrier_state(ws) == (3, 0) and not any(_tile_counters(ws))
+    if T <= 128:   # one MFMA decode-layer launch (2 barriers contracted, else 3), counters back at zero
+        assert _barrier_state(ws) == (2 if _contracted(shape, T) else 3, 0) and not any(_tile_counters(ws))
     dense = _np(ops.svd_mlp(*t))
-    # the same math; at T <= 2 dense factors take the streaming-GEMV layer
-    # (fp32 atomics) and padded ones the MFMA layer, so roundings may differ
+    # the same math; split-K partials are summed in other orders on the
+    # paths the two layouts take, so roundings may differ
     assert _rel(_np(ops.svd_mlp(t[0], *padded)), dense) < 5e-3
 
 

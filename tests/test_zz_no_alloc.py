@@ -46,9 +46,9 @@ def _call_both(lib, x, fs, dims, dev):
 
 
 @pytest.mark.parametrize("shape,Ts,pad", [
-    (inputs.LayerShape(4096, 14336, 2816), (64, 8, 1), 64),    # LLaMA3-8B decode: MFMA decode layer
+    (inputs.LayerShape(4096, 14336, 2816), (64, 8, 1), 64),    # LLaMA3-8B decode: MFMA decode layer (contracted at 1)
     (inputs.LayerShape(1024, 2048, 512, 384), (300, 160), 0),   # large-tile prefill path (fits the scratch)
-    (inputs.LayerShape(1024, 2048, 512), (2, 1), 0),            # streaming-GEMV layer (dense, 1-2 tokens)
+    (inputs.LayerShape(1040, 2064, 400, 272), (2, 1), 0),       # streaming-GEMV layer (1-2 tokens, d % 128 != 0)
 ])
 def test_noalloc_matches_workspace_entry_point(gpu, shape, Ts, pad):
     lib = _lib.load()
