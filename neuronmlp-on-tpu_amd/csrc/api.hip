@@ -153,14 +153,16 @@ struct StageScope {
 size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
 
 // Token counts the contracted decode layer (SVDMLP_CONTRACT) takes: its
-// partial XU_d slices grow with T (8B layer: 2.5 MB per token).  Up to
-// kDlContractAutoT tokens it is the default wherever it runs (8B layer,
-// padded V rows: T=1 74.5 -> 71.0 us, T=2 74.5 -> 72.5, T=3 74.5 -> 74.0,
-// T=4 74.6 -> 75.2; dense factors, against the streaming-GEMV layer at
-// T <= 2 and the three-barrier layer at 3: 77.6 -> 74.5, 80.7 -> 77.0,
-// 81.8 -> 77.4).
+// partial XU_d slices grow with T (8B layer: 2.5 MB per token).  It is the
+// default where it is the fastest layer, measured on the 8B layer: with
+// padded V rows at one token (three-barrier layer against contracted: T=1
+// 71.6 vs 70.0 us, T=2 72.3 vs 72.7, T=3 71.9 vs 73.5), with dense factors
+// up to three (the streaming-GEMV layer at T <= 2, the three-barrier layer
+// at 3, against contracted: 77.4 vs 73.6, 80.7 vs 76.0, 78.3 vs 76.8; T=4
+// 78.6 vs 78.8).
 constexpr int64_t kDlContractMaxT = 4;
-constexpr int64_t kDlContractAutoT = 3;
+constexpr int64_t kDlContractAutoPadded = 1;
+constexpr int64_t kDlContractAutoDense = 3;
 
 struct Ws {
   size_t sync;     // 4 KB of grid-barrier words (zero before first use)
@@ -402,7 +404,7 @@ struct Tune {
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
   int nw = 8;          // waves per block of the fn-8 X.U and XU.V stages (8, or 4: faster in isolation, not in the layer)
-  bool contract = true; // contracted decode layer by default at T <= kDlContractAutoT
+  bool contract = true; // contracted decode layer by default where it is the fastest (kDlContractAuto*)
 };
 
 const Tune& tune() {
@@ -1272,7 +1274,7 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
       if (!scales[i]) return fail("fp8 weights need per-column scales");
   }
   if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_CONTRACT)) return fail("unsupported flags 0x%x", flags);
-  const bool contract = (flags & SVDMLP_CONTRACT) || (T <= kDlContractAutoT && tune().contract);
+  const bool contract_asked = flags & SVDMLP_CONTRACT;
   flags &= ~SVDMLP_CONTRACT;
   if (fp8 && flags) return fail("fp8 weights must use the natural layout");
   // one rank for both branches below; two ranks only on the large-tile path
@@ -1350,9 +1352,11 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
   // With padded V rows the MFMA decode layer is the faster one at every T
   // (8B layer at T=1: 75.5 us against 78 us): the streaming-GEMV layer reads
   // whole 1 KB row pieces, which the padding does not spread over channels.
-  // The contracted instance first wherever it applies (asked for, or at
-  // T <= kDlContractAutoT), then the streaming-GEMV layer, then the
+  // The contracted instance first wherever it applies (asked for, or where
+  // it is the fastest), then the streaming-GEMV layer, then the
   // three-barrier MFMA layer.
+  const bool contract =
+      contract_asked || (tune().contract && T <= (ld.dense ? kDlContractAutoDense : kDlContractAutoPadded));
   const bool mfma_layer = decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld);
   if (mfma_layer && contract && decode_contract_ok(T, ff, r_gu, r_d, L, ws_bytes))
     return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld, true);

@@ -20,14 +20,16 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = 1e-2
 FP8_TOL = 3e-2
 GEMV_LAYER_MAX_T = 2   # kGvMaxT in csrc/decode_gemv.hpp
-CONTRACT_AUTO_T = 3    # kDlContractAutoT in csrc/api.hip: the contracted decode layer by default
+# kDlContractAutoPadded / kDlContractAutoDense in csrc/api.hip: the contracted
+# decode layer by default at 1 token with padded factor rows, up to 3 with dense
+CONTRACT_AUTO_T = {True: 1, False: 3}
 
 
-def _contracted(shape, T):
+def _contracted(shape, T, padded=False):
     """Whether a bf16 natural-layout call runs the contracted decode layer by
-    default: 1-3 tokens, d and ranks multiples of 128, ff of 64, gate/up rank
-    >= 320, a block per h strip and per XU_d tile (256 CUs)."""
-    return (T <= CONTRACT_AUTO_T and shape.d % 128 == 0 and shape.r % 128 == 0 and shape.rd % 128 == 0
+    default: its token counts, d and ranks multiples of 128, ff of 64, gate/up
+    rank >= 320, a block per h strip and per XU_d tile (256 CUs)."""
+    return (T <= CONTRACT_AUTO_T[padded] and shape.d % 128 == 0 and shape.r % 128 == 0 and shape.rd % 128 == 0
             and shape.ff % 64 == 0 and shape.r >= 320 and shape.ff // 64 + shape.rd // 128 <= 256)
 
 
@@ -232,7 +234,7 @@ def _tile_counters(ws):
     (inputs.LayerShape(16640, 1024, 128), (8, 64)),                     # 130 output tiles: phase 4 unsplit
 ])
 def test_decode_layer_workspace_reuse(gpu, shape, Ts):
-    """The persistent decode kernels (the contracted layer at 1-3 tokens, the
+    """The persistent decode kernels (the contracted layer at 1-3 tokens of dense factors, the
     streaming-GEMV layer up to 2 tokens where the former does not run, the
     MFMA layer above; one launch each, grid barriers and split-K tile
     counters in the workspace's first 4096 bytes) over one reused workspace:
@@ -366,7 +368,7 @@ def test_replay_is_bitwise_identical(gpu, layer8b, T, padded):
     (inputs.LayerShape(1040, 2064, 400, 272), 1, False),   # streaming-GEMV layer
     (inputs.LayerShape(1040, 2064, 400, 272), 2, False),   # GEMV, ragged strips
     (inputs.LayerShape(1024, 2048, 512), 4, True),         # contracted layer (asked for): tile-combine waits too
-    (inputs.LayerShape(1024, 2048, 512), 1, False)])       # contracted layer (the default at 1-3 tokens)
+    (inputs.LayerShape(1024, 2048, 512), 1, False)])       # contracted layer (the default at 1 token)
 def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T, contracted):
     """A persistent decode launch whose grid-barrier waits give up (forced
     from the host with a bound of one poll, so every block still runs to its
@@ -739,7 +741,7 @@ def test_padded_factor_rows(gpu, T):
     err = _rel(_np(ops.svd_mlp(t[0], *padded, workspace=ws)), ref)
     assert err < BF16_TOL, err
     if T <= 128:   # one MFMA decode-layer launch (2 barriers contracted, else 3), counters back at zero
-        assert _barrier_state(ws) == (2 if _contracted(shape, T) else 3, 0) and not any(_tile_counters(ws))
+        assert _barrier_state(ws) == (2 if _contracted(shape, T, padded=True) else 3, 0) and not any(_tile_counters(ws))
     dense = _np(ops.svd_mlp(*t))
     # the same math; split-K partials are summed in other orders on the
     # paths the two layouts take, so roundings may differ
