@@ -202,7 +202,8 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
   for (int64_t rr = std::min<int64_t>(r, 8); rr <= r; rr += (rr + 8 <= r ? 8 : std::max<int64_t>(1, r - rr))) {
     // {K, N, batch, fn}: the rank is N of the X.U stages and K of the XU.V stages
     const int64_t stages[][4] = {{d, rr, 2, 8}, {ff, rr, 1, 8}, {rr, d, 1, 8}, {rr, ff, 1, 8}, {rr, d, 1, 4},
-                                 {rr, ff, 1, 4}, {d, rr, 2, 4}, {ff, rr, 1, 4}};
+                                 {rr, ff, 1, 4}, {d, rr, 2, 4}, {ff, rr, 1, 4}, {d, rr, 2, 6}, {d, rr, 2, 7},
+                                 {ff, rr, 1, 6}, {ff, rr, 1, 7}};
     for (const auto& st : stages) {
       const int sp = plan_splits(T, st[0], st[1], (int)st[3], (int)st[2]);
       // slices hold whole 256 x 32*fn tiles (fragment order)
@@ -394,6 +395,7 @@ int prefill_v(const Common& c, int a_src, const void* xu, const void* v, const f
 // Tile choices; SVDMLP_TUNE="s1=44,s4=88,split=256" overrides them (read once).
 struct Tune {
   int s1 = 8;         // X.U stages: block tile 256 x 32*s1
+  int s1g = 0;        // the gate/up X.U stage alone (0: s1)
   int s4 = 8;         // XU.V of the down half: 256 x 32*s4 (8: split-K over r)
   int s2fn = 0;       // gate/up XU.V tile columns/32 (0 = auto: 4 for T <= 512, else 7 when ff % 224 == 0)
   int split = 256;    // CUs assumed by the split-K planner
@@ -423,6 +425,7 @@ const Tune& tune() {
         const std::string k = kv.substr(0, eq);
         const int v = atoi(kv.c_str() + eq + 1);
         if (k == "s1") r.s1 = v;
+        if (k == "s1g") r.s1g = v;
         if (k == "s4") r.s4 = v;
         if (k == "s2fn") r.s2fn = v;
         if (k == "split") r.split = v;
@@ -461,7 +464,7 @@ bool big_ok(const Common& c, bool vec, std::initializer_list<int64_t> bytes, std
 int big_nw(int fn, int epi, bool b_kc) { return (fn == 8 && epi == BEPI_STORE && !b_kc && tune().nw == 4) ? 4 : 8; }
 
 // Tile shapes whose fragment-order split-K slices the reduction kernel takes.
-bool big_frag_reduce_ok(int fn, int nw) { return (nw == 8 && (fn == 8 || fn == 4)) || (nw == 4 && fn == 8); }
+bool big_frag_reduce_ok(int fn, int nw) { return (nw == 8 && fn >= 4 && fn <= 8 && fn != 5) || (nw == 4 && fn == 8); }
 
 // Batch entry 1 of a large-tile launch whose two entries differ in width
 // (gate and up ranks): its output columns, B row pitch, output row pitch
@@ -582,7 +585,7 @@ FactorLd dense_ld(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d) { return Fac
 // workspace's slice area, else one split.
 int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
             int T, int K, int r, int r1, char* ws, const Ws& L, const float* const* su, int64_t ldu, int64_t ldu1) {
-  const int fn = tune().s1;
+  const int fn = tune().s1g ? tune().s1g : tune().s1;
   const int nw = big_nw(fn, BEPI_STORE, u_lin);
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
   const int64_t ldb0 = u_lin ? K : (ldu ? ldu : r), ldb1 = u_lin ? K : (ldu1 ? ldu1 : r1);
@@ -622,9 +625,16 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
            int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr,
            int64_t ldu = 0) {
-  const int fn = tune().s1;
-  const int ks = plan_ksplit(T, K, r, fn, batch);
-  const int splits = (K + ks - 1) / ks;
+  const int fn = stage == ST_GU_XU && tune().s1g ? tune().s1g : tune().s1;
+  int ks = plan_ksplit(T, K, r, fn, batch);
+  int splits = (K + ks - 1) / ks;
+  {  // the slices must fit the workspace's slice area (sized for the planned tiles)
+    const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn);
+    if (splits > 1 && (int64_t)splits * batch * std::max(tp * np, (int64_t)T * r) * 4 > (int64_t)(L.norm - L.part)) {
+      ks = K;
+      splits = 1;
+    }
+  }
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
   const int64_t ldb = u_lin ? K : (ldu ? ldu : r);  // natural U may carry padded rows
   const int64_t u_bytes = (int64_t)(u_lin ? r : K) * ldb * wbytes(c);

@@ -25,19 +25,20 @@ hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hip
   return d.b_kc ? go<FN, true, EPI, F32>(p, splits, batch, st) : go<FN, false, EPI, F32>(p, splits, batch, st);
 }
 
+// FN 6 (256 x 192 tiles, the rank stages' X.U products) has the store
+// epilogues only.
 template <int FN>
 hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st, const char** why) {
   switch (d.epi) {
     case BEPI_STORE:
-      if (d.out_f32) {
-        if constexpr (FN != 7) return go_b<FN, BEPI_STORE, true>(d, p, splits, batch, st);
-        break;
-      }
+      if (d.out_f32) return go_b<FN, BEPI_STORE, true>(d, p, splits, batch, st);
       return go_b<FN, BEPI_STORE>(d, p, splits, batch, st);
     case BEPI_SWIGLU_MEM:
-      return go_b<FN, BEPI_SWIGLU_MEM>(d, p, splits, batch, st);
+      if constexpr (FN != 6) return go_b<FN, BEPI_SWIGLU_MEM>(d, p, splits, batch, st);
+      break;
     case BEPI_STORE_FRAG:
-      return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
+      if constexpr (FN != 6) return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
+      break;
     default: break;
   }
   *why = "big GEMM: unsupported epilogue for this tile";
@@ -116,6 +117,8 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
                                    int batch, hipStream_t st, const uint16_t* gate) {
   if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
+  if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
+  if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
   if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
   if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
   return hipErrorInvalidValue;
@@ -125,6 +128,7 @@ hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batc
                       const char** why) {
   if (d.fn == 8) return go_e<8>(d, p, splits, batch, st, why);
   if (d.fn == 7) return go_e<7>(d, p, splits, batch, st, why);
+  if (d.fn == 6) return go_e<6>(d, p, splits, batch, st, why);
   if (d.fn == 4) return go_e<4>(d, p, splits, batch, st, why);
   *why = "big GEMM: no compiled instance for this tile";
   return hipErrorInvalidValue;
