@@ -36,11 +36,11 @@ def test_library_exports_every_declared_symbol(lib):
 def test_header_constants_match_binding():
     text = HEADER.read_text()
     for name in ("SVDMLP_F32", "SVDMLP_BF16", "SVDMLP_FP8_E4M3", "SVDMLP_U_LINEAR", "SVDMLP_V_LINEAR",
-                 "SVDMLP_OUT_T", "SVDMLP_X_T"):
+                 "SVDMLP_OUT_T", "SVDMLP_X_T", "SVDMLP_CONTRACT"):
         m = re.search(rf"#define {name} (0x[0-9a-f]+|\d+)", text)
         assert m, name
         assert int(m.group(1), 0) == getattr(_lib, name), name
-    for name, val in (("SVDMLP_EINVAL", -1), ("SVDMLP_EHIP", -2), ("SVDMLP_OK", 0)):
+    for name, val in (("SVDMLP_EINVAL", -1), ("SVDMLP_EHIP", -2), ("SVDMLP_EUNSUP", -3), ("SVDMLP_OK", 0)):
         assert re.search(rf"#define {name} \(?{val}\)?", text), name
 
 
@@ -52,6 +52,9 @@ def test_version_and_workspace(lib):
     assert 0 < small < big
     # prefill: bf16 XU (2*T*r*2) + fp32 XU (3*T*r*4) + h (T*ff*4)
     assert big >= 2 * 1024 * 2816 * 2 + 3 * 1024 * 2816 * 4 + 1024 * 14336 * 4
+    # 1-4 tokens: the contracted layer's partial XU_d tiles, (r/128) x (ff/64) x T x 128 fp32
+    for T in (1, 4):
+        assert lib.svdmlp_workspace_bytes(T, 4096, 14336, 2816, 1) >= 22 * 224 * T * 512
 
 
 def _call_gate_up(lib, T=4, d=16, ff=32, r=8, act=1, wt=1, flags=0, ptr=256, ws=1 << 20):
@@ -76,6 +79,16 @@ def test_invalid_arguments_rejected_before_any_hip_call(lib):
     assert lib.svdmlp_xuv(p, p, p, None, None, p, 4, 16, 16, 0, 1, 1, 0, p, 1 << 20, None) == _lib.SVDMLP_EINVAL
     assert lib.svdmlp_svd_mlp(p, p, p, p, p, p, p, None, p, 4, 16, 32, 8, 8, 1, 2, 0, p, 1 << 20,
                               None) == _lib.SVDMLP_EINVAL
+    # the two-rank entries validate as the one-rank ones (ranks must be positive, flags known)
+    assert lib.svdmlp_svd_mlp_ranks(p, p, p, p, p, p, p, None, None, p, 4, 16, 32, 8, 0, 8, 1, 1, 0, p, 1 << 20,
+                                    None) == _lib.SVDMLP_EINVAL
+    assert b"positive" in lib.svdmlp_last_error()
+    assert lib.svdmlp_svd_mlp_ranks(p, p, p, p, p, p, p, None, None, p, 4, 16, 32, 8, 16, 8, 1, 1, 0x20, p, 1 << 20,
+                                    None) == _lib.SVDMLP_EINVAL
+    assert b"unsupported flags" in lib.svdmlp_last_error()
+    assert lib.svdmlp_svd_mlp_block_ranks(p, p, ctypes.c_float(0.0), p, p, p, p, p, p, None, None, ctypes.c_void_p(512),
+                                          4, 16, 32, 8, 16, 8, 1, 1, 0, p, 1 << 20, None) == _lib.SVDMLP_EINVAL
+    assert b"eps" in lib.svdmlp_last_error()
 
 
 def test_check_maps_status_to_exceptions(lib):

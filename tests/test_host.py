@@ -200,6 +200,29 @@ def test_stack_rank_padding_is_exact():
                                O.fused_xuv_ref(x.numpy(), u.numpy(), v.numpy()), rtol=1e-6, atol=1e-6)
 
 
+def test_pad_rank_fp8_and_branches():
+    """fp8 factors pad with zero data (and unit U scales): the dequantized
+    product is unchanged; _pad_branches brings gate and up to one rank."""
+    import torch
+
+    from svdmlp import fp8, ops
+
+    g = torch.Generator().manual_seed(1)
+    u = fp8.quantize_per_channel(torch.randn(16, 6, generator=g) / 4)
+    v = fp8.quantize_per_channel(torch.randn(6, 12, generator=g) / 4)
+    up, vp = ops.pad_rank(ops.QuantizedFactor(u.data, u.scale), ops.QuantizedFactor(v.data, v.scale), 10)
+    assert up.shape == (16, 10) and vp.shape == (10, 12) and up.data.dtype == u.data.dtype
+    assert torch.equal(up.data[:, :6].view(torch.uint8), u.data.view(torch.uint8))
+    assert not up.data[:, 6:].view(torch.uint8).any() and not vp.data[6:].view(torch.uint8).any()
+    assert torch.equal(up.scale[6:], torch.ones(4)) and torch.equal(vp.scale, v.scale)
+    torch.testing.assert_close(up.dequantize() @ vp.dequantize(),
+                               ops.QuantizedFactor(u.data, u.scale).dequantize() @ ops.QuantizedFactor(v.data, v.scale).dequantize())
+    ug, vg, uu, vu = (torch.randn(16, 6), torch.randn(6, 12), torch.randn(16, 9), torch.randn(9, 12))
+    pg, pvg, pu, pvu = ops._pad_branches(ug, vg, uu, vu)
+    assert pg.shape == pu.shape == (16, 9) and pvg.shape == pvu.shape == (9, 12)
+    assert pu is uu and pvu is vu   # the larger branch is passed through
+
+
 def test_stack_flops_uses_drawn_ranks():
     from svdmlp import stack
 
