@@ -182,6 +182,9 @@ struct Ws {
 };
 
 int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch);
+// Tile (columns / 32) and K splits of the split gate/up XU.V passes at one or
+// two row tiles of tokens; *splits = 0 where the passes are not split.
+void gu_split_plan(int64_t T, int64_t ff, int* fn, int* splits);
 
 // Bytes of split-K partial slices for any call with ranks <= r: the
 // large-tile stages X.U (gate/up, batch 2), h.Ud and XU.V (both output
@@ -212,8 +215,11 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
     }
     if (rr == r) break;
   }
-  // gate/up XU.V passes at one or two row tiles split K in two (big_swiglu)
-  if (T <= 512) part = std::max(part, (int64_t)2 * ((T + 255) / 256 * 256) * ((ff + 255) / 256 * 256) * 4);
+  // split gate/up XU.V passes at one or two row tiles (big_swiglu)
+  int gfn = 0, gsp = 0;
+  gu_split_plan(T, ff, &gfn, &gsp);
+  if (gsp >= 2)
+    part = std::max(part, (int64_t)gsp * ((T + 255) / 256 * 256) * ((ff + 32 * gfn - 1) / (32 * gfn) * (32 * gfn)) * 4);
   std::lock_guard<std::mutex> lk(mu);
   if (memo.size() > 4096) memo.clear();
   memo[key] = part;
@@ -407,7 +413,34 @@ struct Tune {
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
   int nw = 8;          // waves per block of the fn-8 X.U and XU.V stages (8, or 4: faster in isolation, not in the layer)
   bool contract = true; // contracted decode layer by default where it is the fastest (kDlContractAuto*)
+  int gusfn = 0;       // split gate/up XU.V passes at one row tile: tile columns / 32 (0: 4)
+  int gusp = 0;        // ... and their K splits (0: CUs / tiles, at most 4)
 };
+
+const Tune& tune();
+
+// One row tile of 256 x 128 tiles: each block streams its whole V column
+// panel, so the passes run at the panel's stream rate per block (8B layer,
+// T=256: 62 us for the g pass); K splits put more blocks on the V stream, as
+// many as fill the CUs, 2 to 4 (8B, 112 column tiles: 2 splits, the layer
+// 230 -> 194 us at T=256; 3B shape, ff=8192, 64 tiles: 4 splits, 141.2 ->
+// 134.4 us; 256 x 256 tiles in 8 splits there 151.7 us, and for the 8B
+// shape in 4 splits 194.8 -> 192.6 at T=256, no gain at T=160).  Two nearly
+// full row tiles (448 < T <= 512): 256 x 256 tiles (whole 512-byte V rows
+// per DMA instruction) in two splits (8B: T=512 261 -> 249 us; 3B: 167.3 us,
+// against 175.0 with four splits that fill the CUs); with a mostly padded
+// second row tile the split costs more than it gains (T=320: 208 -> 224,
+// T=384: 221 -> 233 us).  The fp32 slices are summed into g (fragment order)
+// and, with SiLU(g) applied, into h.
+void gu_split_plan(int64_t T, int64_t ff, int* fn, int* splits) {
+  const bool one = T <= 256, two = T > 448 && T <= 512 && ff % 256 == 0;
+  *fn = one ? (tune().gusfn ? tune().gusfn : 4) : 8;
+  *splits = 0;
+  if (!(one || two) || !tune().gusplit || ff % 128) return;
+  const int64_t tiles = (one ? 1 : 2) * ((ff + 32 * *fn - 1) / (32 * *fn));
+  const int64_t s = tune().gusp ? tune().gusp : (one ? std::min<int64_t>(4, tune().split / std::max<int64_t>(1, tiles)) : 2);
+  *splits = s >= 2 ? (int)s : 0;
+}
 
 const Tune& tune() {
   static const Tune t = [] {
@@ -432,6 +465,8 @@ const Tune& tune() {
         if (k == "big") r.big = v != 0;
         if (k == "dlayer") r.dlayer = v != 0;
         if (k == "contract") r.contract = v != 0;
+        if (k == "gusfn") r.gusfn = v;
+        if (k == "gusp") r.gusp = v;
         if (k == "gusplit") r.gusplit = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
@@ -682,23 +717,14 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   const int64_t ldb = v_lin ? r : (ldv ? ldv : ff), ldb_u = v_lin ? r_u : (ldv_u ? ldv_u : ldb);
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? ff : r) * ldb * wbytes(c);
   const int64_t xuu_bytes = (int64_t)T * r_u * 2, vu_bytes = (int64_t)(v_lin ? ff : r_u) * ldb_u * wbytes(c);
-  // One row tile of 256 x 128 tiles: each block streams its whole V column
-  // panel, so the passes run at the panel's stream rate per block (8B layer,
-  // T=256: 62 us for the g pass); two K splits put twice the blocks on the
-  // V stream, and the fp32 slices are summed into g (fragment order) and,
-  // with SiLU(g) applied, into h.
-  // Two nearly full row tiles (448 < T <= 512): 256 x 256 tiles (whole
-  // 512-byte V rows per DMA instruction) in the same 224 blocks, each
-  // streaming half of K (T=512: 261 -> 249 us); with a mostly padded second
-  // row tile the padding costs more than the split gains (T=320: 208 -> 224,
-  // T=384: 221 -> 233 us).
-  const int sfn = T <= 256 ? 4 : 8;
+  // At one or two row tiles of tokens the passes split K (gu_split_plan).
+  int sfn = 0, nsp = 0;
+  gu_split_plan(T, ff, &sfn, &nsp);
   const int64_t per = (int64_t)((T + 255) / 256 * 256) * ((ff + 32 * sfn - 1) / (32 * sfn) * (32 * sfn));
-  if ((T <= 256 || (T > 448 && T <= 512 && ff % 256 == 0)) && fn == 4 && r >= 64 && r_u >= 64 && tune().gusplit &&
-      2 * per * 4 <= part_cap) {
+  if (nsp >= 2 && fn == 4 && r >= 32 * nsp && r_u >= 32 * nsp && nsp * per * 4 <= part_cap) {
     fn = sfn;
-    const int ks = (r / 2 + 31) / 32 * 32, splits = (r + ks - 1) / ks;
-    const int ks_u = (r_u / 2 + 31) / 32 * 32, splits_u = (r_u + ks_u - 1) / ks_u;
+    const int ks = (r / nsp + 31) / 32 * 32, splits = (r + ks - 1) / ks;
+    const int ks_u = (r_u / nsp + 31) / 32 * 32, splits_u = (r_u + ks_u - 1) / ks_u;
     int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
                       BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
     if (rc) return rc;
