@@ -14,6 +14,8 @@ hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
   return hipGetLastError();
 }
 
+// 256 x 128 tiles with natural-layout bf16 B keep 6 LDS stages (8 KB of B
+// each in 256-byte rows), the others 4.
 template <int FN, int EPI, bool F32 = false>
 hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st) {
   if constexpr (FN == 8 && EPI == BEPI_STORE) {  // 4-wave instances: natural layout, STORE
@@ -22,7 +24,7 @@ hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hip
                    : go<FN, false, EPI, F32, false, 4>(p, splits, batch, st);
   }
   if (d.fp8) return go<FN, false, EPI, F32, true>(p, splits, batch, st);  // fp8 B: natural layout only
-  return d.b_kc ? go<FN, true, EPI, F32>(p, splits, batch, st) : go<FN, false, EPI, F32>(p, splits, batch, st);
+  return d.b_kc ? go<FN, true, EPI, F32>(p, splits, batch, st) : go<FN, false, EPI, F32, false, 8, FN == 4 ? 6 : 4>(p, splits, batch, st);
 }
 
 // FN 6 (256 x 192 tiles, the rank stages' X.U products) has the store

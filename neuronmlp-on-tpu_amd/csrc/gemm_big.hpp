@@ -17,8 +17,10 @@
 //    XOR-swizzled by (row >> 1) & 3; an MFMA fragment is one ds_read_b128
 //    and each 8-lane group of a read touches all 32 banks once.
 //  * B in the reference's natural (in, out) layout (N contiguous): stored
-//    as it lies in HBM, one 512-byte row per k, its 32-byte units
-//    XOR-swizzled by (k & 3) | ((k >> 3) & 1) << 2.  A fragment (16 columns
+//    as it lies in HBM, one 512-byte row per k (256 bytes for tiles of at
+//    most 128 columns, so no DMA lane fetches past the tile and the freed
+//    LDS holds more stages), its 32-byte units XOR-swizzled by k & 3: the
+//    four rows a transposing read touches land on distinct banks.  A fragment (16 columns
 //    x 8 k) is two ds_read_b64_tr_b16: in each 16-lane group, lane i
 //    receives element i % 4 of the 8-byte pieces addressed by lanes
 //    i/4 + 4j, so pointing lane s at row k + s/4, columns n + 4*(s % 4)
@@ -193,13 +195,14 @@ struct BigCfg {
   static constexpr int BM = 256, BN = 32 * FN, BK = 32;  // BK per stage
   static constexpr int STAGES = NS_;  // LDS stages: NS-2 in flight while one is read
   static constexpr int A_BYTES = BM * 64;                      // 16 KB
-  static constexpr int B_PITCH = FP8_B ? 256 : 512;
-  static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (fp8: 8 KB; Linear: rows >= BN read zeros)
+  // natural-layout B row per k: 256 bytes for fp8 and for bf16 tiles of at most 128 columns, else 512
+  static constexpr int B_PITCH = (FP8_B || (!B_KC && BN <= 128)) ? 256 : 512;
+  static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (256-byte rows: 8 KB; Linear: rows >= BN read zeros)
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_UNITS = A_BYTES / 1024 / NW;  // DMA instructions per wave: 2 (NW 4: 4)
-  static constexpr int B_UNITS = B_BYTES / 1024 / NW;  // 2 (fp8: 1); NW 4: 4 (fp8: 2)
+  static constexpr int B_UNITS = B_BYTES / 1024 / NW;  // 2 (256-byte rows: 1); NW 4: 4 (2)
   static_assert(NW == 8 || NW == 4, "8 or 4 waves");
-  static_assert(A_UNITS * NW == 16 && B_UNITS * NW == (FP8_B ? 8 : 16), "DMA instructions per wave and stage");
+  static_assert(A_UNITS * NW == 16 && B_UNITS * NW * 1024 == B_BYTES, "DMA instructions per wave and stage");
   static_assert(!(FP8_B && B_KC), "fp8 B is read in natural layout only");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
   static_assert(B_KC ? BN <= 256 : true, "Linear-layout B tile holds at most 256 rows");
@@ -291,12 +294,15 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * (uint32_t)ldb + (uint32_t)(n0 + col) : kOOB;
     }
   } else {
-    const int kk = 2 * wave + (lane >> 5);
-    const int q = lane & 31;
+    // instruction i fills RPI k-rows from RPI * (wave + NW * i), LPR lanes per
+    // row (512-byte rows: 2 rows of 32 lanes; 256-byte rows: 4 of 16)
+    constexpr int RPI = 1024 / C::B_PITCH, LPR = C::B_PITCH / 16;
+    const int kk = RPI * wave + lane / LPR;
+    const int q = lane % LPR;
     const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
 #pragma unroll
     for (int i = 0; i < C::B_UNITS; ++i)
-      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)(kk + 2 * NW * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)(kk + RPI * NW * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
   }
 
   // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
