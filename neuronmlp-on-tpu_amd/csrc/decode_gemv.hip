@@ -36,12 +36,15 @@ int resident(const void* k) {
 }  // namespace
 
 int gemv_layer_grid(int rw) {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  const void* k = rw == 1 ? reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 1>)
-                          : reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 2>);
-  return resident(k) >= 1 ? std::min(cus, kDlMaxGrid) : 0;
+  auto compute = [rw]() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    const void* k = rw == 1 ? reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 1>)
+                            : reinterpret_cast<const void*>(&gemv_layer_kernel<kGvMaxT, 2>);
+    return resident(k) >= 1 ? std::min(cus, kDlMaxGrid) : 0;
+  };
+  return cached_per_device(rw == 1 ? DC_GV1 : DC_GV2, compute);
 }
 
 int gemv_layer_a_floats() { return kGvAFloats; }

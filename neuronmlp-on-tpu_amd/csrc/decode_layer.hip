@@ -34,21 +34,26 @@ int blocks_per_cu() {
 
 int decode_layer_mt(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : (T <= 64 ? 4 : 8)); }
 
-int decode_layer_grid(int mt) {
+namespace {
+
+template <int MT, bool CONTRACT = false>
+int grid_of() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  const int per = mt == 1 ? blocks_per_cu<1>()
-                  : (mt == 2 ? blocks_per_cu<2>() : (mt == 4 ? blocks_per_cu<4>() : blocks_per_cu<8>()));
-  return per >= 1 ? std::min(cus, kDlMaxGrid) : 0;
+  return blocks_per_cu<MT, CONTRACT>() >= 1 ? std::min(cus, kDlMaxGrid) : 0;
 }
 
-int decode_layer_contract_grid() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  return blocks_per_cu<1, true>() >= 1 ? std::min(cus, kDlMaxGrid) : 0;
+}  // namespace
+
+int decode_layer_grid(int mt) {
+  if (mt == 1) return cached_per_device(DC_DL1, grid_of<1>);
+  if (mt == 2) return cached_per_device(DC_DL2, grid_of<2>);
+  if (mt == 4) return cached_per_device(DC_DL4, grid_of<4>);
+  return cached_per_device(DC_DL8, grid_of<8>);
 }
+
+int decode_layer_contract_grid() { return cached_per_device(DC_DL_CONTRACT, grid_of<1, true>); }
 
 hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStream_t st, const char** why,
                                bool contract) {

@@ -3,6 +3,8 @@
 // requested combination has no compiled instance.
 #pragma once
 
+#include <atomic>
+
 #include "decode.hpp"
 
 namespace svdmlp {
@@ -88,6 +90,23 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
                                    int batch, hipStream_t st, const uint16_t* gate = nullptr);
 hipError_t launch_finalize(const float* g, const float* u, int64_t ldi, uint16_t* out, int64_t ldo, int rows,
                            int cols, bool swiglu, bool out_t, hipStream_t st);
+
+// A per-device constant (a persistent kernel's grid size) computed once per
+// device and slot: the lookups behind it (device attributes, occupancy) cost
+// host time on every decode call otherwise.
+enum DeviceConst : int { DC_DL1 = 0, DC_DL2, DC_DL4, DC_DL8, DC_DL_CONTRACT, DC_GV1, DC_GV2, DC_COUNT };
+template <class F>
+inline int cached_per_device(int slot, F compute) {
+  static std::atomic<int> cache[64][DC_COUNT];  // value + 1; 0 = not yet computed
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return compute();
+  int v = cache[dev][slot].load(std::memory_order_relaxed);
+  if (v == 0) {
+    v = compute() + 1;
+    cache[dev][slot].store(v, std::memory_order_relaxed);
+  }
+  return v - 1;
+}
 
 inline hipError_t gemm_launch(const GemmDesc& d, const GemmParams& p, int splits, int batch, hipStream_t st,
                               const char** why) {
