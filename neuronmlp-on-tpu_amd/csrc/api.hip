@@ -887,6 +887,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.slices = reinterpret_cast<float*>(ws + L.slices);
   p.cslices = contract ? reinterpret_cast<float*>(ws + L.cslices) : nullptr;
   p.sync = reinterpret_cast<uint64_t*>(ws + L.sync);
+  p.a_cached = ((uintptr_t)ws & 127u) == 0;
   p.T = (int)T;
   p.d = (int)d;
   p.ff = (int)ff;

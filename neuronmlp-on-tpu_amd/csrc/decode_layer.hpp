@@ -30,12 +30,20 @@
 //  * before waiting at a barrier, every block already issues the weight DMAs
 //    of its first stages of the next phase (weights do not depend on the
 //    barrier), so barrier latency overlaps the weight stream.
-// Data crosses blocks only through device-coherent accesses: device-scope
-// (sc1) stores and loads (slices, bf16 tiles, the activation DMAs) and the
-// counters' atomics.  Each wave waits for
-// its own writes (vmcnt(0)) before its block arrives at a barrier, so the
-// barriers need no cache write-back or invalidation (with agent-scope fences
-// a barrier costs ~9 us, without ~2 us).
+// Data crosses blocks through device-scope (sc1) stores (slices, bf16
+// tiles), device-scope loads (slices) and the counters' atomics.  Each wave
+// waits for its own writes (vmcnt(0)) before its block arrives at a barrier,
+// so the barriers need no cache write-back or invalidation (with agent-scope
+// fences a barrier costs ~9 us, without ~2 us).  The bf16 activation tiles
+// (XU, h, XU_d) are read back through the caches (plain DMAs) when the
+// workspace is 128-byte aligned: every 128-byte line of them has one writing
+// block, no CU reads a line of them in a launch before the barrier that
+// follows its write (so no cache holds a copy older than the write from this
+// launch), and copies from earlier launches are not served (a kernel sees
+// the writes of the kernels before it, which needs exactly that).  One copy
+// per XCD's L2 then serves its CUs: 8B layer at 32 tokens 82.9 -> 78.4 us.
+// With a workspace aligned to less, lines could have two writers, and the
+// activation DMAs stay device-scope.
 // Grid barriers are two-level: blocks arrive on one of 16 group counters,
 // the last of a group arrives on a root counter, and the last root arrival
 // advances a generation word that every block polls (a single counter for
@@ -78,6 +86,7 @@ struct DecLayerParams {
   int units1, units2, units3, units4;  // tiles x splits
   int splits1, splits3, splits4;       // splits per tile, phases 1, 3 and 4
   int ld_u, ld_v, ld_ud, ld_vd;        // row pitch (elements) of ug and uu, vg and vu, ud, vd
+  int a_cached;                        // activation DMAs through the caches (workspace 128-byte aligned)
 };
 
 constexpr int kDlThreads = 512;
@@ -128,21 +137,34 @@ __device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcn
 // done bit), waits for both to complete, and sets *bad (LDS) for the block;
 // *bad is never cleared within a launch.  (Polling the root counter itself,
 // one atomic hop shorter, was ~2.4 us slower per layer: the polls then share
-// a line with the group completions' atomics.)
+// a line with the group completions' atomics.)  `pre_w0`, run by the whole
+// of wave 0 between its arrival and its first poll, issues that wave's
+// share of the next phase's weight DMAs: issued before the arrival, the
+// arrival atomic's return would wait for them.
+struct DlNoPre {
+  __device__ void operator()() const {}
+};
+template <class Pre = DlNoPre>
 __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k, uint32_t spin_reg,
-                                             const uint32_t* spin_lds, int* bad) {
+                                             const uint32_t* spin_lds, int* bad, const Pre& pre_w0 = Pre{}) {
   dl_block_sync();
-  if (threadIdx.x == 0) {
-    const uint32_t G = gridDim.x, b = blockIdx.x;
-    const uint32_t g = b % kDlGroups;
-    const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
-    const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
-    const uint64_t a = __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((a + 1) % gsize == 0) {
-      const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((r + 1) % ngroups == 0)
-        __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x < 64) {
+    if (threadIdx.x == 0) {
+      const uint32_t G = gridDim.x, b = blockIdx.x;
+      const uint32_t g = b % kDlGroups;
+      const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
+      const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
+      const uint64_t a =
+          __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((a + 1) % gsize == 0) {
+        const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((r + 1) % ngroups == 0)
+          __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
+    pre_w0();
+  }
+  if (threadIdx.x == 0) {
     const uint32_t spin = spin_lds ? *spin_lds : spin_reg;
     uint32_t polls = 0;
     while ((int64_t)(__hip_atomic_load(&sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - gen0 - k) < 0) {
@@ -231,6 +253,7 @@ struct DlCtx {
   uint32_t lbase;  // LDS byte address of the block's array
   lds_cptr l0;
   int wave, lane, lr, lg, T;
+  int a_cached;  // DecLayerParams::a_cached
 };
 
 // Weight DMA of stage j into ring slot `slot` (one instruction per wave):
@@ -279,7 +302,11 @@ __device__ __forceinline__ void dl_dma_a(const DlCtx& c, const DlUnit& U, int j,
         const int lchunk = (c.lane & 3) ^ a_swz(row);
         const uint32_t voff = row < c.T ? (uint32_t)row * (uint32_t)U.lda * 2u + (uint32_t)lchunk * 16u : kOOB;
         const uint32_t soff = live ? (uint32_t)k0 * 2u : 0u;
-        dma16_dev(rs, voff, soff, c.lbase + L::A_OFF + slot * L::A_SLOT + kc * L::A_CHUNK + br * S::A_SUB + qq * 1024);
+        const uint32_t dst = c.lbase + L::A_OFF + slot * L::A_SLOT + kc * L::A_CHUNK + br * S::A_SUB + qq * 1024;
+        if (c.a_cached)
+          dma16(rs, voff, soff, dst);
+        else
+          dma16_dev(rs, voff, soff, dst);
       } else {
         dma16_dev(make_rsrc_sgpr(U.a0, 0u), kOOB, 0u, c.lbase + L::DUMMY_OFF);
       }
@@ -310,10 +337,9 @@ struct DlNoRunOut {
 };
 
 // Runs one unit: returns the accumulators (lane: D[n = 4*lg + t][m = lr] of
-// each 16-row block mt).  `prefetched`: waves 1..7 already issued their
-// weight DMAs of stages 0..NS-2 (before the grid barrier); wave 0 issues
-// its own here, ahead of the activation DMAs, keeping every wave's order
-// W(0..NS-2), A(0..NS-2), then (W, A) per step.  Otherwise the first
+// each 16-row block mt).  `prefetched`: every wave already issued its
+// weight DMAs of stages 0..NS-2 (at the grid barrier), so every wave's order
+// is W(0..NS-2), A(0..NS-2), then (W, A) per step.  Otherwise the first
 // stages go out as (W, A) pairs, so stage 0 is usable as soon as its own
 // pair lands rather than after every CU's whole first burst (8B layer: T=8
 // 74.6 -> 72.0 us, T=64 103.7 -> 102.7 us), and every wait is the steady
@@ -336,8 +362,6 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
       dl_dma_a<MT, DUAL>(c, U, s, s);
     }
   } else {
-    if (c.wave == 0)
-      for (int s = 0; s < NS - 1; ++s) dl_dma_w<MT, DUAL>(c, U, s, s);
     for (int s = 0; s < NS - 1; ++s) dl_dma_a<MT, DUAL>(c, U, s, s);
   }
 
@@ -711,6 +735,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   c.lr = c.lane & 15;
   c.lg = c.lane >> 4;
   c.T = p.T;
+  c.a_cached = p.a_cached;
   int* const flag = reinterpret_cast<int*>(lds + L::FLAG_OFF);
   int* const bad = reinterpret_cast<int*>(lds + L::BAD_OFF);
   uint32_t* const spin_lds = MT >= 4 ? reinterpret_cast<uint32_t*>(lds + L::SPIN_OFF) : nullptr;
@@ -788,10 +813,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     }
   };
   const int units[5] = {0, p.units1, p.units2, p.units3, p.units4};
-  // Waves 1..7 issue the first weight stages of this block's first unit of
-  // `phase` (wave 0 issues its share after the barrier).
-  auto prefetch = [&](int phase) {
-    if (b < units[phase] && c.wave != 0) {
+  // The first NS - 1 weight stages of this block's first unit of `phase`,
+  // issued at the barrier ahead of it: waves 1..7 before their arrival
+  // (prefetch), wave 0 after it (grid_sync).
+  auto prefetch_w = [&](int phase) {
+    if (b < units[phase]) {
       DlUnit U;
       unit_of(phase, b, U);
       for (int s = 0; s < NS - 1; ++s) {
@@ -801,6 +827,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
           dl_dma_w<MT, false>(c, U, s, s);
       }
     }
+  };
+  auto prefetch = [&](int phase) {
+    if (c.wave != 0) prefetch_w(phase);
+  };
+  auto grid_sync = [&](int next_phase) {
+    dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] { prefetch_w(next_phase); });
   };
 
   const int nt1 = 2 * (p.r_gu / 128), nt3 = p.r_d / 128, nt4 = p.d / 128;
@@ -816,7 +848,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(2);
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
+  grid_sync(2);
 
   if constexpr (CONTRACT) {
     // ---- phases 2 and 3 contracted: unit b < units2 keeps its h strip in
@@ -839,7 +871,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     }
     dl_wait_vm<0>();
     prefetch(4);
-    dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
+    grid_sync(4);
   } else {
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
   for (int u = b; u < units[2]; u += G) {
@@ -871,7 +903,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(3);
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
+  grid_sync(3);
 
   // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
   for (int u = b; u < units[3]; u += G) {
@@ -884,7 +916,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   prefetch(4);
-  dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad);
+  grid_sync(4);
   }
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----

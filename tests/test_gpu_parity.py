@@ -363,6 +363,35 @@ def test_replay_is_bitwise_identical(gpu, layer8b, T, padded):
     assert _rel(_np(ys[0])[: min(T, 16)], O.svd_mlp_ref(_np(xt)[: min(T, 16)], *f, dtype="bfloat16")) < BF16_TOL
 
 
+@pytest.mark.parametrize("T,padded", [(1, True), (3, False), (8, False), (40, False), (100, True)])
+def test_decode_activation_reads_through_the_caches(gpu, T, padded):
+    """The MFMA decode layers (contracted at 1 and 3 tokens) read the bf16
+    activation tiles that other blocks of the same launch wrote (XU, h, XU_d)
+    through the caches when the workspace is 128-byte aligned, device-scope
+    when it is not.  On a layer small enough (3 MB of factors) that its lines
+    stay in the L2s from one launch to the next, calls that alternate three
+    inputs on one aligned workspace give, call after call, the bits of the
+    device-scope reads of a workspace 16 bytes off alignment: no launch is
+    served a line that an earlier launch cached."""
+    shape = inputs.LayerShape(512, 1024, 384)
+    _, f = inputs.make_layer(shape, T=T, seed=61)
+    fb = _rounded(f, torch.bfloat16)
+    ft = [_to(a, torch.bfloat16, gpu) for a in fb]
+    fs = [ops.pad_rows(a, 64) if padded and i % 2 else a for i, a in enumerate(ft)]
+    xs = [_to(_x(T, shape.d, 70 + i), torch.bfloat16, gpu) for i in range(3)]
+    nb = ops.svd_mlp_workspace(xs[0], r=shape.r, ff=shape.ff).numel()
+    aligned = torch.zeros(nb, dtype=torch.uint8, device=gpu)
+    off = torch.zeros(nb + 16, dtype=torch.uint8, device=gpu)[16:]
+    assert aligned.data_ptr() % 128 == 0 and off.data_ptr() % 128 == 16
+    refs = [ops.svd_mlp(x, *fs, workspace=off).clone() for x in xs]
+    for x, y in zip(xs, refs):
+        assert _rel(_np(y), O.svd_mlp_ref(_np(x), *fb, dtype="bfloat16")) < BF16_TOL
+    for i in range(30):
+        y = ops.svd_mlp(xs[i % 3], *fs, workspace=aligned)
+        assert torch.equal(y.view(torch.int16), refs[i % 3].view(torch.int16)), (T, i)
+    assert _barrier_state(aligned)[1] == 0 and _barrier_state(off)[1] == 0
+
+
 @pytest.mark.parametrize("shape,T,contracted", [
     (inputs.LayerShape(1024, 2048, 512), 8, False),        # MFMA decode layer
     (inputs.LayerShape(1040, 2064, 400, 272), 1, False),   # streaming-GEMV layer
