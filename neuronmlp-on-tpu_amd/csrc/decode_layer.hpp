@@ -96,11 +96,16 @@ constexpr int kDlMaxGrid = 256;
 constexpr int kDlWStage = 8192;    // 32 k x 128 columns bf16
 // Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
 // weight bytes per block barrier) and the ring holds NS stages, as far as
-// the activation tile, which shares the ring, leaves room.
+// the activation tile, which shares the ring, leaves room.  From 2 tiles up
+// the k loop is bound by its per-stage chain (wait, block barrier, LDS
+// fragment reads, MFMAs) rather than by the bytes in flight: 8B layer at 64
+// tokens 101.4 us with (KC 1, NS 6), 95.8 with (2, 4), 102.6 with (3, 3);
+// at 32 tokens (2, 4) 78.8, (3, 4) 83.7, (2, 5) 79.4; at 128 tokens (1, 4)
+// 141.3, (2, 3) 143.1.
 template <int MT>
 struct DlDepth {
-  static constexpr int KC = MT >= 4 ? 1 : 2;
-  static constexpr int NS = MT == 2 || MT == 8 ? 4 : 6;
+  static constexpr int KC = MT == 8 ? 1 : 2;
+  static constexpr int NS = MT == 1 ? 6 : 4;
 };
 
 // fp32 -> bf16 round to nearest even in integer form (NaN stays NaN): the
