@@ -1,7 +1,12 @@
 // C ABI of libsvdmlp.so (declared in include/svdmlp.h).
 //
 // Kernel choice per call (svdmlp_svd_mlp and its variants):
-//   1-2 tokens, dense bf16 factors:  one streaming-GEMV layer launch
+//   1 token (padded V rows) or 1-3 (dense), bf16, aligned, or up to 4 on
+//   request (SVDMLP_CONTRACT):       the contracted decode layer
+//                                    (decode_layer.hpp): h kept in LDS, two
+//                                    grid barriers
+//   1-2 tokens, dense bf16 factors the contracted layer does not take:
+//                                    one streaming-GEMV layer launch
 //                                    (decode_gemv.hpp)
 //   1-128 tokens, bf16, aligned:     one persistent MFMA decode-layer launch
 //                                    (decode_layer.hpp): four phases, three

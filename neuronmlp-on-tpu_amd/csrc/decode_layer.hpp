@@ -27,9 +27,9 @@
 //    itself, so phases 2 to 4 stream bf16 activations and no barrier
 //    follows phase 4 (fp32 atomics onto shared sums cost ~20 us per phase at
 //    64 tokens);
-//  * before waiting at a barrier, every block already issues the weight DMAs
-//    of its first stages of the next phase (weights do not depend on the
-//    barrier), so barrier latency overlaps the weight stream.
+//  * at a barrier, once its arrival is counted, every block issues the
+//    weight DMAs of its first stages of the next phase (weights do not depend
+//    on the barrier), so barrier latency overlaps the weight stream.
 // Data crosses blocks through device-scope (sc1) stores (slices, bf16
 // tiles), device-scope loads (slices) and the counters' atomics.  Each wave
 // waits for its own writes (vmcnt(0)) before its block arrives at a barrier,
@@ -142,33 +142,33 @@ __device__ __forceinline__ void dl_block_sync() { asm volatile("s_waitcnt lgkmcn
 // done bit), waits for both to complete, and sets *bad (LDS) for the block;
 // *bad is never cleared within a launch.  (Polling the root counter itself,
 // one atomic hop shorter, was ~2.4 us slower per layer: the polls then share
-// a line with the group completions' atomics.)  `pre_w0`, run by the whole
-// of wave 0 between its arrival and its first poll, issues that wave's
-// share of the next phase's weight DMAs: issued before the arrival, the
-// arrival atomic's return would wait for them.
+// a line with the group completions' atomics.)  `pre`, run by every wave
+// once its block's arrival atomics have returned and before the first poll,
+// issues the wave's share of the next phase's first weight DMAs.  Issued
+// before the arrival, they delay it: the block's own 80 KB burst sits
+// ahead of its arrival atomic at the memory side (8B layer: T=1 70.0 ->
+// 68.6 us, T=8 72.0 -> 68.8 us).
 struct DlNoPre {
   __device__ void operator()() const {}
 };
 template <class Pre = DlNoPre>
 __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint32_t k, uint32_t spin_reg,
-                                             const uint32_t* spin_lds, int* bad, const Pre& pre_w0 = Pre{}) {
+                                             const uint32_t* spin_lds, int* bad, const Pre& pre = Pre{}) {
   dl_block_sync();
-  if (threadIdx.x < 64) {
-    if (threadIdx.x == 0) {
-      const uint32_t G = gridDim.x, b = blockIdx.x;
-      const uint32_t g = b % kDlGroups;
-      const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
-      const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
-      const uint64_t a =
-          __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((a + 1) % gsize == 0) {
-        const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((r + 1) % ngroups == 0)
-          __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+  if (threadIdx.x == 0) {
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t g = b % kDlGroups;
+    const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
+    const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
+    const uint64_t a = __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((a + 1) % gsize == 0) {
+      const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((r + 1) % ngroups == 0)
+        __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    pre_w0();
   }
+  dl_block_sync();
+  pre();
   if (threadIdx.x == 0) {
     const uint32_t spin = spin_lds ? *spin_lds : spin_reg;
     uint32_t polls = 0;
@@ -819,8 +819,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   };
   const int units[5] = {0, p.units1, p.units2, p.units3, p.units4};
   // The first NS - 1 weight stages of this block's first unit of `phase`,
-  // issued at the barrier ahead of it: waves 1..7 before their arrival
-  // (prefetch), wave 0 after it (grid_sync).
+  // issued at the barrier ahead of it, once the block has arrived.
   auto prefetch_w = [&](int phase) {
     if (b < units[phase]) {
       DlUnit U;
@@ -832,9 +831,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
           dl_dma_w<MT, false>(c, U, s, s);
       }
     }
-  };
-  auto prefetch = [&](int phase) {
-    if (c.wave != 0) prefetch_w(phase);
   };
   auto grid_sync = [&](int next_phase) {
     dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] { prefetch_w(next_phase); });
@@ -852,7 +848,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
                    false, p.sync);
   }
   dl_wait_vm<0>();
-  prefetch(2);
   grid_sync(2);
 
   if constexpr (CONTRACT) {
@@ -875,7 +870,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       dl_contract_combine<MT>(c, p, lds, b - U2, U2, nt1, spin, spin_lds, bad);
     }
     dl_wait_vm<0>();
-    prefetch(4);
     grid_sync(4);
   } else {
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
@@ -907,7 +901,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     dl_block_sync();
   }
   dl_wait_vm<0>();
-  prefetch(3);
   grid_sync(3);
 
   // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
@@ -920,7 +913,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
                    false, false, p.sync);
   }
   dl_wait_vm<0>();
-  prefetch(4);
   grid_sync(4);
   }
 
