@@ -13,7 +13,8 @@ The JSON line also carries:
                 algorithmic FLOP per launch / average launch duration vs the
                 2.5 PFLOP/s bf16 MFMA peak
   decode        T = 1, 8, 32, 64 decode layers: us/layer
-                and GB/s of compulsory bytes vs the 8 TB/s HBM peak
+                and GB/s of compulsory bytes vs the 8 TB/s HBM peak; block_us
+                is the MLP block (RMSNorm, layer, residual) at the same T
   cpu_baseline  the numpy oracle (oracle/reference_cpu.py) timed on this
                 host's cores on a bounded row sample of the same layer
 
@@ -206,6 +207,13 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
             svdmlp.svd_mlp(xd, *layers[i % len(layers)], workspace=wsd, out=outd)
 
         msd, _ = _time_steps(torch, dstep, args.decode_steps, max(10, args.warmup), stream)
+        # the MLP block around the layer (RMSNorm and residual inside the decode layer's launch)
+        gain = torch.ones(D, dtype=torch.float32, device=dev)
+
+        def bstep(i, xd=xd, wsd=wsd, outd=outd, gain=gain):
+            svdmlp.svd_mlp_block(xd, gain, *layers[i % len(layers)], workspace=wsd, out=outd)
+
+        msb, _ = _time_steps(torch, bstep, args.decode_steps, 10, stream)
         with _lib.StageProfile() as prof:
             _time_steps(torch, dstep, min(args.decode_steps, 50), 0, stream)
         nbytes = factor_bytes + 2 * Td * D * 2
@@ -226,6 +234,7 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
             "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),
             "stages_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in prof.result.items()},
             "kernel": kernel,
+            "block_us": round(msb * 1e3, 2),
         }
         if svdmlp.workspace_status(wsd):
             raise RuntimeError(f"decode T={Td}: a grid-barrier wait gave up (the device was shared?)")

@@ -152,7 +152,12 @@ int svdmlp_svd_mlp(const void* x, const void* ug, const void* vg, const void* uu
  * to the activation dtype) and the residual add rounded to the activation
  * dtype.  norm_w holds d fp32 gains; y must not alias x.  Replaces the MLP
  * half of bench/e2e_block.py:268-278 (_fused_svd_block) with LlamaRMSNorm,
- * models/modeling_llama.py:253-262.
+ * models/modeling_llama.py:253-262.  The persistent decode layers run the
+ * whole block in their one launch (a phase 0 writes RMSNorm(x), one block
+ * per token row, before the layer's first grid barrier; the last phase adds
+ * the residual as it writes y); the streaming-GEMV layer and the large-tile
+ * path add the residual in their output stage after a separate RMSNorm pass;
+ * the other paths run both as passes of their own.
  */
 int svdmlp_svd_mlp_block(const void* x, const float* norm_w, float eps, const void* ug, const void* vg,
                          const void* uu, const void* vu, const void* ud, const void* vd,

@@ -275,10 +275,22 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
+// The MLP block around a layer call (svdmlp_svd_mlp_block*): the kernels
+// that can take them apply the RMSNorm of x on the fly and the residual add
+// in their output stage, and record that they did.
+struct Block {
+  const void* x;  // block input: RMSNorm input and residual
+  const float* gain;
+  float eps;
+  bool norm_done = false;   // the layer's input is the normalised x
+  bool resid_done = false;  // y already holds x + MLP
+};
+
 struct Common {
   int act, wt;
   bool f32;
   hipStream_t st;
+  Block* blk = nullptr;
 };
 
 int check_types(int32_t act, int32_t wt) {
@@ -518,8 +530,9 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
-             int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr) {
+             int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr, const uint16_t* resid = nullptr) {
   BigParams p{};
+  p.resid = resid;
   p.gfrag = gfrag;
   p.out_frag = out_frag;
   const bool fp8 = c.wt == SVDMLP_FP8_E4M3;
@@ -762,19 +775,25 @@ int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T,
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? dout : r) * ldb * wbytes(c);
   const int ks = tune().s4 > 0 && tune().s4 != 8 ? r : plan_ksplit(T, r, dout, fn, 1);
   const int splits = (r + ks - 1) / ks;
-  if (splits == 1)
+  // the MLP block's residual add rides on the output store or the fragment-order reduction
+  const uint16_t* resid = c.blk ? static_cast<const uint16_t*>(c.blk->x) : nullptr;
+  if (splits == 1) {
+    if (c.blk) c.blk->resid_done = true;
     return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1,
-                    fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv);
+                    fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv, nullptr, 0, 0, nullptr, resid);
+  }
   float* part = reinterpret_cast<float*>(ws + L.part);
   const int nw = big_nw(fn, BEPI_STORE, v_lin);
   if (big_frag_reduce_ok(fn, nw)) {
+    if (c.blk) c.blk->resid_done = true;
     const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)dout + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
     int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1, fn,
                       BEPI_STORE, ks, part, dout, per, nullptr, true, per, sv, nullptr, 0, 1);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
     return check(launch_reduce_frag_bf16(part, splits, per, per, static_cast<uint16_t*>(y), dout, (int64_t)T * dout,
-                                         T, dout, (int)(tp / 256), (int)(np / (32 * fn)), fn, nw, 1, c.st),
+                                         T, dout, (int)(tp / 256), (int)(np / (32 * fn)), fn, nw, 1, c.st, nullptr,
+                                         resid),
                  "split-K reduce");
   }
   const int64_t slice = (int64_t)T * dout;
@@ -909,6 +928,25 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.ld_v = (int)ld.v;
   p.ld_ud = (int)ld.ud;
   p.ld_vd = (int)ld.vd;
+  if (c.blk) {
+    // The MLP block: the residual add in phase 4; the RMSNorm in the
+    // kernel's phase 0 (a block per token row, d <= 16384, 16-byte aligned
+    // gains), else as its own pass.
+    p.resid = c.blk->x;
+    c.blk->resid_done = true;
+    if (!c.blk->norm_done && d <= 8 * kDlThreads * kDlNormPieces && T <= grid && aligned16(c.blk->gain)) {
+      p.gain = c.blk->gain;
+      p.eps = c.blk->eps;
+      p.xn = reinterpret_cast<uint16_t*>(ws + L.norm);
+      c.blk->norm_done = true;
+    } else if (!c.blk->norm_done) {
+      void* hn = ws + L.norm;
+      const int rc = check(launch_rmsnorm(c.blk->x, c.blk->gain, hn, T, d, c.blk->eps, true, c.st), "RMSNorm");
+      if (rc) return rc;
+      p.x = hn;
+      c.blk->norm_done = true;
+    }
+  }
   const char* why = nullptr;
   StageScope ss(contract ? ST_DEC_CONTRACT : ST_DEC_LAYER, c.st);
   return check(launch_decode_layer(p, mt, grid, c.st, &why, contract), "decode layer", why);
@@ -949,6 +987,10 @@ int gemv_layer(const Common& c, const void* x, const void* ug, const void* vg, c
   p.ud = static_cast<const uint16_t*>(ud);
   p.vd = static_cast<const uint16_t*>(vd);
   p.y = static_cast<uint16_t*>(y);
+  if (c.blk) {  // the MLP block (x already normalised): residual add in the output write
+    p.resid = static_cast<const uint16_t*>(c.blk->x);
+    c.blk->resid_done = true;
+  }
   p.xu32 = reinterpret_cast<float*>(ws + L.xu32);
   p.xd32 = p.xu32 + 2 * T * r_gu;
   p.gu32 = reinterpret_cast<float*>(ws + L.gu32);
@@ -1011,6 +1053,11 @@ int scratch_of_current_device(hipStream_t st, char** out) {
   *out = static_cast<char*>(g_scratch_ptr[dev]);
   return SVDMLP_OK;
 }
+
+int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, const void* vu, const void* ud,
+                const void* vd, const float* const* scales, const int64_t* ld_in, void* y, int64_t T, int64_t d,
+                int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                void* workspace, size_t ws_bytes, void* stream, Block* blk);
 
 }  // namespace
 
@@ -1076,11 +1123,11 @@ int svdmlp_svd_mlp_block_ranks(const void* x, const float* norm_w, float eps, co
   if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
   const bool bf16 = act_dtype == SVDMLP_BF16;
   hipStream_t st = (hipStream_t)stream;
-  void* h = static_cast<char*>(workspace) + L.norm;
-  if ((rc = check(launch_rmsnorm(x, norm_w, h, T, d, eps, bf16, st), "RMSNorm"))) return rc;
-  if ((rc = svdmlp_svd_mlp_ranks(h, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_g, r_u, r_d, act_dtype,
-                                 w_dtype, flags, workspace, ws_bytes, stream)))
+  Block blk{x, norm_w, eps};
+  if ((rc = svd_mlp_run(x, ug, vg, uu, vu, ud, vd, scales, ld, y, T, d, ff, r_g, r_u, r_d, act_dtype, w_dtype, flags,
+                        workspace, ws_bytes, stream, &blk)))
     return rc;
+  if (blk.resid_done) return SVDMLP_OK;
   return check(launch_residual_add(x, y, T * d, bf16, st), "residual add");
 }
 
@@ -1300,10 +1347,18 @@ int svdmlp_svd_mlp_ld(const void* x, const void* ug, const void* vg, const void*
                               w_dtype, flags, workspace, ws_bytes, stream);
 }
 
-int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
-                         const void* ud, const void* vd, const float* const* scales, const int64_t* ld_in, void* y,
-                         int64_t T, int64_t d, int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d, int32_t act_dtype,
-                         int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The layer (svdmlp_svd_mlp_ranks), or with `blk` the MLP block around it:
+// the kernel chosen for the shape applies the block's RMSNorm and residual
+// add where it can (the decode layers: both; the streaming-GEMV layer and
+// the large-tile path: the residual add), the rest run as their own passes.
+int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, const void* vu, const void* ud,
+                const void* vd, const float* const* scales, const int64_t* ld_in, void* y, int64_t T, int64_t d,
+                int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
+                void* workspace, size_t ws_bytes, void* stream, Block* blk) {
   g_err.clear();
   int rc = validate_dims(T, d, ff, std::min(std::min(r_g, r_u), r_d));
   if (rc) return rc;
@@ -1325,7 +1380,7 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
   const int64_t r = std::max(std::max(r_g, r_u), r_d);
   const Ws L = ws_layout(T, d, ff, r);
   if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
-  const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
+  const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream, blk};
   const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR;
   bool vec = d % 8 == 0 && ff % 8 == 0 && r_g % 8 == 0 && r_u % 8 == 0 && r_d % 8 == 0;
   for (const void* q : {x, ug, vg, uu, vu, ud, vd, (const void*)y, (const void*)workspace}) vec = vec && aligned16(q);
@@ -1354,6 +1409,15 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
     }
   }
   char* ws = static_cast<char*>(workspace);
+  // The MLP block on a path that does not fuse its RMSNorm: the RMSNorm pass
+  // into the workspace's norm region becomes the layer input.
+  auto normed = [&]() -> int {
+    if (!blk || blk->norm_done) return SVDMLP_OK;
+    void* hn = ws + L.norm;
+    blk->norm_done = true;
+    x = hn;
+    return check(launch_rmsnorm(blk->x, blk->gain, hn, T, d, blk->eps, act_dtype == SVDMLP_BF16, c.st), "RMSNorm");
+  };
   const float* S[6] = {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (fp8)
     for (int i = 0; i < 6; ++i) S[i] = scales[i];
@@ -1373,6 +1437,7 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
            (long long)r_g, (long long)r_u, (long long)kDecodeMaxT);
       return SVDMLP_EUNSUP;
     }
+    if ((rc = normed())) return rc;
     const void* us[2] = {ug, uu};
     const float* sus[2] = {S[0], S[2]};
     if ((rc = big_xu2(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, (int)T, (int)d, (int)r_g, (int)r_u, ws, L, sus,
@@ -1402,8 +1467,10 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
   const bool mfma_layer = decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld);
   if (mfma_layer && contract && decode_contract_ok(T, ff, r_gu, r_d, L, ws_bytes))
     return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld, true);
-  if (!(mfma_layer && !ld.dense) && gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld))
+  if (!(mfma_layer && !ld.dense) && gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld)) {
+    if ((rc = normed())) return rc;
     return gemv_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld);
+  }
   if (mfma_layer)
     return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld);
   const bool big = big_ok(c, vec, {T * d * 2, d * ld.u * 2, r_gu * ld.v * 2, T * ff * 2, ff * ld.ud * 2, r_d * ld.vd * 2},
@@ -1411,6 +1478,7 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
   if (!ld.dense && (T <= kDecodeMaxT || !big))
     return fail("factors with padded rows: no kernel takes this shape (the decode layers need d, ranks and ff in "
                 "multiples of 128, 128 and 64, the large-tile path more than %lld tokens)", (long long)kDecodeMaxT);
+  if ((rc = normed())) return rc;
 
   if (decode_ok(c, T, {d, ff, r_gu, r_d}, vec)) {
     float* xu32 = reinterpret_cast<float*>(ws + L.xu32);
@@ -1497,6 +1565,18 @@ int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const vo
   rc = prefill_xu(c, ah, true, ud1, fp8 ? sud : nullptr, u_lin, T, ff, r_d, 1, vec, ws, L, 2, &a_src, &xu, &xu_bs);
   if (rc) return rc;
   return prefill_v(c, a_src, xu, vd, S[5], v_lin, T, r_d, d, vec, y);
+}
+
+}  // namespace
+
+extern "C" {
+
+int svdmlp_svd_mlp_ranks(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
+                         const void* ud, const void* vd, const float* const* scales, const int64_t* ld_in, void* y,
+                         int64_t T, int64_t d, int64_t ff, int64_t r_g, int64_t r_u, int64_t r_d, int32_t act_dtype,
+                         int32_t w_dtype, uint32_t flags, void* workspace, size_t ws_bytes, void* stream) {
+  return svd_mlp_run(x, ug, vg, uu, vu, ud, vd, scales, ld_in, y, T, d, ff, r_g, r_u, r_d, act_dtype, w_dtype, flags,
+                     workspace, ws_bytes, stream, nullptr);
 }
 
 }  // extern "C"

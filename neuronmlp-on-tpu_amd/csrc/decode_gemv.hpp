@@ -42,6 +42,7 @@ struct GvParams {
   const uint16_t* ud;
   const uint16_t* vd;
   uint16_t* y;     // (T, d) bf16
+  const uint16_t* resid;  // MLP block: y = bf16(resid + bf16(MLP)) (row pitch d), else null
   float* xu32;     // (2, T, r_gu)
   float* gu32;     // (2, T, ff)
   float* xd32;     // (T, r_d)
@@ -392,7 +393,8 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
 #pragma unroll
   for (int u = 0; u < D; ++u) gv_wait<0>(ring[u]);
 
-  // ---- phase 5: the last block to finish phase 4 writes y = bf16(Y32) ----
+  // ---- phase 5: the last block to finish phase 4 writes y = bf16(Y32)
+  // (MLP block: y = bf16(resid + bf16(Y32))) ----
   // Every wave has waited for its own atomics; a block counts itself done
   // once all of its waves have.  A block whose barrier wait gave up set
   // kGvDoneBad before its own arrival, so the last arrival sees it and
@@ -421,7 +423,14 @@ __global__ __launch_bounds__(kGvThreads, 1) void gemv_layer_kernel(GvParams p) {
 #pragma unroll
       for (int q = 0; q < SB; ++q) {
         const int64_t i = i0 + q * kGvThreads;
-        if (i < n) reinterpret_cast<uint32_t*>(p.y)[i] = pack_bf16x2(__uint_as_float(v[q].x), __uint_as_float(v[q].y));
+        if (i >= n) continue;
+        uint32_t o = pack_bf16x2(__uint_as_float(v[q].x), __uint_as_float(v[q].y));
+        if (p.resid) {
+          const uint32_t xr = reinterpret_cast<const uint32_t*>(p.resid)[i];
+          o = pack_bf16x2(__uint_as_float(xr << 16) + __uint_as_float(o << 16),
+                          __uint_as_float(xr & 0xffff0000u) + __uint_as_float(o & 0xffff0000u));
+        }
+        reinterpret_cast<uint32_t*>(p.y)[i] = o;
       }
     }
   }

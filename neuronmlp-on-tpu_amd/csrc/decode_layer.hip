@@ -15,9 +15,13 @@ namespace svdmlp {
 
 namespace {
 
+// p.gain set: the MLP block's instance, whose phase 0 applies the RMSNorm.
 template <int MT, bool CONTRACT = false>
 hipError_t coop(const DecLayerParams& p, int grid, hipStream_t st) {
-  hipLaunchKernelGGL((decode_layer_kernel<MT, CONTRACT>), dim3(grid), dim3(kDlThreads), 0, st, p);
+  if (p.gain)
+    hipLaunchKernelGGL((decode_layer_kernel<MT, CONTRACT, true>), dim3(grid), dim3(kDlThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((decode_layer_kernel<MT, CONTRACT>), dim3(grid), dim3(kDlThreads), 0, st, p);
   return hipGetLastError();
 }
 
@@ -59,6 +63,10 @@ hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStr
                                bool contract) {
   if (grid <= 0) {
     *why = "decode layer: the kernel cannot be resident on this device";
+    return hipErrorInvalidValue;
+  }
+  if (p.gain && (p.d > 8 * kDlThreads * kDlNormPieces || p.T > grid || !p.xn || !p.resid)) {
+    *why = "decode layer: the RMSNorm instance takes d <= 16384, a block per token and the block's buffers";
     return hipErrorInvalidValue;
   }
   hipError_t e;

@@ -87,6 +87,13 @@ struct DecLayerParams {
   int splits1, splits3, splits4;       // splits per tile, phases 1, 3 and 4
   int ld_u, ld_v, ld_ud, ld_vd;        // row pitch (elements) of ug and uu, vg and vu, ud, vd
   int a_cached;                        // activation DMAs through the caches (workspace 128-byte aligned)
+  // MLP block (null otherwise): y = bf16(resid + bf16(MLP)); with `gain`
+  // (NORM instances) a phase 0 writes RMSNorm(x) to xn, which phase 1 reads
+  // instead of x.
+  const void* resid;  // (T, d) bf16, row pitch d
+  const float* gain;  // (d) fp32
+  uint16_t* xn;       // (T, d) bf16
+  float eps;
 };
 
 constexpr int kDlThreads = 512;
@@ -422,12 +429,13 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
 //    layer than the extra load.)
 // `out_y`: dst is the layer output; it receives NaN instead if this block
 // gave up a barrier wait (`bad`) or, after the last arrival, the timeout
-// flag is set.
+// flag is set.  With `resid` (the MLP block) it receives bf16(resid + the
+// bf16 MLP output), the residual add of the block.
 // Units of a split phase never exceed the grid (at most one per block).
 template <int MT>
 __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x4 (&acc)[MT], int u, int nt,
                                            int splits, uint32_t* cnt, float* slices, int* flag, uint16_t* dst,
-                                           bool out_y, bool bad, uint64_t* sync) {
+                                           bool out_y, bool bad, uint64_t* sync, const uint16_t* resid = nullptr) {
   const int n = U.n0 + 64 * (c.wave >> 2) + 16 * (c.wave & 3) + 4 * c.lg;
   bool poison = out_y && bad;
   if (splits > 1) {
@@ -493,10 +501,67 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = 16 * mt + c.lr;
-    if (m < c.T)
-      dl_store8(dst + (int64_t)m * U.ldo + n,
-                poison ? u32x2{kNaN2, kNaN2}
-                       : u32x2{dl_pack_bf16x2(acc[mt].x, acc[mt].y), dl_pack_bf16x2(acc[mt].z, acc[mt].w)});
+    if (m < c.T) {
+      u32x2 v = u32x2{dl_pack_bf16x2(acc[mt].x, acc[mt].y), dl_pack_bf16x2(acc[mt].z, acc[mt].w)};
+      if (resid && !poison) {
+        const u32x2 xr = *reinterpret_cast<const u32x2*>(resid + (int64_t)m * U.ldo + n);
+        v = u32x2{dl_pack_bf16x2(__uint_as_float(xr.x << 16) + __uint_as_float(v.x << 16),
+                                 __uint_as_float(xr.x & 0xffff0000u) + __uint_as_float(v.x & 0xffff0000u)),
+                  dl_pack_bf16x2(__uint_as_float(xr.y << 16) + __uint_as_float(v.y << 16),
+                                 __uint_as_float(xr.y & 0xffff0000u) + __uint_as_float(v.y & 0xffff0000u))};
+      }
+      dl_store8(dst + (int64_t)m * U.ldo + n, poison ? u32x2{kNaN2, kNaN2} : v);
+    }
+  }
+}
+
+// Phase 0 of the MLP block: row `row` of x normalised into xn,
+// bf16(gain * (x * rsqrt(mean(x^2) + eps))), LlamaRMSNorm's fp32 formula
+// (models/modeling_llama.py:257-262) rounded once.  Each thread holds 8
+// elements per 4096 (d <= 4096 * kDlNormPieces), the sum of squares is
+// reduced over the block in a fixed order (waves, then the 8 wave sums in
+// order, through `part` in LDS), and the row goes out with device-scope
+// stores, which phase 1 reads after the next grid barrier.
+constexpr int kDlNormPieces = 4;
+__device__ __forceinline__ void dl_norm_row(const DecLayerParams& p, char* part_lds, int row) {
+  const uint16_t* xr = static_cast<const uint16_t*>(p.x) + (int64_t)row * p.d;
+  u32x4 v[kDlNormPieces];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kDlNormPieces; ++i) {
+    const int e = 8 * ((int)threadIdx.x + kDlThreads * i);
+    v[i] = e < p.d ? *reinterpret_cast<const u32x4*>(xr + e) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = __uint_as_float(v[i][w] << 16), hi = __uint_as_float(v[i][w] & 0xffff0000u);
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  float* part = reinterpret_cast<float*>(part_lds);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  dl_block_sync();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kDlThreads / 64; ++w) tot += part[w];
+  const float rstd = 1.0f / sqrtf(tot / (float)p.d + p.eps);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(p.xn, 0, (int)((int64_t)p.T * p.d * 2), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < kDlNormPieces; ++i) {
+    const int e = 8 * ((int)threadIdx.x + kDlThreads * i);
+    if (e < p.d) {
+      const f32x4 g0 = *reinterpret_cast<const f32x4*>(p.gain + e), g1 = *reinterpret_cast<const f32x4*>(p.gain + e + 4);
+      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      u32x4 o;
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        o[w] = dl_pack_bf16x2(g[2 * w] * (__uint_as_float(v[i][w] << 16) * rstd),
+                              g[2 * w + 1] * (__uint_as_float(v[i][w] & 0xffff0000u) * rstd));
+      __builtin_amdgcn_raw_buffer_store_b128(o, rs, (uint32_t)(((int64_t)row * p.d + e) * 2), 0, kDlSc1);
+    }
   }
 }
 
@@ -728,7 +793,7 @@ __device__ __forceinline__ void dl_contract_combine(const DlCtx& c, const DecLay
   }
 }
 
-template <int MT, bool CONTRACT = false>
+template <int MT, bool CONTRACT = false, bool NORM = false>
 __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerParams p) {
   using L = DlLds<MT>;
   __shared__ __attribute__((aligned(1024))) char lds[L::BYTES];
@@ -762,7 +827,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     if (phase == 1) {
       const int per = p.r_gu / 128, nt = 2 * per;
       const int tile = u % nt, split = u / nt, br = tile / per;
-      U.a0 = U.a1 = p.x;
+      U.a0 = U.a1 = NORM ? static_cast<const void*>(p.xn) : p.x;
       U.lda = p.d;
       U.a_bytes = (uint32_t)((int64_t)T * p.d * 2);
       U.b0 = U.b1 = br ? p.uu : p.ug;
@@ -838,12 +903,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
 
   const int nt1 = 2 * (p.r_gu / 128), nt3 = p.r_d / 128, nt4 = p.d / 128;
 
+  // ---- phase 0 (the MLP block): xn = RMSNorm(x), row b by block b; phase
+  // 1's first weight stages stream in at the barrier ----
+  if constexpr (NORM) {
+    if (b < T) dl_norm_row(p, lds + L::A_OFF, b);
+    dl_wait_vm<0>();
+    grid_sync(1);
+  }
+
   // ---- phase 1: XU_g, XU_u = X . [Ug | Uu] -> bf16 XU ----
   for (int u = b; u < units[1]; u += G) {
     DlUnit U;
     unit_of(1, u, U);
     f32x4 acc[MT];
-    dl_run<MT, false>(c, U, false, acc);
+    dl_run<MT, false>(c, U, NORM && u == b, acc);
     dl_combine<MT>(c, U, acc, u, nt1, p.splits1, dl_tile_counter(p.sync, u % nt1), p.slices, flag, U.dst, false,
                    false, p.sync);
   }
@@ -923,7 +996,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
     dl_combine<MT>(c, U, acc, u, nt4, p.splits4, dl_tile_counter(p.sync, nt1 + nt3 + u % nt4), p.slices, flag, U.dst,
-                   true, *bad != 0, p.sync);
+                   true, *bad != 0, p.sync, static_cast<const uint16_t*>(p.resid));
   }
 }
 

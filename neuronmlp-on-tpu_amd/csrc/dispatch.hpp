@@ -84,10 +84,12 @@ hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint1
 // out[m][n] = bf16(sum_s in[s * sstride + zb * bstride + frag(m, n)]) for
 // tiles of 256 x 32*fn with nw waves, batch entries zb (out batch stride
 // obstride elements); with `gate` (bf16 in the same fragment order),
-// out = bf16(SiLU(gate) * sum).
+// out = bf16(SiLU(gate) * sum); with `resid` (bf16, row pitch ldo, batch
+// entry 0), out = bf16(resid + bf16(sum)), the MLP block's residual add.
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
-                                   int batch, hipStream_t st, const uint16_t* gate = nullptr);
+                                   int batch, hipStream_t st, const uint16_t* gate = nullptr,
+                                   const uint16_t* resid = nullptr);
 hipError_t launch_finalize(const float* g, const float* u, int64_t ldi, uint16_t* out, int64_t ldo, int rows,
                            int cols, bool swiglu, bool out_t, hipStream_t st);
 

@@ -56,7 +56,7 @@ template <int FM, int FN>
 __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, int splits, int64_t sstride,
                                                                int64_t bstride, uint16_t* out, int64_t ldo,
                                                                int64_t obstride, int M, int N, int mtiles, int nw,
-                                                               const uint16_t* gate) {
+                                                               const uint16_t* gate, const uint16_t* resid) {
   constexpr int ROWS = 16 * FM, COLS = 16 * FN, PITCH = COLS + 8;  // staged row pitch (elements)
   constexpr int Q = FM * FN * 64;                                   // float4s per wave tile
   __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS * PITCH];
@@ -99,17 +99,23 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
   for (int k = threadIdx.x; k < ROWS * (COLS / 8); k += 256) {
     const int r = k / (COLS / 8), c = 8 * (k % (COLS / 8));
     const int m = m0 + r, n = n0 + c;
-    if (m < M && n < N)  // N % 8 == 0
-      *reinterpret_cast<u32x4*>(dst + (int64_t)m * ldo + n) = *reinterpret_cast<const u32x4*>(tile + r * PITCH + c);
+    if (m < M && n < N) {  // N % 8 == 0
+      u32x4 o = *reinterpret_cast<const u32x4*>(tile + r * PITCH + c);
+      if (resid) {  // the MLP block's residual add, same layout as out (batch entry 0)
+        const u32x4 xr = *reinterpret_cast<const u32x4*>(resid + (int64_t)m * ldo + n);
+        o = u32x4{add_bf16x2(xr.x, o.x), add_bf16x2(xr.y, o.y), add_bf16x2(xr.z, o.z), add_bf16x2(xr.w, o.w)};
+      }
+      *reinterpret_cast<u32x4*>(dst + (int64_t)m * ldo + n) = o;
+    }
   }
 }
 
 template <int FM, int FN>
 hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out, int64_t ldo,
                      int64_t obstride, int M, int N, int mtiles, int ntiles, int nw, int batch, const uint16_t* gate,
-                     hipStream_t st) {
+                     const uint16_t* resid, hipStream_t st) {
   hipLaunchKernelGGL((reduce_frag_bf16_kernel<FM, FN>), dim3(mtiles * ntiles * nw, batch), dim3(256), 0, st, in,
-                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw, gate);
+                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw, gate, resid);
   return hipGetLastError();
 }
 
@@ -117,12 +123,12 @@ hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstri
 
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
-                                   int batch, hipStream_t st, const uint16_t* gate) {
-  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
-  if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
-  if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
-  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
-  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, st);
+                                   int batch, hipStream_t st, const uint16_t* gate, const uint16_t* resid) {
+  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
+  if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
+  if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
+  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
+  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   return hipErrorInvalidValue;
 }
 

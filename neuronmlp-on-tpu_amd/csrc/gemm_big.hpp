@@ -142,6 +142,13 @@ __device__ __forceinline__ u32x4 fp8x8_to_bf16x8(u32x2 v) {
                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, 1.0f, true))};
 }
 
+// bf16(a + b) of four bf16 pairs (the residual add of the MLP block).
+__device__ __forceinline__ uint32_t add_bf16x2(uint32_t a, uint32_t b) {
+  return pack_bf16x2(__uint_as_float(a << 16) + __uint_as_float(b << 16),
+                     __uint_as_float(a & 0xffff0000u) + __uint_as_float(b & 0xffff0000u));
+}
+__device__ __forceinline__ u32x2 add_bf16x4(u32x2 a, u32x2 b) { return u32x2{add_bf16x2(a.x, b.x), add_bf16x2(a.y, b.y)}; }
+
 // 32-byte unit swizzle of a natural-layout B row k.
 __device__ __forceinline__ int bnat_swz(int k) { return k & 3; }
 
@@ -165,6 +172,7 @@ struct BigParams {
   int64_t out_sstride;   // elements between split-K partial slices (fp32 output)
   const uint16_t* gmem;  // BEPI_SWIGLU_MEM: bf16 gate values, same layout as out
   const float* scale[2]; // fp8 B: one fp32 scale per output column, per batch entry
+  const uint16_t* resid; // bf16 STORE epilogue, batch entry 0 (the MLP block's last stage): out = bf16(resid + bf16(C)), row pitch ldo[0]
   int gfrag;             // BEPI_SWIGLU_MEM: gmem holds g in fragment order (BEPI_STORE_FRAG)
   int out_frag;          // fp32 output (split-K slices) in fragment order, padded tiles included
   int M, K;
@@ -524,8 +532,9 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
             u32x2{pack_bf16x2(silu_f32(g0) * v.x, silu_f32(g1) * v.y),
                   pack_bf16x2(silu_f32(g2) * v.z, silu_f32(g3) * v.w)};
       } else {
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) =
-            u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+        u32x2 ov = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+        if (p.resid) ov = add_bf16x4(*reinterpret_cast<const u32x2*>(p.resid + o), ov);
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) = ov;
       }
     }
   }

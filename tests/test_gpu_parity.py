@@ -610,6 +610,63 @@ def test_mlp_stack_nonuniform_ranks(gpu):
     assert _rel(y - x0, ref - x0) < BF16_TOL
 
 
+def _block_case(shape, T, seed):
+    x, f = inputs.make_layer(shape, T=T, seed=seed)
+    xb, *fb = _rounded((x, *f), torch.bfloat16)
+    gain = np.random.default_rng(seed).uniform(0.9, 1.1, size=shape.d).astype(np.float32)
+    return xb, fb, gain
+
+
+@pytest.mark.parametrize("T,padded", [(1, True), (1, False), (2, True), (3, False), (8, True), (32, True),
+                                      (64, True), (100, False)])
+def test_mlp_block_fused_into_decode_layer(gpu, layer8b, T, padded):
+    """The 8B block at decode shapes: one decode-layer launch, whose phase 0
+    writes RMSNorm(x) (a block per token row) and whose phase 4 adds the
+    residual; against the oracle's block, bitwise on replay."""
+    shape, fb, ft = layer8b
+    xb = _x(T, shape.d, 900 + T)
+    gain = np.random.default_rng(T).uniform(0.9, 1.1, size=shape.d).astype(np.float32)
+    g = torch.from_numpy(gain).to(gpu)
+    xt = _to(xb, torch.bfloat16, gpu)
+    fs = [ops.pad_rows(a, 64) if padded and i % 2 else a for i, a in enumerate(ft)]
+    ws = ops.svd_mlp_workspace(xt, r=shape.r, ff=shape.ff)
+    runs = [_np(ops.svd_mlp_block(xt, g, *fs, eps=1e-5, workspace=ws)) for _ in range(2)]
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    assert _rel(runs[0], ref) < BF16_TOL
+    assert _rel(runs[0] - xb, ref - xb) < BF16_TOL, _rel(runs[0] - xb, ref - xb)
+    assert np.array_equal(runs[0], runs[1])
+    # two launches: 2 or 3 barriers each, plus the one after phase 0; counters back at zero
+    per = (2 if _contracted(shape, T, padded=padded) else 3) + 1
+    assert _barrier_state(ws) == (2 * per, 0) and not any(_tile_counters(ws))
+
+
+@pytest.mark.parametrize("shape", [inputs.LayerShape(128, 256, 384, 128), inputs.LayerShape(5248, 1024, 512, 256)])
+@pytest.mark.parametrize("T", [1, 7, 16])
+def test_mlp_block_fused_norm_row_widths(gpu, shape, T):
+    """Phase 0's row pieces (8 elements per thread per 4096): a row shorter
+    than one piece round (d = 128) and one of two rounds, the second partial
+    (d = 5248)."""
+    xb, fb, gain = _block_case(shape, T, 950 + T)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    y = _np(ops.svd_mlp_block(t[0], torch.from_numpy(gain).to(gpu), *t[1:], eps=1e-5))
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    assert _rel(y, ref) < BF16_TOL and _rel(y - xb, ref - xb) < BF16_TOL
+
+
+@pytest.mark.parametrize("T", [1, 2])
+def test_mlp_block_gemv_layer_residual(gpu, T):
+    """The streaming-GEMV layer (d = 1040: no multiple of 128) takes the
+    block's residual add in its output write after the RMSNorm pass."""
+    shape = inputs.LayerShape(1040, 2064, 400, 272)
+    xb, fb, gain = _block_case(shape, T, 960 + T)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ws = ops.svd_mlp_workspace(t[0], r=shape.r, ff=shape.ff)
+    y = _np(ops.svd_mlp_block(t[0], torch.from_numpy(gain).to(gpu), *t[1:], eps=1e-5, workspace=ws))
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    assert _rel(y, ref) < BF16_TOL and _rel(y - xb, ref - xb) < BF16_TOL
+    assert _barrier_state(ws) == (4, 0)   # one GEMV-layer launch
+
+
 # ---------------------------------------------------------------------------
 # distinct gate and up ranks (svdmlp_svd_mlp_ranks)
 # ---------------------------------------------------------------------------
