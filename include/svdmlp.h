@@ -69,6 +69,20 @@ extern "C" {
  * dense factors (no padded rows) up to three. */
 #define SVDMLP_CONTRACT 0x10u
 
+/* svd_mlp entry points with fp8 factors: fp8 activations for the h . Ud
+ * stage.  No counterpart in the reference, which has no fp8 path; BASELINE
+ * configuration 5 asks for the layer on the CDNA4 fp8 MFMA.  h is quantised
+ * to e4m3fn per token row (scale amax / 448) and the stage runs fp8 x fp8
+ * MFMAs (v_mfma_scale_f32_16x16x128_f8f6f4, twice the bf16 rate) with fp32
+ * accumulation.  Only this stage: rounding an activation to e4m3 costs ~2.6%
+ * relative error in the GEMM it feeds, so quantising a second GEMM's input
+ * would exceed the 3e-2 fp8 tolerance (LLaMA3-70B shape: the layer with the
+ * flag is ~2.7% from the math on dequantised factors, against 0.5% without).
+ * Taken on the large-tile path (more than 64 tokens) where ff is a multiple
+ * of 128 and r_d of 16; other shapes run as without it.  bf16 factors:
+ * SVDMLP_EINVAL. */
+#define SVDMLP_FP8_ACT 0x20u
+
 /* status codes */
 #define SVDMLP_OK 0
 #define SVDMLP_EINVAL (-1)

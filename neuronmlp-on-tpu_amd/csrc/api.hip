@@ -39,6 +39,7 @@
 #include "decode_gemv.hpp"
 #include "decode_layer.hpp"
 #include "gemm_big.hpp"
+#include "gemm_f8f8.hpp"
 #include "svdmlp.h"
 
 using namespace svdmlp;
@@ -93,12 +94,15 @@ enum Stage : int {
   ST_DEC_LAYER,
   ST_DEC_GEMV,
   ST_DEC_CONTRACT,
+  ST_QUANT,
+  ST_D_XU_F8,
   ST_COUNT
 };
 const char* const kStageNames[ST_COUNT] = {
     "zero_fill",        "gate_up_xu",       "gate_up_xuv_swiglu", "down_xu",           "down_xuv",
     "decode_gate_up_xu", "decode_gate_up_xuv", "decode_down_xu",   "decode_down_xuv", "finalize",
-    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer",  "decode_layer_contracted"};
+    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer",  "decode_layer_contracted", "quant_h_e4m3", "down_xu_fp8"
+};
 
 struct Profiler {
   std::mutex mu;
@@ -767,6 +771,78 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
                   fn, BEPI_SWIGLU_MEM, r_u, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1);
 }
 
+// fp8 activations for h . Ud (SVDMLP_FP8_ACT): h quantised to e4m3 per
+// token row, then the fp8 x fp8 GEMM (gemm_f8f8.hpp) into bf16 XU_d.  The
+// e4m3 h goes to the g region (dead once the u pass has read it), the row
+// scales to xu32 (unused on the large-tile path).
+bool f8_down_ok(int64_t T, int64_t ff, int64_t r_d, int64_t ldud) {
+  return T > kDecodeMaxT && ff % 128 == 0 && r_d % 16 == 0 && ldud % 16 == 0 && ff <= 32768;
+}
+
+int f8_down_xu(const Common& c, const uint16_t* h, const void* ud, const float* sud, int64_t ldud, int T, int ff,
+               int r, char* ws, const Ws& L) {
+  uint8_t* hq = reinterpret_cast<uint8_t*>(ws + L.g);
+  float* hs = reinterpret_cast<float*>(ws + L.xu32);
+  uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
+  const char* why = nullptr;
+  int rc;
+  {
+    StageScope ss(ST_QUANT, c.st);
+    rc = check(launch_quant_rows_e4m3(h, ff, hq, ff, hs, T, ff, c.st, &why), "e4m3 row quantisation", why);
+  }
+  if (rc) return rc;
+  F8Params p{};
+  p.a = hq;
+  p.b = static_cast<const uint8_t*>(ud);
+  p.a_bytes = (uint32_t)((int64_t)T * ff);
+  p.b_bytes = (uint32_t)((int64_t)ff * ldud);
+  p.lda = ff;
+  p.ldb = ldud;
+  p.sa = hs;
+  p.sb = sud;
+  p.M = T;
+  p.N = r;
+  p.K = ff;
+  p.mtiles = (T + kF8BM - 1) / kF8BM;
+  p.ntiles = (r + kF8BN - 1) / kF8BN;
+  // K splits: rounds of 256 blocks x (128-k steps x ~1100 cycles + ~20K per
+  // block) + the fp32 slices written and read back (~2800 bytes per cycle),
+  // within the workspace's slice area
+  const int64_t per = (int64_t)p.mtiles * kF8BM * p.ntiles * kF8BN;
+  const int blocks = p.mtiles * p.ntiles, ksteps = ff / kF8BK;
+  int splits = 1;
+  double best = 0;
+  for (int s = 1; s <= 4; ++s) {
+    if (s > 1 && (int64_t)s * per * 4 > (int64_t)(L.norm - L.part)) break;
+    const int steps = (ksteps + s - 1) / s;
+    const double cost = (double)((blocks * s + 255) / 256) * (steps * 1100.0 + 20000.0) +
+                        (s > 1 ? (double)s * per * 8 / 2800.0 : 0.0);
+    if (s == 1 || cost < best) {
+      best = cost;
+      splits = s;
+    }
+  }
+  p.k_split = ((ksteps + splits - 1) / splits) * kF8BK;
+  splits = (ff + p.k_split - 1) / p.k_split;
+  if (splits == 1) {
+    p.out = xu;
+    p.ldo = r;
+    StageScope ss(ST_D_XU_F8, c.st);
+    return check(launch_f8_gemm(p, 1, c.st, &why), "fp8 x fp8 GEMM", why);
+  }
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  p.out = part;
+  p.out_sstride = per;
+  {
+    StageScope ss(ST_D_XU_F8, c.st);
+    if ((rc = check(launch_f8_gemm(p, splits, c.st, &why), "fp8 x fp8 GEMM", why))) return rc;
+  }
+  StageScope fin(ST_FINALIZE, c.st);
+  return check(launch_reduce_frag_bf16(part, splits, per, per, xu, r, (int64_t)T * r, T, r, p.mtiles, p.ntiles, 4, 8, 1,
+                                       c.st),
+               "split-K reduce");
+}
+
 // y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
 int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T, int r, int dout, char* ws,
           const Ws& L, void* y, const float* sv = nullptr, int64_t ldv = 0) {
@@ -1370,9 +1446,12 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
     for (int i = 0; i < 6; ++i)
       if (!scales[i]) return fail("fp8 weights need per-column scales");
   }
-  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_CONTRACT)) return fail("unsupported flags 0x%x", flags);
+  if (flags & ~(SVDMLP_U_LINEAR | SVDMLP_V_LINEAR | SVDMLP_CONTRACT | SVDMLP_FP8_ACT))
+    return fail("unsupported flags 0x%x", flags);
   const bool contract_asked = flags & SVDMLP_CONTRACT;
-  flags &= ~SVDMLP_CONTRACT;
+  const bool fp8_act = flags & SVDMLP_FP8_ACT;
+  flags &= ~(SVDMLP_CONTRACT | SVDMLP_FP8_ACT);
+  if (fp8_act && !fp8) return fail("SVDMLP_FP8_ACT needs fp8 factors");
   if (fp8 && flags) return fail("fp8 weights must use the natural layout");
   // one rank for both branches below; two ranks only on the large-tile path
   const bool two = r_g != r_u;
@@ -1452,7 +1531,11 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
       return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};
-    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) return rc;
+    if (fp8_act && f8_down_ok(T, ff, r_d, ld.ud)) {
+      if ((rc = f8_down_xu(c, hbuf, ud, S[4], ld.ud, (int)T, (int)ff, (int)r_d, ws, L))) return rc;
+    } else if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) {
+      return rc;
+    }
     return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);
   }
 
@@ -1544,7 +1627,11 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
       return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};
-    if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) return rc;
+    if (fp8_act && f8_down_ok(T, ff, r_d, ld.ud)) {
+      if ((rc = f8_down_xu(c, hbuf, ud, S[4], ld.ud, (int)T, (int)ff, (int)r_d, ws, L))) return rc;
+    } else if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) {
+      return rc;
+    }
     return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);
   }
 

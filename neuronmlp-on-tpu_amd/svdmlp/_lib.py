@@ -25,6 +25,7 @@ SVDMLP_V_LINEAR = 0x2
 SVDMLP_OUT_T = 0x4
 SVDMLP_X_T = 0x8
 SVDMLP_CONTRACT = 0x10
+SVDMLP_FP8_ACT = 0x20
 SVDMLP_OK = 0
 SVDMLP_EINVAL = -1
 SVDMLP_EHIP = -2

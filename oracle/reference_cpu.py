@@ -17,6 +17,12 @@ Every function cites the reference lines it follows.  What pins each one
   e4m3_encode ........ torch.float8_e4m3fn cast (RNE, saturating) on dense
                        grids incl. midpoints; round-trip of all finite codes.
   quantize_per_channel amax/448 definition; reconstruction error bound.
+  quantize_rows_e4m3 . per-row amax/448 scale; codes equal to torch's e4m3fn
+                       cast of the row times 448/amax; every element within
+                       half an e4m3 step of its code's value; zero rows.
+  svd_mlp_fp8_act_ref  equals svd_mlp_ref when h is already on the row grid
+                       (quantising a quantised h changes nothing); error
+                       against svd_mlp_ref within the e4m3 budget.
   silu ............... closed form x*sigmoid(x) in float64, silu(0)=0, limits,
                        the identity silu(x)-silu(-x)=x, torch silu (<=2 ulp).
   low_rank_dim ....... known answers 1280/1792/2560 (reference.py:29-31),
@@ -48,6 +54,8 @@ __all__ = [
     "e4m3_decode",
     "e4m3_encode",
     "quantize_per_channel",
+    "quantize_rows_e4m3",
+    "svd_mlp_fp8_act_ref",
     "silu",
     "low_rank_dim",
     "fused_gate_up_ref",
@@ -150,6 +158,19 @@ def quantize_per_channel(w, axis: int = 0):
     return q, np.squeeze(scale, axis=axis).astype(F32)
 
 
+def quantize_rows_e4m3(a):
+    """Per-row fp8 quantization of an activation (the MI355X build's
+    fp8-activation mode; the reference has no fp8 path): scale[m] =
+    amax_m / 448 and q = e4m3(a * (448 / amax_m)), the product in float32; a
+    zero row gets scale 1.  Returns (bits uint8, scale float32)."""
+    a = np.asarray(a, dtype=F32)
+    amax = np.max(np.abs(a), axis=1, keepdims=True)
+    inv = np.where(amax > 0, F32(448.0) / np.where(amax > 0, amax, F32(1.0)), F32(1.0)).astype(F32)
+    q = e4m3_encode((a * inv).astype(F32))
+    scale = np.where(amax > 0, amax / F32(448.0), F32(1.0)).astype(F32)
+    return q, scale[:, 0]
+
+
 # ---------------------------------------------------------------------------
 # Reference math (kernels/reference.py)
 # ---------------------------------------------------------------------------
@@ -202,6 +223,18 @@ def svd_mlp_ref(x, u_gate, v_gate, u_up, v_up, u_down, v_down, dtype: str = "flo
     activation dtype between the two halves."""
     h = fused_gate_up_ref(x, u_gate, v_gate, u_up, v_up, dtype)
     return fused_xuv_ref(h, u_down, v_down, dtype)
+
+
+def svd_mlp_fp8_act_ref(x, u_gate, v_gate, u_up, v_up, u_down, v_down) -> np.ndarray:
+    """svd_mlp_ref in bf16 with the down projection's input h quantized to
+    e4m3 per token row (quantize_rows_e4m3), the MI355X fp8-activation mode
+    of the h . Ud stage: xuv(dequant(quant(round(gate_up(x))))).  The
+    reference's math (kernels/reference.py:85-93) with that one extra
+    rounding."""
+    h = fused_gate_up_ref(x, u_gate, v_gate, u_up, v_up, "bfloat16")
+    q, s = quantize_rows_e4m3(h)
+    hq = (e4m3_decode(q).astype(F32) * s[:, None]).astype(F32)
+    return fused_xuv_ref(hq, u_down, v_down, "bfloat16")
 
 
 def dense_mlp_ref(x, w_gate, w_up, w_down, dtype: str = "float32") -> np.ndarray:

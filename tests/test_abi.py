@@ -83,9 +83,13 @@ def test_invalid_arguments_rejected_before_any_hip_call(lib):
     assert lib.svdmlp_svd_mlp_ranks(p, p, p, p, p, p, p, None, None, p, 4, 16, 32, 8, 0, 8, 1, 1, 0, p, 1 << 20,
                                     None) == _lib.SVDMLP_EINVAL
     assert b"positive" in lib.svdmlp_last_error()
-    assert lib.svdmlp_svd_mlp_ranks(p, p, p, p, p, p, p, None, None, p, 4, 16, 32, 8, 16, 8, 1, 1, 0x20, p, 1 << 20,
+    assert lib.svdmlp_svd_mlp_ranks(p, p, p, p, p, p, p, None, None, p, 4, 16, 32, 8, 16, 8, 1, 1, 0x40, p, 1 << 20,
                                     None) == _lib.SVDMLP_EINVAL
     assert b"unsupported flags" in lib.svdmlp_last_error()
+    # SVDMLP_FP8_ACT (0x20) quantises activations for fp8 factors only
+    assert lib.svdmlp_svd_mlp_ranks(p, p, p, p, p, p, p, None, None, p, 4, 16, 32, 8, 16, 8, 1, 1,
+                                    _lib.SVDMLP_FP8_ACT, p, 1 << 20, None) == _lib.SVDMLP_EINVAL
+    assert b"SVDMLP_FP8_ACT needs fp8 factors" in lib.svdmlp_last_error()
     assert lib.svdmlp_svd_mlp_block_ranks(p, p, ctypes.c_float(0.0), p, p, p, p, p, p, None, None, ctypes.c_void_p(512),
                                           4, 16, 32, 8, 16, 8, 1, 1, 0, p, 1 << 20, None) == _lib.SVDMLP_EINVAL
     assert b"eps" in lib.svdmlp_last_error()

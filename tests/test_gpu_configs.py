@@ -115,3 +115,14 @@ def test_config5_70b_fp8_full_shape(gpu):
     print(f"config 5 (70B fp8, T={T}): h rel_l2 {e_h:.3e}, layer {e_y:.3e}, down entry {e_d:.3e}")
     assert np.isfinite(_np(y)).all()
     assert e_h < FP8_TOL and e_y < FP8_TOL and e_d < FP8_TOL
+    # fp8 activations for h . Ud (SVDMLP_FP8_ACT): h quantised per token row,
+    # the stage on the fp8 MFMA; against the oracle's math with the same
+    # quantisation, and against the bf16-activation math (the e4m3 budget)
+    y8 = ops.svd_mlp(x, *fs, fp8_activations=True)
+    q, s = O.quantize_rows_e4m3(_np(h[idx]))
+    hq = (O.e4m3_decode(q) * s[:, None]).astype(np.float32)
+    e_q = O.relative_l2(_np(y8[idx]), O.fused_xuv_ref(hq, deq[4], deq[5], dtype="bfloat16"))
+    e_8 = O.relative_l2(_np(y8[idx]), y_ref)
+    print(f"config 5 with fp8 activations for h . Ud: vs the same quantisation {e_q:.3e}, vs bf16 activations {e_8:.3e}")
+    assert np.isfinite(_np(y8)).all()
+    assert e_q < 1e-2 and e_8 < FP8_TOL

@@ -540,6 +540,46 @@ def test_fp8_factors(gpu, T, shape):
     assert err < FP8_TOL
 
 
+# fp8 activations for h . Ud (SVDMLP_FP8_ACT): T=256 one row tile, T=300
+# ragged rows, r_d = 288 a partial 128-column tile (the large-tile path takes
+# ranks in multiples of 32), T=1024 / ff = 4096 more k-steps per split; T=16
+# (decode) runs as without the flag
+@pytest.mark.parametrize("T,shape", [
+    (256, inputs.LayerShape(1024, 2048, 512)),
+    (300, inputs.LayerShape(1024, 2048, 512, 288)),
+    (1024, inputs.LayerShape(2048, 4096, 640, 384)),
+    (16, inputs.LayerShape(1024, 2048, 512)),
+])
+def test_fp8_activations_down_stage(gpu, T, shape):
+    xb, deq, qg = _fp8_layer(shape, T, 40 + T, gpu)
+    xt = _to(xb, torch.bfloat16, gpu)
+    got = _np(ops.svd_mlp(xt, *qg, fp8_activations=True))
+    plain = O.svd_mlp_ref(xb, *deq, dtype="bfloat16")
+    # the same quantisation applied to the GPU's own h: h's bf16-level
+    # differences from the oracle's h would move ~10% of the e4m3 codes by a
+    # step (~1.5e-2 relative), which is not what this compares
+    h = _np(ops.fused_gate_up(xt, *qg[:4]))
+    q, sc = O.quantize_rows_e4m3(h)
+    hq = (O.e4m3_decode(q) * sc[:, None]).astype(np.float32)
+    err_q = _rel(got, O.fused_xuv_ref(hq, *deq[4:], dtype="bfloat16"))
+    err = _rel(got, plain)
+    print(f"fp8 activations T={T} {shape}: vs the same quantisation {err_q:.3e}, vs bf16 activations {err:.3e}")
+    assert err < FP8_TOL
+    if T > 64:   # the large-tile path quantises h; replays are bitwise identical
+        assert err_q < 1e-2 and err > 5e-3
+        assert np.array_equal(got, _np(ops.svd_mlp(xt, *qg, fp8_activations=True)))
+    else:        # decode shapes run as without the flag (fp32-atomic split-K sums there)
+        assert _rel(got, _np(ops.svd_mlp(xt, *qg))) < 1e-3
+
+
+def test_fp8_activations_need_fp8_factors(gpu):
+    shape = inputs.LayerShape(1024, 2048, 512)
+    x, f = inputs.make_layer(shape, T=256, seed=3)
+    t = [_to(a, torch.bfloat16, gpu) for a in (x, *f)]
+    with pytest.raises(Exception, match="SVDMLP_FP8_ACT needs fp8 factors"):
+        ops.svd_mlp(*t, fp8_activations=True)
+
+
 @pytest.mark.parametrize("T", [16, 512])
 def test_fp8_gate_up_and_xuv_entries(gpu, T):
     """The two halves as separate entry points with fp8 factors."""

@@ -103,6 +103,52 @@ def test_quantize_per_channel_scale_and_error_bound():
     assert np.all(np.abs(deq - w)[big] <= np.abs(w)[big] * 2.0 ** -4 * 1.0001)
 
 
+def test_quantize_rows_e4m3_codes_scale_and_zero_rows():
+    a = (rng.normal(size=(64, 300)) * rng.uniform(0.01, 50, size=(64, 1))).astype(np.float32)
+    a[5] = 0.0
+    q, s = O.quantize_rows_e4m3(a)
+    assert q.shape == a.shape and q.dtype == np.uint8 and s.shape == (64,)
+    amax = np.abs(a).max(axis=1)
+    np.testing.assert_allclose(s[amax > 0], amax[amax > 0] / 448, rtol=1e-6)
+    assert s[5] == 1.0 and not q[5].any()
+    # codes: torch's own e4m3fn cast of the row scaled by 448 / amax (float32)
+    inv = (np.float32(448.0) / np.where(amax > 0, amax, 1)).astype(np.float32)[:, None]
+    ref = torch.from_numpy((a * inv).astype(np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(q, ref)
+    # every element within half an e4m3 step of its code's value (normal range:
+    # 2^-4 relative; subnormal range: half of 2^-9 absolute, in scaled units)
+    deq = O.e4m3_decode(q).astype(np.float64)
+    scaled = (a * inv).astype(np.float64)
+    err = np.abs(deq - scaled)
+    normal = np.abs(scaled) >= 2.0 ** -6
+    assert np.all(err[normal] <= np.abs(scaled)[normal] * 2.0 ** -4 * 1.0001)
+    assert np.all(err[~normal] <= 2.0 ** -10 * 1.0001)
+    # the row max lands on 448 exactly
+    rows = np.nonzero(amax > 0)[0]
+    np.testing.assert_array_equal(np.abs(deq[rows, np.abs(a[rows]).argmax(axis=1)]), 448.0)
+
+
+def test_svd_mlp_fp8_act_ref_fixed_point_and_budget():
+    r = np.random.default_rng(7)
+    T, d, ff, rk = 24, 64, 160, 32
+    f = [(r.normal(size=s) / np.sqrt(s[0])).astype(np.float32)
+         for s in ((d, rk), (rk, ff), (d, rk), (rk, ff), (ff, rk), (rk, d))]
+    x = O.round_bf16(r.normal(size=(T, d)).astype(np.float32))
+    ref = O.svd_mlp_ref(x, *f, dtype="bfloat16")
+    got = O.svd_mlp_fp8_act_ref(x, *f)
+    # the one extra e4m3 rounding of h: above the bf16 level, within the fp8 budget
+    err = O.relative_l2(got, ref)
+    assert 5e-3 < err < 3e-2, err
+    # h already on its rows' e4m3 grid: quantising again changes nothing, so
+    # the down half sees exactly h (the dequantised grid is a fixed point)
+    h = O.fused_gate_up_ref(x, *f[:4], dtype="bfloat16")
+    q, sc = O.quantize_rows_e4m3(h)
+    hq = (O.e4m3_decode(q) * sc[:, None]).astype(np.float32)
+    q2, sc2 = O.quantize_rows_e4m3(hq)
+    np.testing.assert_array_equal(q2, q)
+    np.testing.assert_allclose(O.e4m3_decode(q2) * sc2[:, None], hq, rtol=1e-6)
+
+
 # ---------------------------------------------------------------------------
 # silu
 # ---------------------------------------------------------------------------
