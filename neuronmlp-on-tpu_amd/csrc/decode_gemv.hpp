@@ -19,8 +19,10 @@
 //    2 G, U += XU_g . Vg, XU_u . Vu; 3 XU_d += bf16(SiLU(G) * U) . Ud;
 //    4 Y32 += XU_d . Vd, separated by grid barriers; then the last block to
 //    finish phase 4 (a done counter) writes y = bf16(Y32).  The rank sums
-//    stay fp32 (as the reference's fp32 matmuls do); h is rounded to bf16 as
-//    the reference casts it between the two halves;
+//    accumulate in fp32 and are rounded to bf16 where the next phase stages
+//    them (as the MFMA layers and the prefill path round the rank-r
+//    intermediates); h is rounded to bf16 as the reference casts it between
+//    the two halves;
 //  * the load stream runs on across phases: the last loads a wave issues in
 //    a phase are the first of the next one, so they are in flight during the
 //    phase-end atomics, the grid barrier and the activation staging.

@@ -90,10 +90,10 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
                                    int batch, hipStream_t st, const uint16_t* gate = nullptr,
                                    const uint16_t* resid = nullptr);
-// fp8 x fp8 GEMM (gemm_f8f8.hpp): splits > 1 writes fp32 fragment-order
-// slices (256 x 128 tiles, 8 waves) for launch_reduce_frag_bf16 (fn 4).
+// fp8 x fp8 GEMM (gemm_f8f8.hpp), nw = 8 or 4 waves: splits > 1 writes fp32
+// fragment-order slices (256 x 128 tiles) for launch_reduce_frag_bf16 (fn 4, nw).
 struct F8Params;
-hipError_t launch_f8_gemm(const F8Params& p, int splits, hipStream_t st, const char** why);
+hipError_t launch_f8_gemm(const F8Params& p, int splits, int nw, hipStream_t st, const char** why);
 // e4m3fn row quantisation: q[m] = e4m3(h[m] * 448 / amax_m), s[m] = amax_m / 448.
 hipError_t launch_quant_rows_e4m3(const uint16_t* h, int64_t ldh, uint8_t* q, int64_t ldq, float* s, int rows, int n,
                                   hipStream_t st, const char** why);

@@ -128,6 +128,7 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
   if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
+  if (nw == 4 && fn == 4) return go_reduce<8, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   return hipErrorInvalidValue;
 }

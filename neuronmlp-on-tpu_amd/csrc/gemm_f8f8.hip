@@ -57,17 +57,24 @@ __global__ __launch_bounds__(kF8Threads) void quant_rows_e4m3_kernel(const uint1
 
 }  // namespace
 
-hipError_t launch_f8_gemm(const F8Params& p, int splits, hipStream_t st, const char** why) {
-  if (p.K % kF8BK || p.k_split % kF8BK || p.N % 16 || p.lda % 16 || p.ldb % 16 || splits < 1 ||
+hipError_t launch_f8_gemm(const F8Params& p, int splits, int nw, hipStream_t st, const char** why) {
+  if ((nw != 4 && nw != 8) || p.K % kF8BK || p.k_split % kF8BK || p.N % 16 || p.lda % 16 || p.ldb % 16 || splits < 1 ||
       ((uintptr_t)p.sb & 15u)) {
     *why = "fp8 x fp8 GEMM: K and K per split multiples of 128, N and pitches multiples of 16, aligned scales";
     return hipErrorInvalidValue;
   }
   const dim3 grid(p.mtiles * p.ntiles, splits);
-  if (splits > 1)
-    hipLaunchKernelGGL(f8_gemm_kernel<true>, grid, dim3(kF8Threads), 0, st, p);
-  else
-    hipLaunchKernelGGL(f8_gemm_kernel<false>, grid, dim3(kF8Threads), 0, st, p);
+  if (nw == 4) {
+    if (splits > 1)
+      hipLaunchKernelGGL((f8_gemm_kernel<true, 4>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((f8_gemm_kernel<false, 4>), grid, dim3(256), 0, st, p);
+  } else {
+    if (splits > 1)
+      hipLaunchKernelGGL((f8_gemm_kernel<true, 8>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((f8_gemm_kernel<false, 8>), grid, dim3(512), 0, st, p);
+  }
   return hipGetLastError();
 }
 

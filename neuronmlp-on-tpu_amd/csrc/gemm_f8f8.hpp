@@ -10,10 +10,10 @@
 // scales (127 = 2^0), fp32 accumulation; both scales multiply the fp32
 // accumulator in the epilogue.
 //
-// Block: 512 threads = 8 waves in a 4 (M) x 2 (N) grid; each wave owns a
-// 64 x 64 tile of 16x16 MFMA blocks, so the block tile is 256 x 128 and the
-// wave tile geometry (and hence the fragment order of split-K slices) is the
-// large-tile bf16 kernel's at fn = 4, summed by the same reduction.
+// Block: 8 waves in a 4 (M) x 2 (N) grid of 64 x 64 wave tiles, or 4 waves
+// in a 2 x 2 grid of 128 x 64; the block tile is 256 x 128 either way, and
+// the fragment order of split-K slices is the large-tile bf16 kernel's at
+// fn = 4 with the same wave count, summed by the same reduction.
 //
 // One k-step is 128 k (one MFMA deep).  LDS holds 3 stages of 48 KB:
 //  * A: 256 rows x 128 bytes, 16-byte chunks XOR-swizzled by row & 7; a
@@ -49,7 +49,7 @@ struct F8Params {
   int k_split;  // K per split, a multiple of 128
 };
 
-constexpr int kF8Threads = 512;
+constexpr int kF8Threads = 512;  // the row quantisation's block
 constexpr int kF8BM = 256, kF8BN = 128, kF8BK = 128;
 constexpr int kF8Stages = 3;
 constexpr int kF8ABytes = kF8BM * kF8BK;  // 32 KB
@@ -65,9 +65,12 @@ __device__ __forceinline__ f32x4 mfma_f8(const u32x4 (&b)[2], const u32x4 (&a)[2
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bv, av, c, 0, 0, 0, 127, 0, 127);
 }
 
-template <bool SLICES>
-__global__ __launch_bounds__(kF8Threads, 1) void f8_gemm_kernel(F8Params p) {
-  constexpr int NW = 8, FM = 4, FN = 4, NS = kF8Stages;
+// NW waves in an (NW / 2) x 2 grid: 8 waves of 64 x 64 (two per SIMD) or 4
+// of 128 x 64 (one per SIMD, accumulators in AGPRs), which read a quarter
+// less from LDS per MFMA.
+template <bool SLICES, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
+  constexpr int FM = 32 / NW, FN = 4, NS = kF8Stages;
   constexpr int A_UNITS = kF8ABytes / 1024 / NW, B_UNITS = kF8BBytes / 1024 / NW;  // 4, 2
   constexpr int NDMA = A_UNITS + B_UNITS;
   constexpr int B_REGION = NS * kF8ABytes;
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void f8_gemm_kernel(F8Params p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
-  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+  const int wm0 = (wave >> 1) * 16 * FM, wn0 = (wave & 1) * 64;
 
   const i32x4 ra = make_rsrc_sgpr(p.a, p.a_bytes);
   const i32x4 rb = make_rsrc_sgpr(p.b, p.b_bytes);
@@ -148,7 +151,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void f8_gemm_kernel(F8Params p) {
     u32x4 a[FM][2];
     u32x2 b[FN][4];
   };
-  constexpr int NREAD = 2 * FM + 4 * FN;  // 24
+  constexpr int NREAD = 2 * FM + 4 * FN;  // 24 (NW 8) or 32 (NW 4)
   // read r of stage slot s: A halves first, then B pieces
   auto read_one = [&](int s, int r, Frags& f) {
     if (r < 2 * FM) {
@@ -160,7 +163,7 @@ __global__ __launch_bounds__(kF8Threads, 1) void f8_gemm_kernel(F8Params p) {
       f.b[j][q] = lds_read_tr8(b_rd[j] + s * kF8BBytes + 8 * 128 * q);
     }
   };
-  constexpr int NMFMA = FM * FN;  // 16
+  constexpr int NMFMA = FM * FN;  // 16 or 32
   auto mfma_one = [&](int m, const Frags& f) {
     const int i = m / FN, j = m % FN;
     const u32x4 bb[2] = {u32x4{f.b[j][0].x, f.b[j][0].y, f.b[j][1].x, f.b[j][1].y},
@@ -174,12 +177,15 @@ __global__ __launch_bounds__(kF8Threads, 1) void f8_gemm_kernel(F8Params p) {
   // barrier that ended step kt - 1) interleaved; then wait until stage
   // kt + 2 landed (stage kt + NS may still fly) and meet at the barrier.
   Frags f0, f1;
-  static_assert(NREAD <= 2 * NMFMA && NDMA <= NMFMA, "interleave slots");
+  // reads per MFMA slot: 2 with 8 waves (24 reads, 16 MFMAs), 1 with 4
+  constexpr int RPS = (NREAD + NMFMA - 1) / NMFMA;
+  static_assert(NDMA + 2 <= NMFMA, "interleave slots");
   auto step = [&](int kt, int s, const Frags& cur, Frags& nxt) {
 #pragma unroll
     for (int m = 0; m < NMFMA; ++m) {
-      if (2 * m < NREAD) read_one((s + 1) % NS, 2 * m, nxt);
-      if (2 * m + 1 < NREAD) read_one((s + 1) % NS, 2 * m + 1, nxt);
+#pragma unroll
+      for (int q = 0; q < RPS; ++q)
+        if (RPS * m + q < NREAD) read_one((s + 1) % NS, RPS * m + q, nxt);
       if (m >= 2 && m - 2 < NDMA) dma_one(kt + NS, s, m - 2);
       mfma_one(m, cur);
       __builtin_amdgcn_sched_barrier(0);
