@@ -182,10 +182,19 @@ def _cpu_baseline(layer0, x, T, seconds):
         if (el >= seconds and reps >= 2) or el >= 3 * seconds:
             break
     flops = O.layer_flops(rows, D, FF, R) * reps
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {
         "value": round(flops / el / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": int(threads),
+        "cpu_model": model,
         "kind": "port",
         "sample": f"oracle svd_mlp_ref (numpy fp32 GEMMs, bf16 rounding) on {rows} of {T} rows of layer 0, "
                   f"{reps} reps in {el:.1f} s",
@@ -197,7 +206,23 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
     import svdmlp
     from svdmlp import _lib
 
-    dec = {}
+    # measured HBM ceiling for the decode fractions: a 1 GiB device-to-device
+    # copy (read + write bytes over its time), best of 5
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    best = None
+    for _ in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        dst.copy_(src)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3
+        best = t if best is None else min(best, t)
+    del src, dst
+    copy_gbs = 2 * n / best / 1e9
+    dec = {"hbm_copy_GBps": round(copy_gbs, 1)}
     for Td in args.decode_tokens:
         xd = x[:Td].contiguous()
         wsd = svdmlp.svd_mlp_workspace(xd, r=R, ff=FF)
@@ -229,6 +254,7 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
             "us_per_layer": round(msd * 1e3, 2),
             "GB/s": round(gbs, 1),
             "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+            "frac_measured_copy": round(gbs / copy_gbs, 4),
             "traffic": traffic,
             "traffic_GB/s": round(traffic / (msd * 1e-3) / 1e9, 1) if traffic else None,
             "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),
@@ -455,6 +481,15 @@ def main(argv=None) -> int:
         with _lib.StageProfile() as prof:
             ms_prof, _ = _time_steps(torch, step, args.steps, 0, stream)
         stages = {k: v[0] / v[1] for k, v in prof.result.items()}
+        # per-step distribution: each step between its own pair of events
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        for i, (e0, e1) in enumerate(evs):
+            e0.record(stream)
+            step(i)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        per_step = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+        pct = lambda q: per_step[min(len(per_step) - 1, int(q * (len(per_step) - 1) + 0.5))]
         # Each GEMM stage is one kernel launch; the roofline line is for the
         # one with the most time per layer.
         stage_work = _stage_work(T)
@@ -508,6 +543,7 @@ def main(argv=None) -> int:
             },
             "stages_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
             "ms_per_step_with_stage_events": round(ms_prof, 4),
+            "step_us_p10_p50_p90": [round(pct(0.1), 1), round(pct(0.5), 1), round(pct(0.9), 1)],
         })
 
     # CPU work last (the oracle is the checker only; nothing below is timed
@@ -525,7 +561,7 @@ def main(argv=None) -> int:
     if args.only in (None, "fp8"):
         record["fp8_70b"].update(_fp8_parity(args, f_fs, f_x, f_out))
     if args.only == "decode":
-        t1 = record["decode"].get("T=1") or next(iter(record["decode"].values()))
+        t1 = record["decode"].get("T=1") or next(v for v in record["decode"].values() if isinstance(v, dict))
         record.update({"metric": METRIC, "value": t1["GB/s"], "unit": "GB/s", "n_gpus": 1,
                        "steps": args.decode_steps, "warmup": max(10, args.warmup), "ms_per_step": t1["us_per_layer"] / 1e3,
                        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
