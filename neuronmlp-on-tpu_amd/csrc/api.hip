@@ -778,7 +778,9 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
 // e4m3 h goes to the g region (dead once the u pass has read it), the row
 // scales to xu32 (unused on the large-tile path).
 bool f8_down_ok(int64_t T, int64_t ff, int64_t r_d, int64_t ldud) {
-  return T > kDecodeMaxT && ff % 128 == 0 && r_d % 16 == 0 && ldud % 16 == 0 && ff <= 32768;
+  const int64_t lim = (int64_t)1 << 31;  // 32-bit buffer offsets of e4m3 h and Ud
+  return T > kDecodeMaxT && ff % 128 == 0 && r_d % 16 == 0 && ldud % 16 == 0 && ff <= 32768 && T * ff < lim &&
+         ff * ldud < lim;
 }
 
 int f8_down_xu(const Common& c, const uint16_t* h, const void* ud, const float* sud, int64_t ldud, int T, int ff,
