@@ -542,6 +542,8 @@ def main(argv=None) -> int:
                 "avg_launch_us": round(dom_ms * 1e3, 2) if dom_ms else None,
             },
             "stages_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
+            # per layer: the split-K reductions ("finalize") run three times per layer
+            "stages_us_per_layer": {k: round(v[0] / args.steps * 1e3, 2) for k, v in prof.result.items()},
             "ms_per_step_with_stage_events": round(ms_prof, 4),
             "step_us_p10_p50_p90": [round(pct(0.1), 1), round(pct(0.5), 1), round(pct(0.9), 1)],
         })
