@@ -53,7 +53,10 @@ class GateUpBlocks(NamedTuple):
     bn: int
 
 
-# Down (XUV) tile constants of the reference API (results/down_static_analysis_8b.json:17-22).
+# Down (XUV) tile constants of the reference's config module (values from
+# results/down_static_analysis_8b.json:17-22), kept so that importers of that
+# module (bench/diagnose_down.py:23-26) resolve; the HIP kernels pick their own
+# tiles and do not read them.
 XUV_ROW_TILE = 128
 XUV_INPUT_TILE = 1024
 XUV_RANK_TILE = 512
