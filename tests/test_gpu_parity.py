@@ -680,6 +680,27 @@ def test_mlp_block_fused_into_decode_layer(gpu, layer8b, T, padded):
     assert _barrier_state(ws) == (2 * per, 0) and not any(_tile_counters(ws))
 
 
+@pytest.mark.parametrize("T", [1, 8])
+def test_mlp_block_decode_unaligned_gain(gpu, T):
+    """Gains that are not 16-byte aligned (a view 4 bytes into a buffer): the
+    decode layer runs the RMSNorm as its own pass, then adds the residual in
+    its last phase; the result matches the fused phase 0's to the bf16
+    level and the oracle's block."""
+    shape = inputs.LayerShape(1024, 2048, 512, 384)
+    xb, fb, gain = _block_case(shape, T, 970 + T)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    g = torch.from_numpy(gain).to(gpu)
+    buf = torch.empty(shape.d + 4, dtype=torch.float32, device=gpu)
+    buf[1:shape.d + 1] = g
+    g_off = buf[1:shape.d + 1]
+    assert g_off.data_ptr() % 16 != 0
+    y_off = _np(ops.svd_mlp_block(t[0], g_off, *t[1:], eps=1e-5))
+    y = _np(ops.svd_mlp_block(t[0], g, *t[1:], eps=1e-5))
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    assert _rel(y_off, ref) < BF16_TOL and _rel(y_off - xb, ref - xb) < BF16_TOL
+    assert _rel(y_off - xb, y - xb) < 5e-3
+
+
 @pytest.mark.parametrize("shape", [inputs.LayerShape(128, 256, 384, 128), inputs.LayerShape(5248, 1024, 512, 256)])
 @pytest.mark.parametrize("T", [1, 7, 16])
 def test_mlp_block_fused_norm_row_widths(gpu, shape, T):
