@@ -268,16 +268,23 @@ struct DlCtx {
   int a_cached;  // DecLayerParams::a_cached
 };
 
+// 32-byte unit swizzle of weight row k (128-byte rows, two per 64-bank
+// row): a transposing read's lanes 0-15 touch rows k0..k0+3 and lanes 16-31
+// rows k0+8..k0+11 in the same pass; k & 3 spreads each group's rows over
+// distinct units and k & 8 flips the low bit, so the second group takes the
+// units of each half of the banks that the first leaves free.
+__device__ __forceinline__ int dl_wswz(int k) { return (k & 3) ^ ((k >> 3) & 1); }
+
 // Weight DMA of stage j into ring slot `slot` (one instruction per wave):
 // rows 8*(wave%4)..+7 of sub-tile wave/4; lane L takes row 8*(wave%4) + L/8,
 // physical chunk L%8 of 32-byte unit pu = (L%8)/2, which holds logical unit
-// pu ^ (row & 3).
+// pu ^ dl_wswz(row).
 template <int MT, bool DUAL>
 __device__ __forceinline__ void dl_dma_w(const DlCtx& c, const DlUnit& U, int j, int slot) {
   using L = DlLds<MT>;
   const int sub = c.wave >> 2;
   const int row = 8 * (c.wave & 3) + (c.lane >> 3);
-  const int col = (DUAL ? 0 : 64 * sub) + 16 * (((c.lane & 7) >> 1) ^ (row & 3)) + 8 * (c.lane & 1);
+  const int col = (DUAL ? 0 : 64 * sub) + 16 * (((c.lane & 7) >> 1) ^ dl_wswz(row)) + 8 * (c.lane & 1);
   const void* bp = (DUAL && sub) ? U.b1 : U.b0;
   const uint32_t voff = (uint32_t)row * (uint32_t)U.ldb * 2u + (uint32_t)(U.n0 + col) * 2u;
 #pragma unroll
@@ -380,7 +387,7 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
   // fragment addresses within a slot
   const int sub = c.wave >> 2, lu = c.wave & 3;
   const int k_lo = 8 * c.lg + (c.lr >> 2);
-  const int b_off = L::W_OFF + sub * 4096 + k_lo * 128 + ((lu ^ (k_lo & 3)) << 5) + ((c.lr & 3) << 3);
+  const int b_off = L::W_OFF + sub * 4096 + k_lo * 128 + ((lu ^ dl_wswz(k_lo)) << 5) + ((c.lr & 3) << 3);
   const int abr = DUAL ? sub : 0;
 
   for (int j = 0; j < nk; ++j) {
@@ -630,7 +637,7 @@ __device__ __forceinline__ void dl_contract_dma(const DlCtx& c, const void* ud, 
   static_assert(L::KC == 2, "one 64-k strip per ring stage");
   const int sub = c.wave >> 2, lu = c.wave & 3;
   const int row = 8 * lu + (c.lane >> 3);
-  const int col = 64 * sub + 16 * (((c.lane & 7) >> 1) ^ (row & 3)) + 8 * (c.lane & 1);
+  const int col = 64 * sub + 16 * (((c.lane & 7) >> 1) ^ dl_wswz(row)) + 8 * (c.lane & 1);
   const uint32_t ldb2 = (uint32_t)ld_ud * 2u;
   const uint32_t voff = (uint32_t)row * ldb2 + (uint32_t)col * 2u;
   const bool live = j < NT;  // uniform
@@ -681,7 +688,7 @@ __device__ __forceinline__ void dl_contract_down(const DlCtx& c, const DecLayerP
       fa[kc][mt] = lds_read_b128(c.l0 + L::A_OFF + H::OFF + kc * H::CHUNK + m * 64 + ((c.lg ^ a_swz(m)) << 4));
     }
   const int k_lo = 8 * c.lg + (c.lr >> 2);
-  const int b_off = L::W_OFF + sub * 4096 + k_lo * 128 + ((lu ^ (k_lo & 3)) << 5) + ((c.lr & 3) << 3);
+  const int b_off = L::W_OFF + sub * 4096 + k_lo * 128 + ((lu ^ dl_wswz(k_lo)) << 5) + ((c.lr & 3) << 3);
   const int colo = 64 * sub + 16 * lu + 4 * c.lg;
   const __amdgpu_buffer_rsrc_t rs_sl =
       __builtin_amdgcn_make_buffer_rsrc(p.cslices, 0, (int)dl_contract_bytes(NT, U2, c.T), 0x00020000);

@@ -14,13 +14,13 @@
 // MFMA with the current step's MFMAs (sched_barrier-pinned), so a wave
 // never holds its MFMAs behind a burst of memory instructions:
 //  * A (K contiguous): one 64-byte row per m (four 16-byte chunks), chunk
-//    XOR-swizzled by (row >> 1) & 3; an MFMA fragment is one ds_read_b128
-//    and each 8-lane group of a read touches all 32 banks once.
+//    XOR-swizzled by (row >> 1) & 3; an MFMA fragment is one ds_read_b128,
+//    free of bank conflicts.
 //  * B in the reference's natural (in, out) layout (N contiguous): stored
 //    as it lies in HBM, one 512-byte row per k (256 bytes for tiles of at
 //    most 128 columns, so no DMA lane fetches past the tile and the freed
-//    LDS holds more stages), its 32-byte units XOR-swizzled by k & 3: the
-//    four rows a transposing read touches land on distinct banks.  A fragment (16 columns
+//    LDS holds more stages), its 32-byte units XOR-swizzled by bnat_swz(k):
+//    the rows a transposing read touches land on distinct banks.  A fragment (16 columns
 //    x 8 k) is two ds_read_b64_tr_b16: in each 16-lane group, lane i
 //    receives element i % 4 of the 8-byte pieces addressed by lanes
 //    i/4 + 4j, so pointing lane s at row k + s/4, columns n + 4*(s % 4)
@@ -149,8 +149,24 @@ __device__ __forceinline__ uint32_t add_bf16x2(uint32_t a, uint32_t b) {
 }
 __device__ __forceinline__ u32x2 add_bf16x4(u32x2 a, u32x2 b) { return u32x2{add_bf16x2(a.x, b.x), add_bf16x2(a.y, b.y)}; }
 
-// 32-byte unit swizzle of a natural-layout B row k.
-__device__ __forceinline__ int bnat_swz(int k) { return k & 3; }
+// LDS on gfx950: 64 banks of 4 bytes; a 64-bit read (ds_read_b64_tr_b16 /
+// _b8 included) serves 32 lanes per pass, so lanes 0-15 and 16-31 of a
+// transposing read must not share banks (with the k & 3 / k & 7 swizzles
+// alone they did, and every such read took two passes: SQ_LDS_BANK_CONFLICT
+// equal to the conflict-free active cycles in a probe of the pattern).
+//
+// 32-byte unit swizzle of a natural-layout bf16 B row k (512- or 256-byte
+// rows, which all start at bank 0).  A transposing read's lanes 0-15 touch
+// rows k0..k0+3 and lanes 16-31 rows k0+8..k0+11: bits 0-1 put the four
+// rows of a group on distinct units of one 128-byte half of the banks, bit
+// 2 (k & 8) moves the second group to the other half.
+__device__ __forceinline__ int bnat_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+
+// 16-byte chunk swizzle of an fp8 natural B row k of 256 bytes (one full
+// bank row): lanes 0-15 of a transposing read touch rows k0..k0+7 (bits 0-2
+// spread them over 8 chunks) and lanes 16-31 rows k0+8..k0+15 (bit 3, k & 8,
+// moves them to the other 8 chunks).
+__device__ __forceinline__ int f8nat_swz(int k) { return (k & 7) | (((k >> 3) & 1) << 3); }
 
 // BEPI_STORE_FRAG writes bf16 in fragment order: the 16x16 block (i, j) of
 // wave w of output tile t = m_tile + mtiles * n_tile is 512 contiguous bytes
@@ -294,23 +310,26 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   } else if constexpr (C::FP8_B) {
     // fp8 natural: instruction i fills k-rows 4*(wave + NW*i) + lane/16
     // (256 bytes each); slot lane%16 holds logical 16-byte chunk
-    // (lane%16) ^ (row & 7), i.e. columns 16 * that chunk .. +15.
+    // (lane%16) ^ f8nat_swz(row), i.e. columns 16 * that chunk .. +15.
 #pragma unroll
     for (int i = 0; i < C::B_UNITS; ++i) {
       const int kk = 4 * (wave + NW * i) + (lane >> 4);
-      const int col = 16 * ((lane & 15) ^ (kk & 7));
+      const int col = 16 * ((lane & 15) ^ f8nat_swz(kk));
       b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * (uint32_t)ldb + (uint32_t)(n0 + col) : kOOB;
     }
   } else {
     // instruction i fills RPI k-rows from RPI * (wave + NW * i), LPR lanes per
     // row (512-byte rows: 2 rows of 32 lanes; 256-byte rows: 4 of 16)
+    // (with 4 waves and 512-byte rows the rows of successive instructions
+    // differ by 8, which changes bnat_swz: one column per instruction)
     constexpr int RPI = 1024 / C::B_PITCH, LPR = C::B_PITCH / 16;
-    const int kk = RPI * wave + lane / LPR;
     const int q = lane % LPR;
-    const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
 #pragma unroll
-    for (int i = 0; i < C::B_UNITS; ++i)
-      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)(kk + RPI * NW * i) * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+    for (int i = 0; i < C::B_UNITS; ++i) {
+      const int kk = RPI * (wave + NW * i) + lane / LPR;
+      const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
+      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+    }
   }
 
   // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
@@ -334,34 +353,31 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   const lds_cptr a_rd = l0 + (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
   // B natural: the lane reads k rows k_lo = 8*lg + lr/4 (and k_lo + 4 for
   // the upper half, same swizzle) in 32-byte unit U = wn0/16 + j for
-  // fragment j, stored at unit U ^ (k_lo & 3).  Only the low two bits of U
-  // are swizzled, so with t = j % 4 the unit of fragment j is that of
-  // fragment t plus 4 * (j / 4): fragment j of stage s is at
-  // b_rd[j % 4] + 128 * (j / 4) + s * B_BYTES (+ 2 KB for the upper half).
+  // fragment j, stored at unit U ^ bnat_swz(k_lo): fragment j of stage s is
+  // at b_rd[j] + s * B_BYTES (+ 2 KB for the upper half).
   // B Linear: like A, fragment j of stage s at b_rd[0] + s * B_BYTES + 1 KB * j.
-  lds_cptr b_rd[4];
+  lds_cptr b_rd[FN];
   if constexpr (C::B_KC) {
     const int row0 = wn0 + lr;
     b_rd[0] = l0 + B_REGION + row0 * 64 + ((lg ^ a_swz(row0)) << 4);
-    b_rd[1] = b_rd[2] = b_rd[3] = b_rd[0];
   } else {
     const int k_lo = 8 * lg + (lr >> 2);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int u = (wn0 >> 4) + t;
-      b_rd[t] = l0 + B_REGION + k_lo * C::B_PITCH + (((u & ~3) | ((u & 3) ^ bnat_swz(k_lo))) << 5) + ((lr & 3) << 3);
+    for (int j = 0; j < FN; ++j) {
+      const int u = (wn0 >> 4) + j;
+      b_rd[j] = l0 + B_REGION + k_lo * C::B_PITCH + ((u ^ bnat_swz(k_lo)) << 5) + ((lr & 3) << 3);
     }
   }
   // fp8 B: lane s = lr of group lg points at k-row 8*lg + lr/2, bytes
   // 8*(lr & 1) of 16-byte chunk c = wn0/16 + j (fragment j's 16 columns),
-  // stored at chunk (c & ~7) | ((c & 7) ^ (row & 7)); one base per fragment.
+  // stored at chunk c ^ f8nat_swz(row); one base per fragment.
   lds_cptr b8[C::FP8_B ? FN : 1];
   if constexpr (C::FP8_B) {
     const int row = 8 * lg + (lr >> 1);
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int cc = (wn0 >> 4) + j;
-      b8[j] = l0 + B_REGION + row * C::B_PITCH + (((cc & ~7) | ((cc & 7) ^ (row & 7))) << 4) + ((lr & 1) << 3);
+      b8[j] = l0 + B_REGION + row * C::B_PITCH + ((cc ^ f8nat_swz(row)) << 4) + ((lr & 1) << 3);
     }
   }
 
@@ -391,7 +407,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       f.b[2 * (r - FM) + 1] = u32x2{v.z, v.w};
     } else {
       const int j = (r - FM) >> 1, hi = (r - FM) & 1;
-      f.b[2 * j + hi] = lds_read_tr(b_rd[j & 3] + 128 * (j >> 2) + s * C::B_BYTES + hi * 4 * C::B_PITCH);
+      f.b[2 * j + hi] = lds_read_tr(b_rd[j] + s * C::B_BYTES + hi * 4 * C::B_PITCH);
     }
   };
   constexpr int NREAD = FM + ((C::B_KC || C::FP8_B) ? FN : 2 * FN);

@@ -20,8 +20,8 @@
 //    fragment (16 rows x 128 k: lane l holds row l % 16, k = 32 (l / 16) ..
 //    +31, 32 bytes) is two ds_read_b128;
 //  * B: 128 k-rows x 128 bytes (128 columns) as they lie in HBM, chunks
-//    XOR-swizzled by k & 7; a fragment (16 columns x 128 k, lane l: column
-//    l % 16, the same 32 k as A) is four ds_read_b64_tr_b8.
+//    XOR-swizzled by f8b_swz(k); a fragment (16 columns x 128 k, lane l:
+//    column l % 16, the same 32 k as A) is four ds_read_b64_tr_b8.
 // The MFMA contracts the k of its two operands position by position, so
 // any k order works as long as A and B share it; the one used here is
 // k = 32 (l / 16) + byte for both.  Operands go global -> LDS by direct DMA
@@ -56,6 +56,14 @@ constexpr int kF8ABytes = kF8BM * kF8BK;  // 32 KB
 constexpr int kF8BBytes = kF8BK * kF8BN;  // 16 KB
 constexpr int kF8Stage = kF8ABytes + kF8BBytes;
 static_assert(kF8Stages * kF8Stage <= 160 * 1024, "LDS budget");
+
+// Chunk swizzle of B k-row k (128-byte rows: two per 64-bank row).  A
+// transposing read's lanes 0-15 touch rows k0..k0+7 and lanes 16-31 rows
+// k0+32..k0+39, served in the same pass: k & 7 places each group's rows on
+// 8 distinct 16-byte bank groups (even rows in one half of the banks, odd
+// in the other) and k & 32 flips the chunk's low bit, so the second group
+// takes the 16 bank groups the first leaves free.
+__device__ __forceinline__ int f8b_swz(int k) { return (k & 7) ^ ((k >> 5) & 1); }
 
 // 16 e4m3 x 16 e4m3 over 128 k into a 16x16 fp32 block (unit E8M0 scales).
 __device__ __forceinline__ f32x4 mfma_f8(const u32x4 (&b)[2], const u32x4 (&a)[2], f32x4 c) {
@@ -98,9 +106,10 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
 
   // DMA geometry: instruction i of this wave fills 8 rows (A: m rows, B: k
   // rows) 8 * (wave + NW * i) + lane / 8 of 128 bytes; lane slot lane % 8
-  // holds logical chunk (lane % 8) ^ (row & 7).  Rows or columns outside the
-  // matrix take an offset past the records and fetch zeros; the stage's k
-  // goes into the scalar offset (stages wholly past kend use r_none).
+  // holds logical chunk (lane % 8) ^ (A: row & 7, B: f8b_swz(row)).  Rows or
+  // columns outside the matrix take an offset past the records and fetch
+  // zeros; the stage's k goes into the scalar offset (stages wholly past
+  // kend use r_none).
   uint32_t a_voff[A_UNITS], b_voff[B_UNITS];
 #pragma unroll
   for (int i = 0; i < A_UNITS; ++i) {
@@ -111,7 +120,7 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
 #pragma unroll
   for (int i = 0; i < B_UNITS; ++i) {
     const int kr = 8 * (wave + NW * i) + (lane >> 3);
-    const int col = 16 * ((lane & 7) ^ (kr & 7));
+    const int col = 16 * ((lane & 7) ^ f8b_swz(kr));
     b_voff[i] = n0 + col < p.N ? (uint32_t)((int64_t)kr * p.ldb) + (uint32_t)(n0 + col) : kOOB;
   }
   auto dma_one = [&](int kt, int s, int d) {
@@ -138,7 +147,7 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int cc = (wn0 >> 4) + j;
-    b_rd[j] = l0 + B_REGION + bk * 128 + ((cc ^ (bk & 7)) << 4) + ((lr & 1) << 3);
+    b_rd[j] = l0 + B_REGION + bk * 128 + ((cc ^ f8b_swz(bk)) << 4) + ((lr & 1) << 3);
   }
 
   f32x4 acc[FM][FN];
@@ -159,7 +168,8 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
       f.a[i][r & 1] = lds_read_b128((r & 1 ? a_rd1 : a_rd0) + s * kF8ABytes + 16 * 128 * i);
     } else {
       const int j = (r - 2 * FM) >> 2, q = (r - 2 * FM) & 3;
-      // k-row + 8 q keeps k-row & 7, so the swizzle is that of q = 0
+      // k-row + 8 q keeps k-row & 7 and k-row & 32 (k-row % 32 + 8 q < 32),
+      // so the swizzle is that of q = 0
       f.b[j][q] = lds_read_tr8(b_rd[j] + s * kF8BBytes + 8 * 128 * q);
     }
   };
