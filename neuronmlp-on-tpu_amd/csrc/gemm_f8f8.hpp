@@ -17,17 +17,21 @@
 //
 // One k-step is 128 k (one MFMA deep).  LDS holds 3 stages of 48 KB:
 //  * A: 256 rows x 128 bytes, 16-byte chunks XOR-swizzled by row & 7; a
-//    fragment (16 rows x 128 k: lane l holds row l % 16, k = 32 (l / 16) ..
-//    +31, 32 bytes) is two ds_read_b128;
+//    fragment (16 rows x 128 k, lane l: row l % 16, 32 bytes) is two
+//    ds_read_b128, chunks l / 16 and l / 16 + 4;
 //  * B: 128 k-rows x 128 bytes (128 columns) as they lie in HBM, chunks
 //    XOR-swizzled by f8b_swz(k); a fragment (16 columns x 128 k, lane l:
 //    column l % 16, the same 32 k as A) is four ds_read_b64_tr_b8.
 // The MFMA contracts the k of its two operands position by position, so
-// any k order works as long as A and B share it; the one used here is
-// k = 32 (l / 16) + byte for both.  Operands go global -> LDS by direct DMA
-// (buffer_load ... lds), six 1 KB instructions per wave and stage (4 A, 2
-// B); the DMA of stage kt + 3 and the fragment reads of stage kt + 1 are
-// interleaved with the MFMAs of stage kt, as in the bf16 kernel.
+// any k order works as long as A and B share it.  The one used here: byte
+// b of lane group g = l / 16 is k = 16 g + b for b < 16 and 64 + 16 g +
+// (b - 16) above.  With it each A read takes chunk g (or g + 4) of its row,
+// which an LDS probe measured at the rate of a linear read; chunks 2 g and
+// 2 g + 1 (k = 32 g + b) took 1.65 times as long.  Operands go global ->
+// LDS by direct DMA (buffer_load ... lds), 1 KB instructions (per wave and
+// stage: 8 A and 4 B with 4 waves, 4 and 2 with 8); the DMA of stage
+// kt + 3 and the fragment reads of stage kt + 1 are interleaved with the
+// MFMAs of stage kt, as in the bf16 kernel.
 #pragma once
 
 #include "gemm_big.hpp"
@@ -59,11 +63,11 @@ static_assert(kF8Stages * kF8Stage <= 160 * 1024, "LDS budget");
 
 // Chunk swizzle of B k-row k (128-byte rows: two per 64-bank row).  A
 // transposing read's lanes 0-15 touch rows k0..k0+7 and lanes 16-31 rows
-// k0+32..k0+39, served in the same pass: k & 7 places each group's rows on
+// k0+16..k0+23, served in the same pass: k & 7 places each group's rows on
 // 8 distinct 16-byte bank groups (even rows in one half of the banks, odd
-// in the other) and k & 32 flips the chunk's low bit, so the second group
+// in the other) and k & 16 flips the chunk's low bit, so the second group
 // takes the 16 bank groups the first leaves free.
-__device__ __forceinline__ int f8b_swz(int k) { return (k & 7) ^ ((k >> 5) & 1); }
+__device__ __forceinline__ int f8b_swz(int k) { return (k & 7) ^ ((k >> 4) & 1); }
 
 // 16 e4m3 x 16 e4m3 over 128 k into a 16x16 fp32 block (unit E8M0 scales).
 __device__ __forceinline__ f32x4 mfma_f8(const u32x4 (&b)[2], const u32x4 (&a)[2], f32x4 c) {
@@ -105,11 +109,11 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
   const uint32_t lbase = lds_addr(lds);
 
   // DMA geometry: instruction i of this wave fills 8 rows (A: m rows, B: k
-  // rows) 8 * (wave + NW * i) + lane / 8 of 128 bytes; lane slot lane % 8
-  // holds logical chunk (lane % 8) ^ (A: row & 7, B: f8b_swz(row)).  Rows or
-  // columns outside the matrix take an offset past the records and fetch
-  // zeros; the stage's k goes into the scalar offset (stages wholly past
-  // kend use r_none).
+  // rows) 8 * (wave + NW * i) + lane / 8 of 128 bytes (whole 128-byte
+  // lines); lane slot lane % 8 holds logical chunk (lane % 8) ^ (A: row & 7,
+  // B: f8b_swz(row)).  Rows or columns outside the matrix take an offset past
+  // the records and fetch zeros; the stage's k goes into the scalar offset
+  // (stages wholly past kend use r_none).
   uint32_t a_voff[A_UNITS], b_voff[B_UNITS];
 #pragma unroll
   for (int i = 0; i < A_UNITS; ++i) {
@@ -134,15 +138,15 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
   };
 
   // Fragment addresses within a stage.  A fragment i: row wm0 + 16 i + lr,
-  // chunks 2 lg and 2 lg + 1 (row & 7 is lr & 7 for every i).  B fragment
-  // j, read q: lane lr points at k-row 32 lg + 8 q + lr / 2, byte 8 (lr & 1)
-  // of column chunk c = (wn0 + 16 j) / 16 (swizzled by that k-row & 7 =
-  // lr / 2).
+  // chunks lg (k 16 lg ..) and lg + 4 (k 64 + 16 lg ..); row & 7 is lr & 7
+  // for every i.  B fragment j, read q: lane lr points at k-row 16 lg +
+  // 8 (q & 1) + 64 (q >> 1) + lr / 2, byte 8 (lr & 1) of column chunk
+  // c = (wn0 + 16 j) / 16, giving the lane bytes 8 q .. 8 q + 7 of its k
+  // order.
   const lds_cptr l0 = (lds_cptr)lds;
-  const int sw = lr & 7;
-  const lds_cptr a_rd0 = l0 + (wm0 + lr) * 128 + (((2 * lg) ^ sw) << 4);
-  const lds_cptr a_rd1 = l0 + (wm0 + lr) * 128 + (((2 * lg + 1) ^ sw) << 4);
-  const int bk = 32 * lg + (lr >> 1);
+  const lds_cptr a_rd0 = l0 + (wm0 + lr) * 128 + ((lg ^ (lr & 7)) << 4);
+  const lds_cptr a_rd1 = l0 + (wm0 + lr) * 128 + (((lg + 4) ^ (lr & 7)) << 4);
+  const int bk = 16 * lg + (lr >> 1);
   lds_cptr b_rd[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
@@ -168,9 +172,9 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
       f.a[i][r & 1] = lds_read_b128((r & 1 ? a_rd1 : a_rd0) + s * kF8ABytes + 16 * 128 * i);
     } else {
       const int j = (r - 2 * FM) >> 2, q = (r - 2 * FM) & 3;
-      // k-row + 8 q keeps k-row & 7 and k-row & 32 (k-row % 32 + 8 q < 32),
-      // so the swizzle is that of q = 0
-      f.b[j][q] = lds_read_tr8(b_rd[j] + s * kF8BBytes + 8 * 128 * q);
+      // the row offsets 8 and 64 keep k-row & 7 and k-row & 16 (k-row % 16
+      // + 8 < 16), so the swizzle is that of q = 0
+      f.b[j][q] = lds_read_tr8(b_rd[j] + s * kF8BBytes + 128 * (8 * (q & 1) + 64 * (q >> 1)));
     }
   };
   constexpr int NMFMA = FM * FN;  // 16 or 32
