@@ -593,17 +593,21 @@ namespace {
 // depend on the device queried):
 //   rounds * (k-steps per split * cycles per step + fixed cost per block)
 //   + per fp32 slice: writing it and reading it back in the reduction.
-// The constants are measured on MI355X: a 32-k step costs ~41 cycles per
-// MFMA of the wave tile (64 x 32*fn), prologue + epilogue ~20k cycles, and
-// a slice byte ~0.00045 cycles each way (~4 TB/s at ~1.8 GHz).
+// The constants are measured on MI355X: a 32-k step of a 256 x 256 tile
+// costs ~1312 cycles (41 per MFMA of the 64 x 128 wave tile), of which ~60%
+// does not shrink with the tile width (the 256-row A tile, the barrier): a
+// 256 x 192 step took ~0.9 of a 256 x 256 one in the X.U stages, hence
+// 787 + 65.6 * fn; prologue + epilogue ~20k cycles, and a slice byte
+// ~0.00045 cycles each way (~4 TB/s at ~1.8 GHz).
 // N1 >= 0: a second batch entry N1 columns wide (its own column tiles);
-// otherwise `batch` entries of N columns.
-int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch, int64_t N1 = -1) {
+// otherwise `batch` entries of N columns.  *cost_out (if given) receives the
+// model's cost of the chosen split.
+int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch, int64_t N1 = -1, double* cost_out = nullptr) {
   const int64_t cus = tune().split;
   const int64_t bn = 32 * fn;
   const int64_t ntl = N1 >= 0 ? (N + bn - 1) / bn + (N1 + bn - 1) / bn : ((N + bn - 1) / bn) * batch;
   const int64_t tiles = ((T + 255) / 256) * ntl;
-  const double c_step = 41.0 * 4 * fn, c_block = 20000.0;
+  const double c_step = 787.0 + 65.6 * fn, c_block = 20000.0;
   const double c_slice = 0.0009 * (double)T * (double)(N1 >= 0 ? N + N1 : batch * N) * 4.0;
   int64_t best_ks = K;
   double best = -1.0;
@@ -619,7 +623,30 @@ int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch, int64_t N1 =
       best_ks = ks;
     }
   }
+  if (cost_out) *cost_out = best;
   return (int)std::min<int64_t>(best_ks, K);
+}
+
+// Tile width (columns / 32) of the gate/up X.U stage: SVDMLP_TUNE s1g, else
+// the split planner's cheaper of 256 x 256 and 256 x 192 tiles up to 2048
+// tokens.  256 x 192 tiles fill the last round of blocks better where
+// 256 x 256 leave it part-empty (70B fp8 layer, T=2048: 352 blocks of
+// 256 x 256 in 1.4 rounds against 480 of 256 x 192 in 1.9; the stage 360-371
+// -> 310-316 us, the layer 2236-2243 -> 2208-2210 us, 1884-1892 -> 1838-1856
+// with e4m3 h; 8B layer, us per layer: T=160 178.7 -> 177.7, T=256 191.9 ->
+// 191.1, T=512 249.6 -> 247.5, T=1024 343.7-344.5 -> 341.1-341.6; same box,
+// alternating runs).  The model keeps 256 x 256 at T=768 (3 splits of 66
+// tiles against 2 of 90: 256 x 192 measured 303.9 -> 308.5 us there).  At
+// 4096 tokens (the 32-layer stack) 256 x 256 measured 0.5% faster per stack
+// in the same runs, so it stays there.
+int gate_xu_fn(int64_t T, int64_t K, int64_t r, int batch, int64_t r1 = -1) {
+  if (tune().s1g) return tune().s1g;
+  const int fn = tune().s1;
+  if (fn != 8 || T > 2048) return fn;
+  double c8 = 0.0, c6 = 0.0;
+  plan_ksplit(T, K, r, 8, batch, r1, &c8);
+  plan_ksplit(T, K, r, 6, batch, r1, &c6);
+  return c6 < c8 ? 6 : 8;
 }
 
 int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
@@ -644,7 +671,7 @@ FactorLd dense_ld(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d) { return Fac
 // workspace's slice area, else one split.
 int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
             int T, int K, int r, int r1, char* ws, const Ws& L, const float* const* su, int64_t ldu, int64_t ldu1) {
-  const int fn = tune().s1g ? tune().s1g : tune().s1;
+  const int fn = gate_xu_fn(T, K, r, 2, r1);
   const int nw = big_nw(fn, BEPI_STORE, u_lin);
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
   const int64_t ldb0 = u_lin ? K : (ldu ? ldu : r), ldb1 = u_lin ? K : (ldu1 ? ldu1 : r1);
@@ -684,7 +711,7 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
            int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr,
            int64_t ldu = 0) {
-  const int fn = stage == ST_GU_XU && tune().s1g ? tune().s1g : tune().s1;
+  const int fn = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : tune().s1;
   int ks = plan_ksplit(T, K, r, fn, batch);
   int splits = (K + ks - 1) / ks;
   {  // the slices must fit the workspace's slice area (sized for the planned tiles)
