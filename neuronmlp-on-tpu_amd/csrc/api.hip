@@ -437,6 +437,7 @@ struct Tune {
   int gusfn = 0;       // split gate/up XU.V passes at one row tile: tile columns / 32 (0: 4)
   int gusp = 0;        // ... and their K splits (0: CUs / tiles, at most 4)
   int f8nw = 4;        // waves per block of the fp8 x fp8 GEMM (4: 70B h.Ud 309 -> 293 us against 8)
+  bool p2split = true;  // decode layer phase 2 with one branch per unit from two token tiles up
 };
 
 const Tune& tune();
@@ -495,6 +496,7 @@ const Tune& tune() {
         if (k == "gvrw") r.gvrw = v;
         if (k == "nw") r.nw = v;
         if (k == "f8nw") r.f8nw = v == 4 ? 4 : 8;
+        if (k == "p2split") r.p2split = v != 0;
       }
       pos = end + 1;
     }
@@ -1026,6 +1028,14 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.r_d = (int)r_d;
   p.ks1 = dl_plan(d, 2 * r_gu / 128, grid, &p.units1);
   p.units2 = (int)(ff / 64);
+  // From two 16-row token tiles up, phase 2 runs one branch per unit over
+  // 128 columns (units 2t, 2t+1: g and u of tile t) instead of both over 64:
+  // each unit streams the T x r_gu activations of one branch per 128 weight
+  // columns, half the activation bytes per weight byte, and the pair meets
+  // through a tile counter after phases 1, 3 and 4's.
+  const int64_t nt2 = ff / 128;
+  p.p2split = !contract && mt >= 2 && ff % 128 == 0 && 2 * nt2 <= grid &&
+              2 * r_gu / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles && tune().p2split;
   p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
   p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
   p.splits1 = p.units1 / (int)(2 * r_gu / 128);

@@ -69,6 +69,11 @@ hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStr
     *why = "decode layer: the RMSNorm instance takes d <= 16384, a block per token and the block's buffers";
     return hipErrorInvalidValue;
   }
+  if (p.p2split && (contract || p.ff % 128 || p.units2 > grid || p.units2 != 2 * (p.ff / 128) ||
+                    2 * (p.r_gu / 128) + p.r_d / 128 + p.d / 128 + p.ff / 128 > kDlMaxTiles)) {
+    *why = "decode layer: one-branch phase 2 takes ff % 128 == 0, a block per unit and a counter per column tile";
+    return hipErrorInvalidValue;
+  }
   hipError_t e;
   if (contract) {
     // one unit per h strip plus one combining block per XU_d tile

@@ -87,6 +87,11 @@ struct DecLayerParams {
   int splits1, splits3, splits4;       // splits per tile, phases 1, 3 and 4
   int ld_u, ld_v, ld_ud, ld_vd;        // row pitch (elements) of ug and uu, vg and vu, ud, vd
   int a_cached;                        // activation DMAs through the caches (workspace 128-byte aligned)
+  // Phase 2 with one branch per unit: unit u = 2 t + b computes g (b = 0) or
+  // u (b = 1) over 128 columns 128 t..; the pair meets through a tile
+  // counter after phases 1, 3 and 4's.  Otherwise a unit computes both over
+  // 64 columns.
+  int p2split;
   // MLP block (null otherwise): y = bf16(resid + bf16(MLP)); with `gain`
   // (NORM instances) a phase 0 writes RMSNorm(x) to xn, which phase 1 reads
   // instead of x.
@@ -420,6 +425,54 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
   }
   dl_wait_vm<0>();  // drain run-out DMAs before the ring is reused
   dl_block_sync();
+}
+
+// Phase 2 with one branch per unit (DecLayerParams::p2split): unit u holds
+// g (u even) or u (u odd) of 128 columns from U.n0 in acc (the lane layout
+// of dl_combine).  It stores its rows < T as slice u and counts its arrival
+// on the column tile's counter; the second of the pair resets the counter,
+// loads the other unit's slice and writes h = bf16(SiLU(g) * u) -- the same
+// fp32 operands, so the same bits, as a unit that computes both branches.
+template <int MT>
+__device__ __forceinline__ void dl_swiglu_pair(const DlCtx& c, const DlUnit& U, const f32x4 (&acc)[MT], int u,
+                                               uint32_t* cnt, float* slices, int* flag, uint16_t* h) {
+  const int n = U.n0 + 64 * (c.wave >> 2) + 16 * (c.wave & 3) + 4 * c.lg;
+  const __amdgpu_buffer_rsrc_t rs = dl_slice_rsrc<MT>(slices);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t off = 16 * mt + c.lr < c.T ? (uint32_t)(((u * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y),
+                                                 __float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)},
+                                           rs, off, 0, kDlSc1);
+  }
+  dl_wait_vm<0>();
+  dl_block_sync();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == 2u;
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  dl_block_sync();
+  if (!*flag) return;
+  u32x4 v[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t off =
+        16 * mt + c.lr < c.T ? (uint32_t)((((u ^ 1) * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+    v[mt] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kDlSc1);
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = 16 * mt + c.lr;
+    if (m < c.T) {
+      const f32x4 o = f32x4{__uint_as_float(v[mt].x), __uint_as_float(v[mt].y), __uint_as_float(v[mt].z),
+                            __uint_as_float(v[mt].w)};
+      const f32x4 g = (u & 1) ? o : acc[mt], uv = (u & 1) ? acc[mt] : o;
+      dl_store8(h + (int64_t)m * U.ldo + n, u32x2{dl_pack_bf16x2(silu_f32(g.x) * uv.x, silu_f32(g.y) * uv.y),
+                                                  dl_pack_bf16x2(silu_f32(g.z) * uv.z, silu_f32(g.w) * uv.w)});
+    }
+  }
 }
 
 // Split-K combination of unit u = tile + split * nt (splits per tile) into
@@ -845,6 +898,19 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       U.ke = min(p.d, U.kb + p.ks1);
       U.dst = p.xu16 + (int64_t)br * T * p.r_gu;
       U.ldo = p.r_gu;
+    } else if (phase == 2 && p.p2split) {
+      const int br = u & 1;
+      U.a0 = U.a1 = p.xu16 + (int64_t)br * T * p.r_gu;
+      U.lda = p.r_gu;
+      U.a_bytes = (uint32_t)((int64_t)T * p.r_gu * 2);
+      U.b0 = U.b1 = br ? p.vu : p.vg;
+      U.ldb = p.ld_v;
+      U.b_bytes = (uint32_t)((int64_t)p.r_gu * p.ld_v * 2);
+      U.n0 = (u >> 1) * 128;
+      U.kb = 0;
+      U.ke = p.r_gu;
+      U.dst = p.h;
+      U.ldo = p.ff;
     } else if (phase == 2) {
       U.a0 = p.xu16;
       U.a1 = p.xu16 + (int64_t)T * p.r_gu;
@@ -897,7 +963,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       DlUnit U;
       unit_of(phase, b, U);
       for (int s = 0; s < NS - 1; ++s) {
-        if (phase == 2)
+        if (phase == 2 && !p.p2split)
           dl_dma_w<MT, true>(c, U, s, s);
         else
           dl_dma_w<MT, false>(c, U, s, s);
@@ -952,6 +1018,17 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     dl_wait_vm<0>();
     grid_sync(4);
   } else {
+  if (p.p2split) {
+    // ---- phase 2, one branch per unit: g or u of 128 columns; the second
+    // unit of each pair to finish writes h = bf16(SiLU(g) * u) ----
+    for (int u = b; u < units[2]; u += G) {
+      DlUnit U;
+      unit_of(2, u, U);
+      f32x4 acc[MT];
+      dl_run<MT, false>(c, U, u == b, acc);
+      dl_swiglu_pair<MT>(c, U, acc, u, dl_tile_counter(p.sync, nt1 + nt3 + nt4 + (u >> 1)), p.slices, flag, p.h);
+    }
+  } else {
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
   for (int u = b; u < units[2]; u += G) {
     DlUnit U;
@@ -979,6 +1056,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       }
     }
     dl_block_sync();
+  }
   }
   dl_wait_vm<0>();
   grid_sync(3);
