@@ -9,20 +9,23 @@
 //    of one or two 32-k chunks (by token count: the activation tile shares
 //    the ring).  A chunk is 32 k x 128 columns, stored as two 64-column
 //    sub-tiles of 128-byte rows whose 32-byte units are XOR-swizzled by
-//    k & 3, and read with the transposing ds_read_b64_tr_b16, so no
+//    dl_wswz(k), and read with the transposing ds_read_b64_tr_b16, so no
 //    register transpose exists;
 //  * the activation rows (zero-padded to 16 * MT) follow in the same ring;
 //  * the layer runs as four phases separated by three grid barriers:
 //      1  XU_g, XU_u = X . [Ug | Uu]                (split-K)
-//      2  h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu))    (a block owns 64 columns
-//         of both branches over the whole rank: no split)
+//      2  h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu))    (whole rank, no split: a
+//         block owns 64 columns of both branches at one token tile, else
+//         128 columns of one branch, the g and u units of a column tile
+//         meeting through its counter)
 //      3  XU_d = h . Ud                              (split-K)
 //      4  y = XU_d . Vd                              (split-K)
 //  * split-K tiles (128 columns) are combined without atomics or a zero
 //    fill: every unit stores its fp32 accumulators, in register order, as a
 //    slice of the workspace and counts its arrival on the tile's counter;
-//    the block whose arrival completes the count adds the other slices to
-//    its registers and rounds the tile to bf16 once: XU and XU_d (the
+//    the block whose arrival completes the count sums every slice, its own
+//    included, in split order (so replays are bitwise identical) and rounds
+//    the tile to bf16 once: XU and XU_d (the
 //    reference rounds the rank-r intermediate to the activation dtype) and y
 //    itself, so phases 2 to 4 stream bf16 activations and no barrier
 //    follows phase 4 (fp32 atomics onto shared sums cost ~20 us per phase at
