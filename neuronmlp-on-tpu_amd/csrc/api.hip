@@ -437,7 +437,7 @@ struct Tune {
   int gusfn = 0;       // split gate/up XU.V passes at one row tile: tile columns / 32 (0: 4)
   int gusp = 0;        // ... and their K splits (0: CUs / tiles, at most 4)
   int f8nw = 4;        // waves per block of the fp8 x fp8 GEMM (4: 70B h.Ud 309 -> 293 us against 8)
-  bool p2split = true;  // decode layer phase 2 with one branch per unit from two token tiles up
+  int p2split = 1;     // decode layer phase 2 with one branch per unit: 0 never, 1 where it pays (below), 2 always
 };
 
 const Tune& tune();
@@ -496,7 +496,7 @@ const Tune& tune() {
         if (k == "gvrw") r.gvrw = v;
         if (k == "nw") r.nw = v;
         if (k == "f8nw") r.f8nw = v == 4 ? 4 : 8;
-        if (k == "p2split") r.p2split = v != 0;
+        if (k == "p2split") r.p2split = v;
       }
       pos = end + 1;
     }
@@ -1028,14 +1028,21 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.r_d = (int)r_d;
   p.ks1 = dl_plan(d, 2 * r_gu / 128, grid, &p.units1);
   p.units2 = (int)(ff / 64);
-  // From two 16-row token tiles up, phase 2 runs one branch per unit over
-  // 128 columns (units 2t, 2t+1: g and u of tile t) instead of both over 64:
-  // each unit streams the T x r_gu activations of one branch per 128 weight
-  // columns, half the activation bytes per weight byte, and the pair meets
-  // through a tile counter after phases 1, 3 and 4's.
+  // Phase 2 with one branch per unit over 128 columns (units 2t, 2t+1: g
+  // and u of tile t) instead of both over 64; the pair meets through a tile
+  // counter after phases 1, 3 and 4's.  From two 16-row token tiles up each
+  // unit then streams half the activation bytes per weight byte (8B layer,
+  // T=32 / 64 / 128: 77.7 / 94.8 / 140.9 -> 76.0 / 91.7 / 130.2 us).  At one
+  // tile it pays with dense factors only: their 4 KB-multiple V row pitch
+  // maps the two-branch units' 128-byte column pieces onto a subset of the
+  // HBM channels, and 256-byte pieces spread them (T=4 / 8 / 16: 75.8 / 76.4
+  // / 78.2 -> 73.2 / 73.5 / 75.0 us); with padded rows the pair's extra
+  // slice round trip costs ~1 us there (T=8 69.3 -> 70.4 us).
   const int64_t nt2 = ff / 128;
-  p.p2split = !contract && mt >= 2 && ff % 128 == 0 && 2 * nt2 <= grid &&
-              2 * r_gu / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles && tune().p2split;
+  const bool p2_pays = mt >= 2 || ld.dense;
+  p.p2split = !contract && ff % 128 == 0 && 2 * nt2 <= grid &&
+              2 * r_gu / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles &&
+              (tune().p2split >= 2 || (tune().p2split == 1 && p2_pays));
   p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
   p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
   p.splits1 = p.units1 / (int)(2 * r_gu / 128);
