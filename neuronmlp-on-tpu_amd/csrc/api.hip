@@ -1000,6 +1000,13 @@ bool decode_contract_ok(int64_t T, int64_t ff, int64_t r_gu, int64_t r_d, const 
   return grid > 0 && ff / 64 + r_d / 128 <= grid;
 }
 
+// Phase 2 with one branch per unit fits the shape: ff in whole 128-column
+// tiles, a block per unit and one more tile counter per column tile.
+bool p2split_fits(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int grid) {
+  const int64_t nt2 = ff / 128;
+  return ff % 128 == 0 && 2 * nt2 <= grid && 2 * r_gu / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles;
+}
+
 int decode_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
                  const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
                  char* ws, const Ws& L, const FactorLd& ld, bool contract = false) {
@@ -1038,10 +1045,8 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   // HBM channels, and 256-byte pieces spread them (T=4 / 8 / 16: 75.8 / 76.4
   // / 78.2 -> 73.2 / 73.5 / 75.0 us); with padded rows the pair's extra
   // slice round trip costs ~1 us there (T=8 69.3 -> 70.4 us).
-  const int64_t nt2 = ff / 128;
   const bool p2_pays = mt >= 2 || ld.dense;
-  p.p2split = !contract && ff % 128 == 0 && 2 * nt2 <= grid &&
-              2 * r_gu / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles &&
+  p.p2split = !contract && p2split_fits(d, ff, r_gu, r_d, grid) &&
               (tune().p2split >= 2 || (tune().p2split == 1 && p2_pays));
   p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
   p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
@@ -1590,15 +1595,22 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
   // With padded V rows the MFMA decode layer is the faster one at every T
   // (8B layer at T=1: 75.5 us against 78 us): the streaming-GEMV layer reads
   // whole 1 KB row pieces, which the padding does not spread over channels.
-  // The contracted instance first wherever it applies (asked for, or where
-  // it is the fastest), then the streaming-GEMV layer, then the
-  // three-barrier MFMA layer.
-  const bool contract =
-      contract_asked || (tune().contract && T <= (ld.dense ? kDlContractAutoDense : kDlContractAutoPadded));
+  // With dense factors the three-barrier MFMA layer runs one-branch phase-2
+  // units at every T where they fit (decode_layer), and then beats the
+  // contracted and the streaming-GEMV layers too (8B layer, dense V, T=1 / 2
+  // / 3: 72.6 / 71.7 / 71.6 us against 73.2 / 74.0 / 75.0 contracted and
+  // 78.0 / 81.3 (T=1 / 2) streaming-GEMV).  Otherwise the contracted instance
+  // first wherever it applies (asked for, or where it is the fastest), then
+  // the streaming-GEMV layer, then the three-barrier MFMA layer.
   const bool mfma_layer = decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld);
+  const bool dense_p2 = mfma_layer && ld.dense && tune().p2split > 0 &&
+                        p2split_fits(d, ff, r_gu, r_d, decode_layer_grid(decode_layer_mt((int)T)));
+  const bool contract =
+      contract_asked ||
+      (tune().contract && !dense_p2 && T <= (ld.dense ? kDlContractAutoDense : kDlContractAutoPadded));
   if (mfma_layer && contract && decode_contract_ok(T, ff, r_gu, r_d, L, ws_bytes))
     return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld, true);
-  if (!(mfma_layer && !ld.dense) && gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld)) {
+  if (!(mfma_layer && (!ld.dense || dense_p2)) && gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld)) {
     if ((rc = normed())) return rc;
     return gemv_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld);
   }

@@ -25,12 +25,34 @@ GEMV_LAYER_MAX_T = 2   # kGvMaxT in csrc/decode_gemv.hpp
 CONTRACT_AUTO_T = {True: 1, False: 3}
 
 
+def _mfma_layer(shape):
+    """Whether the MFMA decode layers take a bf16 natural-layout shape (d and
+    ranks multiples of 128, ff of 64)."""
+    return shape.d % 128 == 0 and shape.r % 128 == 0 and shape.rd % 128 == 0 and shape.ff % 64 == 0
+
+
+def _p2split_fits(shape, cus=256, max_tiles=384):
+    """Whether the MFMA decode layer can run one-branch phase-2 units (ff in
+    whole 128-column tiles, a block per unit, a counter per column tile): with
+    dense factors it then takes every decode token count."""
+    nt2 = shape.ff // 128
+    return (shape.ff % 128 == 0 and 2 * nt2 <= cus
+            and 2 * (shape.r // 128) + shape.rd // 128 + shape.d // 128 + nt2 <= max_tiles)
+
+
 def _contracted(shape, T, padded=False):
     """Whether a bf16 natural-layout call runs the contracted decode layer by
     default: its token counts, d and ranks multiples of 128, ff of 64, gate/up
-    rank >= 320, a block per h strip and per XU_d tile (256 CUs)."""
-    return (T <= CONTRACT_AUTO_T[padded] and shape.d % 128 == 0 and shape.r % 128 == 0 and shape.rd % 128 == 0
-            and shape.ff % 64 == 0 and shape.r >= 320 and shape.ff // 64 + shape.rd // 128 <= 256)
+    rank >= 320, a block per h strip and per XU_d tile (256 CUs); with dense
+    factors only where one-branch phase-2 units do not fit."""
+    return (T <= CONTRACT_AUTO_T[padded] and _mfma_layer(shape) and shape.r >= 320
+            and shape.ff // 64 + shape.rd // 128 <= 256 and (padded or not _p2split_fits(shape)))
+
+
+def _gemv_layer(shape, T):
+    """Whether a dense bf16 call at decode shapes runs the streaming-GEMV
+    layer by default (up to 2 tokens, where neither MFMA layer runs)."""
+    return T <= GEMV_LAYER_MAX_T and not _contracted(shape, T) and not (_mfma_layer(shape) and _p2split_fits(shape))
 
 
 def _to(a, dtype, dev):
@@ -234,9 +256,10 @@ def _tile_counters(ws):
     (inputs.LayerShape(16640, 1024, 128), (8, 64)),                     # 130 output tiles: phase 4 unsplit
 ])
 def test_decode_layer_workspace_reuse(gpu, shape, Ts):
-    """The persistent decode kernels (the contracted layer at 1-3 tokens of dense factors, the
-    streaming-GEMV layer up to 2 tokens where the former does not run, the
-    MFMA layer above; one launch each, grid barriers and split-K tile
+    """The persistent decode kernels (the three-barrier MFMA layer, or where
+    its one-branch phase 2 does not fit the contracted layer at 1-3 tokens of
+    dense factors and the streaming-GEMV layer up to 2 tokens; one launch
+    each, grid barriers and split-K tile
     counters in the workspace's first 4096 bytes) over one reused workspace:
     results match the oracle, every call advances the shared barrier
     generation by its barriers, no barrier times out and every tile counter
@@ -251,7 +274,7 @@ def test_decode_layer_workspace_reuse(gpu, shape, Ts):
         err = _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16"))
         assert err < BF16_TOL, (T, err)
         # contracted layer: 2 barriers, GEMV layer: 4, MFMA layer: 3
-        gen += 2 if _contracted(shape, T) else (4 if T <= GEMV_LAYER_MAX_T else 3)
+        gen += 2 if _contracted(shape, T) else (4 if _gemv_layer(shape, T) else 3)
         assert _barrier_state(ws) == (gen, 0), T
         assert not any(_tile_counters(ws)), T
 
@@ -365,7 +388,7 @@ def test_replay_is_bitwise_identical(gpu, layer8b, T, padded):
 
 @pytest.mark.parametrize("T,padded", [(1, True), (3, False), (8, False), (40, False), (100, True)])
 def test_decode_activation_reads_through_the_caches(gpu, T, padded):
-    """The MFMA decode layers (contracted at 1 and 3 tokens) read the bf16
+    """The MFMA decode layers (contracted at 1 token with padded rows) read the bf16
     activation tiles that other blocks of the same launch wrote (XU, h, XU_d)
     through the caches when the workspace is 128-byte aligned, device-scope
     when it is not.  On a layer small enough (3 MB of factors) that its lines
@@ -397,7 +420,7 @@ def test_decode_activation_reads_through_the_caches(gpu, T, padded):
     (inputs.LayerShape(1040, 2064, 400, 272), 1, False),   # streaming-GEMV layer
     (inputs.LayerShape(1040, 2064, 400, 272), 2, False),   # GEMV, ragged strips
     (inputs.LayerShape(1024, 2048, 512), 4, True),         # contracted layer (asked for): tile-combine waits too
-    (inputs.LayerShape(1024, 2048, 512), 1, False)])       # contracted layer (the default at 1 token)
+    (inputs.LayerShape(1024, 2048, 512), 1, False)])       # MFMA layer, one-branch phase 2 at one token tile (dense)
 def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T, contracted):
     """A persistent decode launch whose grid-barrier waits give up (forced
     from the host with a bound of one poll, so every block still runs to its
