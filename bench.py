@@ -13,7 +13,8 @@ The JSON line also carries:
                 algorithmic FLOP per launch / average launch duration vs the
                 2.5 PFLOP/s bf16 MFMA peak
   decode        T = 1, 8, 32, 64 decode layers: us/layer
-                and GB/s of compulsory bytes vs the 8 TB/s HBM peak; block_us
+                and GB/s of compulsory bytes vs the 8 TB/s HBM peak and vs
+                this box's measured copy and streaming-read rates; block_us
                 is the MLP block (RMSNorm, layer, residual) at the same T
   cpu_baseline  the numpy oracle (oracle/reference_cpu.py) timed on this
                 host's cores on a bounded row sample of the same layer
@@ -201,6 +202,37 @@ def _cpu_baseline(layer0, x, T, seconds):
     }, y
 
 
+def _read_rate(torch, stream, buf, blocks=8192, reps=6):
+    """Streaming-read rate (GB/s) of `buf` (a device tensor, whole 16-byte
+    words) by the probe library libhbmread.so (csrc/probe/hbm_read.hip,
+    built with libsvdmlp.so): best of `reps` launches timed by events on
+    `stream`, the stream the probe is launched on."""
+    import ctypes
+
+    path = ROOT / "neuronmlp-on-tpu_amd" / "svdmlp" / "libhbmread.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+    lib = ctypes.CDLL(str(path))
+    lib.hbm_read_words.restype = ctypes.c_int
+    lib.hbm_read_words.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                   ctypes.c_int32, ctypes.c_void_p]
+    nbytes = buf.numel() * buf.element_size()
+    out = torch.empty(blocks * 256, dtype=torch.int32, device=buf.device)
+    best = None
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rc = lib.hbm_read_words(buf.data_ptr(), nbytes, out.data_ptr(), out.numel() * 4, blocks,
+                                stream.cuda_stream)
+        e1.record(stream)
+        if rc != 0:
+            raise RuntimeError(f"hbm_read_words failed ({rc})")
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3
+        best = t if best is None else min(best, t)
+    return nbytes / best / 1e9
+
+
 def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
     """the 8B layer at decode token counts (GPU only)."""
     import svdmlp
@@ -220,9 +252,12 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
         torch.cuda.synchronize()
         t = e0.elapsed_time(e1) * 1e-3
         best = t if best is None else min(best, t)
-    del src, dst
     copy_gbs = 2 * n / best / 1e9
-    dec = {"hbm_copy_GBps": round(copy_gbs, 1)}
+    # ... and a streaming read of the same 1 GiB (the decode layers read their
+    # factors and write almost nothing): libhbmread.so, best of 6
+    read_gbs = _read_rate(torch, stream, src)
+    del src, dst
+    dec = {"hbm_copy_GBps": round(copy_gbs, 1), "hbm_read_GBps": round(read_gbs, 1)}
     for Td in args.decode_tokens:
         xd = x[:Td].contiguous()
         wsd = svdmlp.svd_mlp_workspace(xd, r=R, ff=FF)
@@ -255,6 +290,7 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
             "GB/s": round(gbs, 1),
             "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
             "frac_measured_copy": round(gbs / copy_gbs, 4),
+            "frac_measured_read": round(gbs / read_gbs, 4),
             "traffic": traffic,
             "traffic_GB/s": round(traffic / (msd * 1e-3) / 1e9, 1) if traffic else None,
             "TFLOP/s": round(2.0 * Td * 3 * R * (D + FF) / (msd * 1e-3) / 1e12, 3),

@@ -24,6 +24,9 @@ CSRC = ROOT / "csrc"
 INCLUDE = ROOT.parent / "include"
 BUILD_DIR = ROOT / "_build"
 LIB_PATH = PKG_DIR / "libsvdmlp.so"
+# the benchmark's streaming-read probe (csrc/probe/), its own library outside the SVD-MLP C ABI
+PROBE_SRC = CSRC / "probe" / "hbm_read.hip"
+PROBE_LIB = PKG_DIR / "libhbmread.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -88,7 +91,17 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB_PATH)
+    build_probe(hipcc)
     return LIB_PATH
+
+
+def build_probe(hipcc: str | None = None) -> Path:
+    """Compile and link the benchmark's streaming-read probe, libhbmread.so."""
+    hipcc = hipcc or _hipcc()
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([hipcc, *HIPCC_FLAGS, "-shared", str(PROBE_SRC), "-o", str(tmp)])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 if __name__ == "__main__":
