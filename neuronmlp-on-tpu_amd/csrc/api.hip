@@ -1,12 +1,13 @@
 // C ABI of libsvdmlp.so (declared in include/svdmlp.h).
 //
 // Kernel choice per call (svdmlp_svd_mlp and its variants):
-//   1 token (padded V rows) or 1-3 (dense), bf16, aligned, or up to 4 on
-//   request (SVDMLP_CONTRACT):       the contracted decode layer
+//   1 token (padded V rows), 1-3 (dense factors whose shape the MFMA
+//   layer's one-branch phase 2 does not fit), bf16, aligned, or up to 4
+//   on request (SVDMLP_CONTRACT):    the contracted decode layer
 //                                    (decode_layer.hpp): h kept in LDS, two
 //                                    grid barriers
-//   1-2 tokens, dense bf16 factors the contracted layer does not take:
-//                                    one streaming-GEMV layer launch
+//   1-2 tokens, dense bf16 factors neither that layer nor the one-branch
+//   phase 2 takes:                   one streaming-GEMV layer launch
 //                                    (decode_gemv.hpp)
 //   1-128 tokens, bf16, aligned:     one persistent MFMA decode-layer launch
 //                                    (decode_layer.hpp): four phases, three
@@ -168,7 +169,9 @@ size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
 // 71.6 vs 70.0 us, T=2 72.3 vs 72.7, T=3 71.9 vs 73.5), with dense factors
 // up to three (the streaming-GEMV layer at T <= 2, the three-barrier layer
 // at 3, against contracted: 77.4 vs 73.6, 80.7 vs 76.0, 78.3 vs 76.8; T=4
-// 78.6 vs 78.8).
+// 78.6 vs 78.8).  With dense factors it applies only where the three-barrier
+// layer cannot run one-branch phase-2 units (p2split_fits): with them that
+// layer is faster at 1-3 tokens too (72.6 / 71.7 / 71.6 us).
 constexpr int64_t kDlContractMaxT = 4;
 constexpr int64_t kDlContractAutoPadded = 1;
 constexpr int64_t kDlContractAutoDense = 3;

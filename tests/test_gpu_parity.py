@@ -22,6 +22,7 @@ FP8_TOL = 3e-2
 GEMV_LAYER_MAX_T = 2   # kGvMaxT in csrc/decode_gemv.hpp
 # kDlContractAutoPadded / kDlContractAutoDense in csrc/api.hip: the contracted
 # decode layer by default at 1 token with padded factor rows, up to 3 with dense
+# factors whose shape the one-branch phase 2 does not fit (_contracted)
 CONTRACT_AUTO_T = {True: 1, False: 3}
 
 
