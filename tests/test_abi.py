@@ -101,3 +101,21 @@ def test_check_maps_status_to_exceptions(lib):
         _lib.check(_lib.SVDMLP_EINVAL)
     with pytest.raises(_lib.SvdMlpError):
         _lib.check(_lib.SVDMLP_EHIP)
+
+
+def test_read_probe_library_validates_before_launch():
+    """bench.py's streaming-read probe (libhbmread.so, csrc/probe/): built
+    beside libsvdmlp.so, exports hbm_read_words, and rejects invalid
+    arguments (-1) before any HIP call."""
+    path = Path(_lib.__file__).resolve().parent / "libhbmread.so"
+    assert path.exists(), f"{path} is not built"
+    probe = ctypes.CDLL(str(path))
+    fn = probe.hbm_read_words
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+    fake, out = 0x1000, 0x2000  # never dereferenced: every case fails validation
+    assert fn(None, 1 << 20, out, 1 << 23, 8192, None) == -1        # no buffer
+    assert fn(fake, (1 << 20) + 8, out, 1 << 23, 8192, None) == -1  # not whole 16-byte words
+    assert fn(fake + 8, 1 << 20, out, 1 << 23, 8192, None) == -1    # misaligned
+    assert fn(fake, 1 << 20, out, 8192 * 256 * 4 - 4, 8192, None) == -1  # out too small for the grid
+    assert fn(fake, 1 << 20, out, 1 << 23, 0, None) == -1           # no blocks
