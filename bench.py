@@ -236,32 +236,39 @@ def _read_rate(torch, stream, buf, blocks=8192, groups=3, per_group=5):
     return nbytes / best / 1e9
 
 
-def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
-    """the 8B layer at decode token counts (GPU only)."""
+def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes, tokens=None, rates=None, layout=None):
+    """the 8B layer at decode token counts (GPU only).
+    `rates` (copy, read GB/s) reuses the HBM rates of an earlier call;
+    `layout` names the factors' storage when it differs from
+    args.weights_layout (no committed traffic profile applies then)."""
     import svdmlp
     from svdmlp import _lib
 
-    # measured HBM ceiling for the decode fractions: a 1 GiB device-to-device
-    # copy (read + write bytes over its time), best of 5
-    n = 1 << 30
-    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-    dst = torch.empty_like(src)
-    best = None
-    for _ in range(6):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        dst.copy_(src)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) * 1e-3
-        best = t if best is None else min(best, t)
-    copy_gbs = 2 * n / best / 1e9
-    # ... and a streaming read of the same 1 GiB (the decode layers read their
-    # factors and write almost nothing): libhbmread.so
-    read_gbs = _read_rate(torch, stream, src)
-    del src, dst
-    dec = {"hbm_copy_GBps": round(copy_gbs, 1), "hbm_read_GBps": round(read_gbs, 1)}
-    for Td in args.decode_tokens:
+    if rates is None:
+        # measured HBM ceiling for the decode fractions: a 1 GiB device-to-device
+        # copy (read + write bytes over its time), best of 5
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        best = None
+        for _ in range(6):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            dst.copy_(src)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) * 1e-3
+            best = t if best is None else min(best, t)
+        copy_gbs = 2 * n / best / 1e9
+        # ... and a streaming read of the same 1 GiB (the decode layers read their
+        # factors and write almost nothing): libhbmread.so
+        read_gbs = _read_rate(torch, stream, src)
+        del src, dst
+    else:
+        copy_gbs, read_gbs = rates
+    layout = layout or args.weights_layout
+    dec = {"hbm_copy_GBps": round(copy_gbs, 1), "hbm_read_GBps": round(read_gbs, 1), "weights_layout": layout}
+    for Td in (tokens or args.decode_tokens):
         xd = x[:Td].contiguous()
         wsd = svdmlp.svd_mlp_workspace(xd, r=R, ff=FF)
         outd = torch.empty(Td, D, dtype=torch.bfloat16, device=dev)
@@ -287,7 +294,7 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
         kernel = "decode_layer_contracted" if "decode_layer_contracted" in prof.result else "decode_layer"
         key = f"decode_layer_contracted_T{Td}" if kernel == "decode_layer_contracted" else f"decode_layer_mt{mt}"
         traffic = (_profiled_traffic(key, DECODE_TRAFFIC_PROFILE)
-                   if args.weights_layout == TRAFFIC_LAYOUT and Td <= 128 else None)
+                   if layout == TRAFFIC_LAYOUT and Td <= 128 else None)
         dec[f"T={Td}"] = {
             "us_per_layer": round(msd * 1e3, 2),
             "GB/s": round(gbs, 1),
@@ -304,6 +311,60 @@ def _bench_decode(torch, dev, stream, args, layers, x, factor_bytes):
         if svdmlp.workspace_status(wsd):
             raise RuntimeError(f"decode T={Td}: a grid-barrier wait gave up (the device was shared?)")
     return dec
+
+
+# BASELINE config 4 draws the gate, up and down ranks of a layer
+# independently from {2048, ..., 3072}; one such draw, at decode shapes
+TWO_RANKS = (2304, 3072, 2560)
+
+
+def _bench_decode_ranks(torch, dev, stream, args, x, rates):
+    """The 8B layer at decode token counts with a gate, an up and a down rank
+    of their own (TWO_RANKS): each branch at its rank inside the decode
+    layer's launch (GPU only)."""
+    import svdmlp
+    from svdmlp import _lib
+
+    r_g, r_u, r_d = TWO_RANKS
+
+    def layer(seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+
+        def rnd(rows, cols):
+            return (torch.randn(rows, cols, generator=g, device=dev, dtype=torch.float32)
+                    / math.sqrt(rows)).to(torch.bfloat16)
+
+        return rnd(D, r_g), rnd(r_g, FF), rnd(D, r_u), rnd(r_u, FF), rnd(FF, r_d), rnd(r_d, D)
+
+    layers = [layer(args.seed + 50 + i) for i in range(args.layers)]
+    nbytes_w = 2 * (D * r_g + r_g * FF + D * r_u + r_u * FF + FF * r_d + r_d * D)
+    out = {"ranks_gate_up_down": list(TWO_RANKS), "factor_bytes": nbytes_w}
+    for Td in [t for t in (1, 8, 64) if t <= x.shape[0]]:
+        xd = x[:Td].contiguous()
+        wsd = svdmlp.svd_mlp_workspace(xd, r=max(TWO_RANKS), ff=FF)
+        outd = torch.empty(Td, D, dtype=torch.bfloat16, device=dev)
+        gain = torch.ones(D, dtype=torch.float32, device=dev)
+
+        def dstep(i, xd=xd, wsd=wsd, outd=outd):
+            svdmlp.svd_mlp(xd, *layers[i % len(layers)], workspace=wsd, out=outd)
+
+        def bstep(i, xd=xd, wsd=wsd, outd=outd, gain=gain):
+            svdmlp.svd_mlp_block(xd, gain, *layers[i % len(layers)], workspace=wsd, out=outd)
+
+        msd, _ = _time_steps(torch, dstep, args.decode_steps, 10, stream)
+        msb, _ = _time_steps(torch, bstep, args.decode_steps, 10, stream)
+        with _lib.StageProfile() as prof:
+            _time_steps(torch, dstep, 20, 0, stream)
+        gbs = (nbytes_w + 2 * Td * D * 2) / (msd * 1e-3) / 1e9
+        out[f"T={Td}"] = {"us_per_layer": round(msd * 1e3, 2), "GB/s": round(gbs, 1),
+                          "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                          "frac_measured_read": round(gbs / rates[1], 4),
+                          "launches": {k: v[1] // 20 for k, v in prof.result.items()},
+                          "block_us": round(msb * 1e3, 2)}
+        if svdmlp.workspace_status(wsd):
+            raise RuntimeError(f"two-rank decode T={Td}: a grid-barrier wait gave up (the device was shared?)")
+    return out
 
 
 def _stack_inputs(torch, dev, args):
@@ -354,8 +415,10 @@ def _stack_parity(torch, args, layers, x, ws):
     import oracle as O
     from svdmlp import ops
 
-    rows = min(args.parity_rows, x.shape[0])
-    idx = torch.arange(rows, device=x.device)
+    # rows spread evenly over the whole token range (first and last included)
+    rows = min(max(args.parity_rows, 16), x.shape[0])
+    idx = torch.linspace(0, x.shape[0] - 1, rows, device=x.device).round().long().unique()
+    rows = int(idx.numel())
     bufs = (torch.empty_like(x), torch.empty_like(x))
     cur = x
     chain = x[idx].float().cpu().numpy()
@@ -377,6 +440,7 @@ def _stack_parity(torch, args, layers, x, ws):
     exact = chain64.astype(np.float32)
     return {
         "parity_rows": rows,
+        "parity_row_indices": [int(i) for i in idx.tolist()],
         "parity_rel_l2_first_layer": round(first, 6),
         "parity_rel_l2_worst_layer": round(worst, 6),
         "after_all_layers_rel_l2_gpu_vs_float64": round(O.relative_l2(got, exact), 6),
@@ -452,13 +516,15 @@ def _fp8_parity(args, fs, x, y):
 
     import oracle as O
 
-    rows = min(args.parity_rows, x.shape[0])
+    # 64 rows spread evenly over the token range (first and last included)
+    idx = np.unique(np.linspace(0, x.shape[0] - 1, min(64, x.shape[0])).round().astype(np.int64))
     table = O.e4m3_decode(np.arange(256, dtype=np.uint8))
     deq = [table[f.data.view(__import__("torch").uint8).cpu().numpy()] * f.scale.cpu().numpy()[None, :] for f in fs]
-    ref = O.svd_mlp_ref(x[:rows].float().cpu().numpy(), *deq, dtype="bfloat16")
+    ref = O.svd_mlp_ref(x.float().cpu().numpy()[idx], *deq, dtype="bfloat16")
     y, y8 = y
-    return {"parity_rows": rows, "parity_rel_l2_vs_oracle": round(O.relative_l2(y[:rows].float().cpu().numpy(), ref), 6),
-            "fp8_activations_h_parity_rel_l2_vs_oracle": round(O.relative_l2(y8[:rows].float().cpu().numpy(), ref), 6)}
+    return {"parity_rows": int(idx.size),
+            "parity_rel_l2_vs_oracle": round(O.relative_l2(y.float().cpu().numpy()[idx], ref), 6),
+            "fp8_activations_h_parity_rel_l2_vs_oracle": round(O.relative_l2(y8.float().cpu().numpy()[idx], ref), 6)}
 
 
 def main(argv=None) -> int:
@@ -508,6 +574,16 @@ def main(argv=None) -> int:
 
     if args.only in (None, "decode"):
         record["decode"] = _bench_decode(torch, dev, stream, args, layers, x, factor_bytes)
+        if args.weights_layout == "padded":
+            # the dense natural-layout factors kernels/reference.py takes, at the
+            # config-3 token counts, on the same box and HBM rates
+            dense = [_layer_weights(torch, dev, args.seed + i) for i in range(args.layers)]
+            rates = (record["decode"]["hbm_copy_GBps"], record["decode"]["hbm_read_GBps"])
+            record["decode_dense"] = _bench_decode(torch, dev, stream, args, dense, x, factor_bytes,
+                                                   tokens=[t for t in (1, 8, 32, 64) if t <= x.shape[0]],
+                                                   rates=rates, layout="natural")
+            del dense
+            record["decode_two_ranks"] = _bench_decode_ranks(torch, dev, stream, args, x, rates)
     if args.only in (None, "stack"):
         s_layers, s_x = _stack_inputs(torch, dev, args)
         s_ws, record["stack"] = _time_stack(torch, dev, stream, args, s_layers, s_x)

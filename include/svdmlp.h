@@ -245,14 +245,31 @@ int svdmlp_svd_mlp_block_ranks(const void* x, const float* norm_w, float eps, co
  * call on a device looks the scratch up and clears its sync area on `stream`
  * (the current device's).  Every call on a device shares that device's
  * scratch and leaves its contents behind: calls that overlap on one device
- * (different streams, threads) race; serialise them.  svdmlp_workspace_status
- * does not see this scratch; a timed-out call still writes NaN into y.
+ * (different streams, threads) race; serialise them.  A call whose
+ * grid-barrier waits give up writes NaN into y and sets the scratch's sticky
+ * timeout flag, after which every later call on that device writes NaN too
+ * until svdmlp_noalloc_status resets the scratch.
  */
 int svdmlp_svd_mlp_noalloc(const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
                            const void* ud, const void* vd, const float* const* scales /* 6 or NULL */,
                            const int64_t* ld /* 6 or NULL */, void* y, int64_t T, int64_t d, int64_t ff,
                            int64_t r_gu, int64_t r_d, int32_t act_dtype, int32_t w_dtype, uint32_t flags,
                            void* stream);
+
+/*
+ * svdmlp_workspace_status for the fixed scratch of svdmlp_svd_mlp_noalloc on
+ * the current device (no counterpart in the reference; for the same callers).
+ * Waits for `stream`, then returns 1 if a grid-barrier wait of an earlier
+ * noalloc call gave up (its y and those of the calls after it hold NaN), 0 if
+ * not, or a negative status.  reset != 0 then zeroes the scratch's 4096-byte
+ * sync area (a fill kernel on `stream`), after which calls compute again.
+ * wait_bound >= 0 afterwards sets the bound of the barrier waits in polls
+ * (0: the default of 2^22 polls, seconds; failure tests set 1 so that every
+ * wait gives up at once and every kernel still runs to its end); a negative
+ * wait_bound leaves it.  Allocates no device memory; it synchronises, so it
+ * does not belong inside graph capture.
+ */
+int svdmlp_noalloc_status(int32_t reset, int64_t wait_bound, void* stream);
 
 /*
  * Per-stage GPU timing (no counterpart in the reference, whose timing is host

@@ -193,7 +193,7 @@ struct Ws {
   size_t total;
 };
 
-int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch);
+int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch, int kg = 1);
 // Tile (columns / 32) and K splits of the split gate/up XU.V passes at one or
 // two row tiles of tokens; *splits = 0 where the passes are not split.
 void gu_split_plan(int64_t T, int64_t ff, int* fn, int* splits);
@@ -224,6 +224,12 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
       // slices hold whole 256 x 32*fn tiles (fragment order)
       const int64_t bn = 32 * st[3], tp = (T + 255) / 256 * 256, np = (st[1] + bn - 1) / bn * bn;
       if (sp > 1) part = std::max(part, (int64_t)sp * st[2] * tp * np * 4);
+      // the K-group tiles of 128 x 128 and 128 x 192 (whole 128-row tiles)
+      if (st[3] == 4 || st[3] == 6) {
+        const int sp2 = plan_splits(T, st[0], st[1], (int)st[3], (int)st[2], 2);
+        const int64_t tp2 = (T + 127) / 128 * 128;
+        if (sp2 > 1) part = std::max(part, (int64_t)sp2 * st[2] * tp2 * np * 4);
+      }
     }
     if (rr == r) break;
   }
@@ -441,6 +447,9 @@ struct Tune {
   int gusp = 0;        // ... and their K splits (0: CUs / tiles, at most 4)
   int f8nw = 4;        // waves per block of the fp8 x fp8 GEMM (4: 70B h.Ud 309 -> 293 us against 8)
   int p2split = 1;     // decode layer phase 2 with one branch per unit: 0 never, 1 where it pays (below), 2 always
+  int kg = 1;          // K-group 128-row tiles for the rank stages: 0 never, 1 where the planner rates them cheaper, 2 always
+  int kgw = 125;       // planner: cycles of a K-group 64-k step, percent of a 256-row tile's 32-k step
+  int kgs = 7;         // stages that may take K-group tiles: 1 gate/up X.U, 2 h.Ud, 4 XU_d.Vd
 };
 
 const Tune& tune();
@@ -500,6 +509,9 @@ const Tune& tune() {
         if (k == "nw") r.nw = v;
         if (k == "f8nw") r.f8nw = v == 4 ? 4 : 8;
         if (k == "p2split") r.p2split = v;
+        if (k == "kg") r.kg = v;
+        if (k == "kgw") r.kgw = v;
+        if (k == "kgs") r.kgs = v;
       }
       pos = end + 1;
     }
@@ -541,7 +553,8 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
-             int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr, const uint16_t* resid = nullptr) {
+             int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr, const uint16_t* resid = nullptr,
+             int kg = 1) {
   BigParams p{};
   p.resid = resid;
   p.gfrag = gfrag;
@@ -570,7 +583,8 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   p.N[0] = N;
   p.N[1] = e1 ? e1->N : N;
   p.K = K;
-  p.mtiles = (M + 255) / 256;
+  const int bm = kg == 2 ? 128 : 256;  // K-group tiles are 128 rows
+  p.mtiles = (M + bm - 1) / bm;
   p.ntiles = (N + 32 * fn - 1) / (32 * fn);
   if (e1) {  // both entries' column tiles in one grid of z = 1
     if (batch != 2) return fail("large-tile GEMM: a second entry of its own width needs a batch of two");
@@ -580,7 +594,7 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
   }
   p.k_split = k_split;
   const int splits = (K + k_split - 1) / k_split;
-  const BigDesc d{fn, b_kc, epi, out_f32, fp8, big_nw(fn, epi, b_kc)};
+  const BigDesc d{fn, b_kc, epi, out_f32, fp8, kg == 2 ? 8 : big_nw(fn, epi, b_kc), kg};
   const char* why = nullptr;
   StageScope ss(stage, c.st);
   return check(launch_big(d, p, splits, batch, c.st, &why), "large-tile GEMM", why);
@@ -607,21 +621,34 @@ namespace {
 // N1 >= 0: a second batch entry N1 columns wide (its own column tiles);
 // otherwise `batch` entries of N columns.  *cost_out (if given) receives the
 // model's cost of the chosen split.
-int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch, int64_t N1 = -1, double* cost_out = nullptr) {
+//
+// kg = 2 plans the K-group tiles (128 rows, 8 waves in two groups that take
+// the two 32-k halves of a 64-k step): each wave does the same MFMAs and
+// fragment reads per step as in the 256-row tile of the same width, and the
+// block fetches twice the B rows per step, which makes the step ~25% dearer
+// (tune().kgw percent): 8B layer, T=1024, h.Ud as 240 blocks of 128 x 192
+// in two splits took 92.9 us against 78.6 us for 220 blocks of 256 x 256 in
+// five (~0.72 against ~0.61 us per MFMA step of a wave), which the slices
+// saved (23.6 against 57.7 MB, 8.5 against 12.4 us of reduction) did not
+// repay, while X.[Ug|Uu] (240 tiles of 128 x 192, no split) and XU_d.Vd
+// (256 of 128 x 128, no split) each saved their reduction: the layer
+// 343.3 -> 328.4 us (same box, alternating runs).
+int plan_ksplit(int64_t T, int64_t K, int64_t N, int fn, int batch, int64_t N1 = -1, double* cost_out = nullptr,
+                int kg = 1) {
   const int64_t cus = tune().split;
-  const int64_t bn = 32 * fn;
+  const int64_t bn = 32 * fn, bm = kg == 2 ? 128 : 256, sk = 32 * kg;
   const int64_t ntl = N1 >= 0 ? (N + bn - 1) / bn + (N1 + bn - 1) / bn : ((N + bn - 1) / bn) * batch;
-  const int64_t tiles = ((T + 255) / 256) * ntl;
-  const double c_step = 787.0 + 65.6 * fn, c_block = 20000.0;
+  const int64_t tiles = ((T + bm - 1) / bm) * ntl;
+  const double c_step = (787.0 + 65.6 * fn) * (kg == 2 ? tune().kgw / 100.0 : 1.0), c_block = 20000.0;
   const double c_slice = 0.0009 * (double)T * (double)(N1 >= 0 ? N + N1 : batch * N) * 4.0;
   int64_t best_ks = K;
   double best = -1.0;
   const int64_t max_s = std::max<int64_t>(1, std::min<int64_t>(64, K / 128));
   for (int64_t s = 1; s <= max_s; ++s) {
-    const int64_t ks = ((K + s - 1) / s + 31) / 32 * 32;
+    const int64_t ks = ((K + s - 1) / s + sk - 1) / sk * sk;
     const int64_t splits = (K + ks - 1) / ks;
     const int64_t rounds = (tiles * splits + cus - 1) / cus;
-    const double cost = (double)rounds * ((double)(ks / 32) * c_step + c_block) +
+    const double cost = (double)rounds * ((double)(ks / sk) * c_step + c_block) +
                         (splits > 1 ? (double)splits * c_slice : 0.0);
     if (best < 0 || cost < best) {
       best = cost;
@@ -654,9 +681,40 @@ int gate_xu_fn(int64_t T, int64_t K, int64_t r, int batch, int64_t r1 = -1) {
   return c6 < c8 ? 6 : 8;
 }
 
-int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch) {
-  const int64_t ks = plan_ksplit(T, K, N, fn, batch);
+int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch, int kg) {
+  const int64_t ks = plan_ksplit(T, K, N, fn, batch, -1, nullptr, kg);
   return (int)((K + ks - 1) / ks);
+}
+
+// Tile plan of a rank stage (the X.U products and XU_d.Vd): 256-row tiles
+// fn1 * 32 wide, or K-group tiles of 128 x 128 or 128 x 192 where they apply
+// (kg_ok: natural-layout bf16 B, K a multiple of 64) and the cost model rates
+// them cheaper (tune().kg 1; 2 takes them wherever they apply).  At the 8B
+// layer's 1024 tokens they run X.[Ug|Uu] (240 tiles of 128 x 192) and
+// XU_d.Vd (256 of 128 x 128) without K splits and h.Ud (120 tiles) in two
+// instead of five.
+struct RankPlan {
+  int kg, fn, ks, splits;
+};
+
+RankPlan plan_rank(int64_t T, int64_t K, int64_t N, int fn1, int batch, int64_t N1, bool kg_ok, int stage) {
+  double c1 = 0.0;
+  const int ks1 = plan_ksplit(T, K, N, fn1, batch, N1, &c1, 1);
+  RankPlan best{1, fn1, ks1, (int)((K + ks1 - 1) / ks1)};
+  const int bit = stage == ST_GU_XU ? 1 : (stage == ST_D_XU ? 2 : 4);
+  if (!kg_ok || tune().kg == 0 || !(tune().kgs & bit) || K % 64) return best;
+  // the K-group tiles must undercut the 256-row plan by 5% (the model's
+  // margin: at 2048 tokens it rates h.Ud within 1% either way)
+  double bestc = tune().kg == 2 ? 1e300 : 0.95 * c1;
+  for (int fn : {4, 6}) {
+    double c = 0.0;
+    const int ks = plan_ksplit(T, K, N, fn, batch, N1, &c, 2);
+    if (c < bestc) {
+      bestc = c;
+      best = RankPlan{2, fn, ks, (int)((K + ks - 1) / ks)};
+    }
+  }
+  return best;
 }
 
 // Row pitch (elements) of the factors as stored, natural layout: ug and uu
@@ -676,37 +734,39 @@ FactorLd dense_ld(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d) { return Fac
 // workspace's slice area, else one split.
 int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
             int T, int K, int r, int r1, char* ws, const Ws& L, const float* const* su, int64_t ldu, int64_t ldu1) {
-  const int fn = gate_xu_fn(T, K, r, 2, r1);
-  const int nw = big_nw(fn, BEPI_STORE, u_lin);
+  const RankPlan pl = plan_rank(T, K, r, gate_xu_fn(T, K, r, 2, r1), 2, r1, !u_lin && c.wt == SVDMLP_BF16, stage);
+  const int fn = pl.fn, kg = pl.kg;
+  const int nw = kg == 2 ? 8 : big_nw(fn, BEPI_STORE, u_lin);
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
   const int64_t ldb0 = u_lin ? K : (ldu ? ldu : r), ldb1 = u_lin ? K : (ldu1 ? ldu1 : r1);
   const int64_t b0 = (int64_t)(u_lin ? r : K) * ldb0 * wbytes(c), b1 = (int64_t)(u_lin ? r1 : K) * ldb1 * wbytes(c);
   const float* s0 = su ? su[0] : nullptr;
   const float* s1 = su ? su[1] : nullptr;
-  const int64_t bn = 32 * fn, tp = (T + 255) / 256 * 256;
+  const int64_t bn = 32 * fn, bm = kg == 2 ? 128 : 256, tp = (T + bm - 1) / bm * bm;
   const int64_t per0 = tp * ((r + bn - 1) / bn * bn), per1 = tp * ((r1 + bn - 1) / bn * bn);
-  int ks = plan_ksplit(T, K, r, fn, 2, r1);
-  int splits = (K + ks - 1) / ks;
-  if (splits > 1 && (!big_frag_reduce_ok(fn, nw) || (int64_t)splits * (per0 + per1) * 4 > (int64_t)(L.norm - L.part))) {
+  int ks = pl.ks;
+  int splits = pl.splits;
+  if (splits > 1 && ((kg == 1 && !big_frag_reduce_ok(fn, nw)) ||
+                     (int64_t)splits * (per0 + per1) * 4 > (int64_t)(L.norm - L.part))) {
     ks = K;
     splits = 1;
   }
   const Entry1 e1{r1, ldb1, r1, b1};
   if (splits == 1)
     return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, K, xu, r,
-                    (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, &e1);
+                    (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, &e1, nullptr, kg);
   float* part = reinterpret_cast<float*>(ws + L.part);
   int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, ks, part, r,
-                    per0, nullptr, true, per0 + per1, s0, s1, 0, 1, &e1);
+                    per0, nullptr, true, per0 + per1, s0, s1, 0, 1, &e1, nullptr, kg);
   if (rc) return rc;
   StageScope fin(ST_FINALIZE, c.st);
-  const int mt = (int)(tp / 256);
+  const int mt = (int)(tp / bm);
   rc = check(launch_reduce_frag_bf16(part, splits, per0 + per1, 0, xu, r, 0, T, r, mt, (int)(per0 / tp / bn), fn, nw,
-                                     1, c.st),
+                                     1, c.st, nullptr, nullptr, kg),
              "split-K reduce");
   if (rc) return rc;
   return check(launch_reduce_frag_bf16(part + per0, splits, per0 + per1, 0, xu + (int64_t)T * r, r1, 0, T, r1, mt,
-                                       (int)(per1 / tp / bn), fn, nw, 1, c.st),
+                                       (int)(per1 / tp / bn), fn, nw, 1, c.st, nullptr, nullptr, kg),
                "split-K reduce");
 }
 
@@ -716,11 +776,14 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
            int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr,
            int64_t ldu = 0) {
-  const int fn = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : tune().s1;
-  int ks = plan_ksplit(T, K, r, fn, batch);
-  int splits = (K + ks - 1) / ks;
+  const int fn1 = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : tune().s1;
+  const RankPlan pl = plan_rank(T, K, r, fn1, batch, -1, !u_lin && c.wt == SVDMLP_BF16, stage);
+  const int fn = pl.fn, kg = pl.kg;
+  const int64_t bm = kg == 2 ? 128 : 256;
+  int ks = pl.ks;
+  int splits = pl.splits;
   {  // the slices must fit the workspace's slice area (sized for the planned tiles)
-    const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn);
+    const int64_t tp = (T + bm - 1) / bm * bm, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn);
     if (splits > 1 && (int64_t)splits * batch * std::max(tp * np, (int64_t)T * r) * 4 > (int64_t)(L.norm - L.part)) {
       ks = K;
       splits = 1;
@@ -734,18 +797,18 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
   const float* s1 = su && batch > 1 ? su[1] : s0;
   if (splits == 1)
     return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
-                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1);
+                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, nullptr, nullptr, kg);
   float* part = reinterpret_cast<float*>(ws + L.part);
-  const int nw = big_nw(fn, BEPI_STORE, u_lin);
-  if (big_frag_reduce_ok(fn, nw)) {
+  const int nw = kg == 2 ? 8 : big_nw(fn, BEPI_STORE, u_lin);
+  if (kg == 2 || big_frag_reduce_ok(fn, nw)) {
     // slices in fragment order: per split, `batch` blocks of whole tiles
-    const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
+    const int64_t tp = (T + bm - 1) / bm * bm, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
     int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn, BEPI_STORE, ks,
-                      part, r, per, nullptr, true, batch * per, s0, s1, 0, 1);
+                      part, r, per, nullptr, true, batch * per, s0, s1, 0, 1, nullptr, nullptr, kg);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
-    return check(launch_reduce_frag_bf16(part, splits, batch * per, per, xu, r, (int64_t)T * r, T, r, (int)(tp / 256),
-                                         (int)(np / (32 * fn)), fn, nw, batch, c.st),
+    return check(launch_reduce_frag_bf16(part, splits, batch * per, per, xu, r, (int64_t)T * r, T, r, (int)(tp / bm),
+                                         (int)(np / (32 * fn)), fn, nw, batch, c.st, nullptr, nullptr, kg),
                  "split-K reduce");
   }
   const int64_t slice = (int64_t)batch * T * r;
@@ -882,30 +945,34 @@ int f8_down_xu(const Common& c, const uint16_t* h, const void* ud, const float* 
 // y = XU . V with bf16 XU (T x r); bf16 y (T x dout).
 int big_v(const Common& c, const uint16_t* xu, const void* v, bool v_lin, int T, int r, int dout, char* ws,
           const Ws& L, void* y, const float* sv = nullptr, int64_t ldv = 0) {
-  const int fn = tune().s4 > 0 ? tune().s4 : 8;
+  const int fn1 = tune().s4 > 0 ? tune().s4 : 8;
   const int64_t ldb = v_lin ? r : (ldv ? ldv : dout);
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? dout : r) * ldb * wbytes(c);
-  const int ks = tune().s4 > 0 && tune().s4 != 8 ? r : plan_ksplit(T, r, dout, fn, 1);
-  const int splits = (r + ks - 1) / ks;
+  RankPlan pl = plan_rank(T, r, dout, fn1, 1, -1, !v_lin && c.wt == SVDMLP_BF16, ST_D_XUV);
+  if (pl.kg == 1 && tune().s4 > 0 && tune().s4 != 8) pl = RankPlan{1, fn1, r, 1};
+  const int fn = pl.fn, kg = pl.kg;
+  const int64_t bm = kg == 2 ? 128 : 256;
+  const int ks = pl.ks;
+  const int splits = pl.splits;
   // the MLP block's residual add rides on the output store or the fragment-order reduction
   const uint16_t* resid = c.blk ? static_cast<const uint16_t*>(c.blk->x) : nullptr;
   if (splits == 1) {
     if (c.blk) c.blk->resid_done = true;
     return big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1,
-                    fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv, nullptr, 0, 0, nullptr, resid);
+                    fn, BEPI_STORE, r, y, dout, 0, nullptr, false, 0, sv, nullptr, 0, 0, nullptr, resid, kg);
   }
   float* part = reinterpret_cast<float*>(ws + L.part);
-  const int nw = big_nw(fn, BEPI_STORE, v_lin);
-  if (big_frag_reduce_ok(fn, nw)) {
+  const int nw = kg == 2 ? 8 : big_nw(fn, BEPI_STORE, v_lin);
+  if (kg == 2 || big_frag_reduce_ok(fn, nw)) {
     if (c.blk) c.blk->resid_done = true;
-    const int64_t tp = (T + 255) / 256 * 256, np = ((int64_t)dout + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
+    const int64_t tp = (T + bm - 1) / bm * bm, np = ((int64_t)dout + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
     int rc = big_gemm(c, ST_D_XUV, xu, nullptr, r, xu_bytes, v, nullptr, ldb, v_bytes, v_lin, T, dout, r, 1, fn,
-                      BEPI_STORE, ks, part, dout, per, nullptr, true, per, sv, nullptr, 0, 1);
+                      BEPI_STORE, ks, part, dout, per, nullptr, true, per, sv, nullptr, 0, 1, nullptr, nullptr, kg);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
     return check(launch_reduce_frag_bf16(part, splits, per, per, static_cast<uint16_t*>(y), dout, (int64_t)T * dout,
-                                         T, dout, (int)(tp / 256), (int)(np / (32 * fn)), fn, nw, 1, c.st, nullptr,
-                                         resid),
+                                         T, dout, (int)(tp / bm), (int)(np / (32 * fn)), fn, nw, 1, c.st, nullptr,
+                                         resid, kg),
                  "split-K reduce");
   }
   const int64_t slice = (int64_t)T * dout;
@@ -968,17 +1035,21 @@ bool decode_ok(const Common& c, int64_t T, std::initializer_list<int64_t> dims, 
 // streaming-GEMV layer, tried first, takes 1 <= T <= kGvMaxT.
 constexpr int64_t kDlMinT = 1;
 
+// r_u: the up branch's rank (r_gu the gate's); with distinct ranks phase 2
+// must run one-branch units (p2split_fits).
 bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, uint32_t flags,
-                     bool vec, const FactorLd& ld) {
+                     bool vec, const FactorLd& ld, int64_t r_u = -1) {
+  if (r_u < 0) r_u = r_gu;
   if (c.f32 || c.wt != SVDMLP_BF16 || !vec || flags || T > kDlMaxT || !tune().dlayer) return false;
   if (T < std::min<int64_t>(kDlMinT, tune().dlmin)) return false;
-  if (d % 128 || r_gu % 128 || r_d % 128 || ff % 64) return false;
+  if (d % 128 || r_gu % 128 || r_u % 128 || r_d % 128 || ff % 64) return false;
   // one counter per split-K tile of phases 1, 3 and 4; the bf16 XU_d
   // lives in the decode-only gu32 region (2 T max(d, ff) fp32)
-  if (2 * r_gu / 128 + r_d / 128 + d / 128 > kDlMaxTiles || r_d > 4 * std::max(d, ff)) return false;
+  if ((r_gu + r_u) / 128 + r_d / 128 + d / 128 > kDlMaxTiles || r_d > 4 * std::max(d, ff)) return false;
   const int64_t lim = (int64_t)1 << 31;
-  for (int64_t bytes : {T * d * 2, d * ld.u * 2, r_gu * ld.v * 2, ff * ld.ud * 2, r_d * ld.vd * 2, T * ff * 2,
-                        2 * T * r_gu * 4})
+  const int64_t uu = ld.uu ? ld.uu : ld.u, vu = ld.vu ? ld.vu : ld.v;
+  for (int64_t bytes : {T * d * 2, d * ld.u * 2, d * uu * 2, r_gu * ld.v * 2, r_u * vu * 2, ff * ld.ud * 2,
+                        r_d * ld.vd * 2, T * ff * 2, 2 * T * std::max(r_gu, r_u) * 4})
     if (bytes >= lim) return false;
   return decode_layer_grid(decode_layer_mt((int)T)) > 0;
 }
@@ -1005,14 +1076,19 @@ bool decode_contract_ok(int64_t T, int64_t ff, int64_t r_gu, int64_t r_d, const 
 
 // Phase 2 with one branch per unit fits the shape: ff in whole 128-column
 // tiles, a block per unit and one more tile counter per column tile.
-bool p2split_fits(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int grid) {
+bool p2split_fits(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d, int grid, int64_t r_u = -1) {
+  if (r_u < 0) r_u = r_gu;
   const int64_t nt2 = ff / 128;
-  return ff % 128 == 0 && 2 * nt2 <= grid && 2 * r_gu / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles;
+  return ff % 128 == 0 && 2 * nt2 <= grid && (r_gu + r_u) / 128 + r_d / 128 + d / 128 + nt2 <= kDlMaxTiles;
 }
 
+// r_u >= 0 and != r_gu: distinct gate and up ranks (the caller checked
+// decode_layer_ok and p2split_fits with both; phase 2 runs one-branch units).
 int decode_layer(const Common& c, const void* x, const void* ug, const void* vg, const void* uu, const void* vu,
                  const void* ud, const void* vd, void* y, int64_t T, int64_t d, int64_t ff, int64_t r_gu, int64_t r_d,
-                 char* ws, const Ws& L, const FactorLd& ld, bool contract = false) {
+                 char* ws, const Ws& L, const FactorLd& ld, bool contract = false, int64_t r_u = -1) {
+  if (r_u < 0) r_u = r_gu;
+  const bool two = r_u != r_gu;
   const int mt = decode_layer_mt((int)T);
   const int grid = contract ? decode_layer_contract_grid() : decode_layer_grid(mt);
   DecLayerParams p{};
@@ -1035,8 +1111,9 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.d = (int)d;
   p.ff = (int)ff;
   p.r_gu = (int)r_gu;
+  p.r_up = (int)r_u;
   p.r_d = (int)r_d;
-  p.ks1 = dl_plan(d, 2 * r_gu / 128, grid, &p.units1);
+  p.ks1 = dl_plan(d, (r_gu + r_u) / 128, grid, &p.units1);
   p.units2 = (int)(ff / 64);
   // Phase 2 with one branch per unit over 128 columns (units 2t, 2t+1: g
   // and u of tile t) instead of both over 64; the pair meets through a tile
@@ -1049,15 +1126,17 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   // / 78.2 -> 73.2 / 73.5 / 75.0 us); with padded rows the pair's extra
   // slice round trip costs ~1 us there (T=8 69.3 -> 70.4 us).
   const bool p2_pays = mt >= 2 || ld.dense;
-  p.p2split = !contract && p2split_fits(d, ff, r_gu, r_d, grid) &&
-              (tune().p2split >= 2 || (tune().p2split == 1 && p2_pays));
+  p.p2split = !contract && p2split_fits(d, ff, r_gu, r_d, grid, r_u) &&
+              (two || tune().p2split >= 2 || (tune().p2split == 1 && p2_pays));
   p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
   p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
-  p.splits1 = p.units1 / (int)(2 * r_gu / 128);
+  p.splits1 = p.units1 / (int)((r_gu + r_u) / 128);
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;
+  p.ld_uu = (int)(ld.uu ? ld.uu : ld.u);
+  p.ld_vu = (int)(ld.vu ? ld.vu : ld.v);
   p.ld_ud = (int)ld.ud;
   p.ld_vd = (int)ld.vd;
   if (c.blk) {
@@ -1217,6 +1296,25 @@ int svdmlp_svd_mlp_noalloc(const void* x, const void* ug, const void* vg, const 
                            ws, kScratchBytes, stream);
 }
 
+int svdmlp_noalloc_status(int32_t reset, int64_t wait_bound, void* stream) {
+  g_err.clear();
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = nullptr;
+  int rc = scratch_of_current_device(st, &ws);
+  if (rc) return rc;
+  uint64_t flag = 0;
+  rc = check(hipMemcpyAsync(&flag, ws + kDlFlag * 8, 8, hipMemcpyDeviceToHost, st), "scratch status read");
+  if (!rc) rc = check(hipStreamSynchronize(st), "scratch status read");
+  if (!rc && reset) rc = check(launch_fill_zero(reinterpret_cast<float*>(ws), 4096 / 4, st), "scratch sync area reset");
+  if (!rc && wait_bound >= 0) {
+    const uint64_t bound = (uint64_t)wait_bound;
+    rc = check(hipMemcpyAsync(ws + kDlSpin * 8, &bound, 8, hipMemcpyHostToDevice, st), "scratch wait bound");
+    if (!rc) rc = check(hipStreamSynchronize(st), "scratch wait bound");
+  }
+  if (rc) return rc;
+  return flag ? 1 : 0;
+}
+
 int svdmlp_version(void) { return SVDMLP_VERSION; }
 
 const char* svdmlp_last_error(void) { return g_err.c_str(); }
@@ -1372,14 +1470,22 @@ int svdmlp_gate_up(const void* x, const void* ug, const void* vg, const void* uu
                  "SwiGLU finalize");
   }
 
-  if (!out_t && big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2}, {d, r})) {
+  if (big_ok(c, vec, {T * d * 2, d * r * 2, r * ff * 2, T * ff * 2}, {d, r})) {
     const void* us[2] = {ug, uu};
     const float* sus[2] = {s_ug, s_uu};
     if ((rc = big_xu(c, ST_GU_XU, x, d, T * d * 2, us, u_lin, T, d, r, 2, ws, L, fp8 ? sus : nullptr))) return rc;
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
-    return big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, h, reinterpret_cast<float*>(ws + L.part),
-                      (int64_t)(L.norm - L.part), fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr);
+    // (I, S) output (the reference's TPU launcher fused_mlp_up_T,
+    // test_speedup.py:522-544): h in the natural layout into the workspace's
+    // h region, then one transpose pass into the caller's buffer
+    uint16_t* hn = out_t ? reinterpret_cast<uint16_t*>(ws + L.h) : static_cast<uint16_t*>(h);
+    if ((rc = big_swiglu(c, xu, xu + T * r, vg, vu, v_lin, T, r, ff, gbuf, hn, reinterpret_cast<float*>(ws + L.part),
+                         (int64_t)(L.norm - L.part), fp8 ? s_vg : nullptr, fp8 ? s_vu : nullptr)) ||
+        !out_t)
+      return rc;
+    StageScope fin(ST_FINALIZE, c.st);
+    return check(launch_transpose_bf16(hn, ff, static_cast<uint16_t*>(h), T, (int)T, (int)ff, c.st), "h transpose");
   }
 
   const Operand ax{x, nullptr, d};
@@ -1409,11 +1515,26 @@ int svdmlp_xuv(const void* x, const void* u, const void* v, const float* s_u, co
   const Ws L = ws_layout(T, din, dout, r);
   if (ws_bytes < L.need) return fail("workspace too small: need %zu bytes, got %zu", L.need, ws_bytes);
   const Common c{act_dtype, w_dtype, act_dtype == SVDMLP_F32, (hipStream_t)stream};
-  const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR, x_t = flags & SVDMLP_X_T;
+  const bool u_lin = flags & SVDMLP_U_LINEAR, v_lin = flags & SVDMLP_V_LINEAR;
+  bool x_t = flags & SVDMLP_X_T;
   bool vec = din % 8 == 0 && dout % 8 == 0 && r % 8 == 0 && (!x_t || T % 8 == 0);
   for (const void* q : {x, u, v, (const void*)y, (const void*)workspace}) vec = vec && aligned16(q);
   if (fp8 && !vec) return fail("fp8 weights need d_in, d_out and r to be multiples of 8 and 16-byte aligned buffers");
   char* ws = static_cast<char*>(workspace);
+  // x given as (I, S) (the reference's TPU launcher fused_three_mm_XTUV,
+  // test_speedup.py:500-519): bf16 x is transposed once into the workspace's
+  // h region (unused by this entry point) and the layer runs as for (S, I)
+  if (x_t && !c.f32 && vec) {
+    uint16_t* xs = reinterpret_cast<uint16_t*>(ws + L.h);
+    {
+      StageScope ss(ST_FINALIZE, c.st);
+      if ((rc = check(launch_transpose_bf16(static_cast<const uint16_t*>(x), T, xs, din, (int)din, (int)T, c.st),
+                      "x transpose")))
+        return rc;
+    }
+    x = xs;
+    x_t = false;
+  }
 
   if (!x_t && decode_ok(c, T, {din, dout, r}, vec)) {
     float* xd32 = reinterpret_cast<float*>(ws + L.xu32) + 2 * T * r;
@@ -1558,18 +1679,23 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
     for (int i = 0; i < 6; ++i) S[i] = scales[i];
 
   if (two) {
-    // The large-tile path runs each branch at its own rank: X.Ug and X.Uu
-    // in one launch (their column tiles side by side), then the g pass over
-    // r_g and the u pass over r_u.
+    // The persistent decode layer (up to 128 tokens) runs each branch at its
+    // own rank in phases 1 and 2 (one-branch phase-2 units); the large-tile
+    // path does too: X.Ug and X.Uu in one launch (their column tiles side by
+    // side), then the g pass over r_g and the u pass over r_u.
+    if (decode_layer_ok(c, T, d, ff, r_g, r_d, flags, vec, ld, r_u) &&
+        p2split_fits(d, ff, r_g, r_d, decode_layer_grid(decode_layer_mt((int)T)), r_u))
+      return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_g, r_d, ws, L, ld, false, r_u);
     const bool big2 = T > kDecodeMaxT &&
                       big_ok(c, vec, {T * d * 2, d * ld.u * 2, d * ld.uu * 2, r_g * ld.v * 2, r_u * ld.vu * 2,
                                       T * ff * 2, ff * ld.ud * 2, r_d * ld.vd * 2},
                              {d, r_g, r_u, ff, r_d});
     if (!big2) {
-      fail("distinct gate and up ranks (%lld, %lld) run on the large-tile path only (bf16 activations, bf16 or fp8 "
-           "weights, more than %lld tokens, 16-byte aligned, d, ff and ranks multiples of 32); pad the smaller "
-           "branch with zero U columns and V rows for this shape",
-           (long long)r_g, (long long)r_u, (long long)kDecodeMaxT);
+      fail("distinct gate and up ranks (%lld, %lld) run on the persistent decode layer (bf16 natural-layout "
+           "factors, up to %lld tokens, d and ranks multiples of 128, ff of 128) and the large-tile path (bf16 "
+           "activations, bf16 or fp8 weights, more than %lld tokens, 16-byte aligned, d, ff and ranks multiples "
+           "of 32); pad the smaller branch with zero U columns and V rows for this shape",
+           (long long)r_g, (long long)r_u, (long long)kDlMaxT, (long long)kDecodeMaxT);
       return SVDMLP_EUNSUP;
     }
     if ((rc = normed())) return rc;

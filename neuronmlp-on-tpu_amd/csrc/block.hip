@@ -152,6 +152,27 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
+// out[c][r] = in[r][c] (bf16, r < rows, c < cols): 64 x 64 tiles through
+// LDS, 256 threads; a quarter-wave group moves 64 consecutive elements (128
+// contiguous bytes) of one row per access on both sides.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* in, int64_t ldi, uint16_t* out,
+                                                             int64_t ldo, int rows, int cols) {
+  __shared__ uint16_t tile[64][65];  // odd pitch: the column reads of the store side hit distinct banks
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 4 * i + q, c = t;
+    if (r0 + r < rows && c0 + c < cols) tile[r][c] = in[(int64_t)(r0 + r) * ldi + c0 + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = 4 * i + q, r = t;
+    if (c0 + c < cols && r0 + r < rows) out[(int64_t)(c0 + c) * ldo + r0 + r] = tile[r][c];
+  }
+}
+
 hipError_t launch_rmsnorm(const void* x, const float* gain, void* y, int64_t T, int64_t d, float eps, bool bf16,
                           hipStream_t st) {
   if (T <= 0) return hipSuccess;
@@ -181,6 +202,15 @@ hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hip
     hipLaunchKernelGGL((residual_add_kernel<false, true>), dim3(blocks), dim3(256), 0, st, x, y, n);
   else
     hipLaunchKernelGGL((residual_add_kernel<false, false>), dim3(blocks), dim3(256), 0, st, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_bf16(const uint16_t* in, int64_t ldi, uint16_t* out, int64_t ldo, int rows, int cols,
+                                 hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return hipSuccess;
+  dim3 grid((cols + 63) / 64, (rows + 63) / 64);
+  if (grid.y > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, st, in, ldi, out, ldo, rows, cols);
   return hipGetLastError();
 }
 

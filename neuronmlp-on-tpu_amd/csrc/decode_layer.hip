@@ -70,8 +70,12 @@ hipError_t launch_decode_layer(const DecLayerParams& p, int mt, int grid, hipStr
     return hipErrorInvalidValue;
   }
   if (p.p2split && (contract || p.ff % 128 || p.units2 > grid || p.units2 != 2 * (p.ff / 128) ||
-                    2 * (p.r_gu / 128) + p.r_d / 128 + p.d / 128 + p.ff / 128 > kDlMaxTiles)) {
+                    p.r_gu / 128 + p.r_up / 128 + p.r_d / 128 + p.d / 128 + p.ff / 128 > kDlMaxTiles)) {
     *why = "decode layer: one-branch phase 2 takes ff % 128 == 0, a block per unit and a counter per column tile";
+    return hipErrorInvalidValue;
+  }
+  if (p.r_up != p.r_gu && (!p.p2split || contract)) {
+    *why = "decode layer: distinct gate and up ranks need the one-branch phase 2 (not the contracted layer)";
     return hipErrorInvalidValue;
   }
   hipError_t e;

@@ -78,17 +78,19 @@ struct DecLayerParams {
   const void* ud;
   const void* vd;
   void* y;         // (T, d) bf16
-  uint16_t* xu16;  // (2, T, r_gu) bf16 gate/up rank intermediates
+  uint16_t* xu16;  // bf16 gate/up rank intermediates: (T, r_gu) gate, then (T, r_up) up
   uint16_t* h;     // (T, ff) bf16
   uint16_t* xd16;  // (T, r_d) bf16 down rank intermediate
   float* slices;   // split-K partial sums, MT * 2048 floats per unit (kDlMaxGrid units)
   float* cslices;  // contracted layer: partial XU_d tiles, (r_d / 128, units2, T, 128) fp32
   uint64_t* sync;  // barrier words, one per 128-byte line (kDl*), then split-K tile counters
   int T, d, ff, r_gu, r_d;
+  int r_up;                            // up-branch rank (r_gu is the gate's); distinct ranks need p2split
   int ks1, ks3, ks4;                   // K per split, phases 1, 3, 4 (multiples of 32)
   int units1, units2, units3, units4;  // tiles x splits
   int splits1, splits3, splits4;       // splits per tile, phases 1, 3 and 4
-  int ld_u, ld_v, ld_ud, ld_vd;        // row pitch (elements) of ug and uu, vg and vu, ud, vd
+  int ld_u, ld_v, ld_ud, ld_vd;        // row pitch (elements) of ug, vg, ud, vd
+  int ld_uu, ld_vu;                    // ... of uu and vu
   int a_cached;                        // activation DMAs through the caches (workspace 128-byte aligned)
   // Phase 2 with one branch per unit: unit u = 2 t + b computes g (b = 0) or
   // u (b = 1) over 128 columns 128 t..; the pair meets through a tile
@@ -888,33 +890,35 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
-      const int per = p.r_gu / 128, nt = 2 * per;
-      const int tile = u % nt, split = u / nt, br = tile / per;
+      // tiles 0 .. r_gu/128 - 1 of XU_g, then those of XU_u
+      const int pg = p.r_gu / 128, nt = pg + p.r_up / 128;
+      const int tile = u % nt, split = u / nt, br = tile >= pg;
       U.a0 = U.a1 = NORM ? static_cast<const void*>(p.xn) : p.x;
       U.lda = p.d;
       U.a_bytes = (uint32_t)((int64_t)T * p.d * 2);
       U.b0 = U.b1 = br ? p.uu : p.ug;
-      U.ldb = p.ld_u;
-      U.b_bytes = (uint32_t)((int64_t)p.d * p.ld_u * 2);
-      U.n0 = (tile % per) * 128;
+      U.ldb = br ? p.ld_uu : p.ld_u;
+      U.b_bytes = (uint32_t)((int64_t)p.d * U.ldb * 2);
+      U.n0 = (br ? tile - pg : tile) * 128;
       U.kb = split * p.ks1;
       U.ke = min(p.d, U.kb + p.ks1);
-      U.dst = p.xu16 + (int64_t)br * T * p.r_gu;
-      U.ldo = p.r_gu;
+      U.dst = p.xu16 + (br ? (int64_t)T * p.r_gu : 0);
+      U.ldo = br ? p.r_up : p.r_gu;
     } else if (phase == 2 && p.p2split) {
-      const int br = u & 1;
-      U.a0 = U.a1 = p.xu16 + (int64_t)br * T * p.r_gu;
-      U.lda = p.r_gu;
-      U.a_bytes = (uint32_t)((int64_t)T * p.r_gu * 2);
+      // each branch over its own rank
+      const int br = u & 1, rk = br ? p.r_up : p.r_gu;
+      U.a0 = U.a1 = p.xu16 + (br ? (int64_t)T * p.r_gu : 0);
+      U.lda = rk;
+      U.a_bytes = (uint32_t)((int64_t)T * rk * 2);
       U.b0 = U.b1 = br ? p.vu : p.vg;
-      U.ldb = p.ld_v;
-      U.b_bytes = (uint32_t)((int64_t)p.r_gu * p.ld_v * 2);
+      U.ldb = br ? p.ld_vu : p.ld_v;
+      U.b_bytes = (uint32_t)((int64_t)rk * U.ldb * 2);
       U.n0 = (u >> 1) * 128;
       U.kb = 0;
-      U.ke = p.r_gu;
+      U.ke = rk;
       U.dst = p.h;
       U.ldo = p.ff;
-    } else if (phase == 2) {
+    } else if (phase == 2) {  // both branches of 64 columns: one rank (r_up == r_gu), one V pitch
       U.a0 = p.xu16;
       U.a1 = p.xu16 + (int64_t)T * p.r_gu;
       U.lda = p.r_gu;
@@ -977,7 +981,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] { prefetch_w(next_phase); });
   };
 
-  const int nt1 = 2 * (p.r_gu / 128), nt3 = p.r_d / 128, nt4 = p.d / 128;
+  const int nt1 = p.r_gu / 128 + p.r_up / 128, nt3 = p.r_d / 128, nt4 = p.d / 128;
 
   // ---- phase 0 (the MLP block): xn = RMSNorm(x), row b by block b; phase
   // 1's first weight stages stream in at the barrier ----

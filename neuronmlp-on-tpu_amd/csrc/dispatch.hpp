@@ -36,6 +36,7 @@ struct BigDesc {
   bool out_f32;  // fp32 output (split-K partial slices)
   bool fp8 = false;  // fp8 e4m3fn B (natural layout) with per-column scales
   int nw = 8;        // waves per block: 8, or 4 (natural-layout fn-8 STORE tiles)
+  int kg = 1;        // K groups: 1 (256-row tiles), or 2 (128-row tiles, two 32-k halves per stage)
 };
 
 struct BigParams;
@@ -60,6 +61,10 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 hipError_t launch_rmsnorm(const void* x, const float* gain, void* y, int64_t T, int64_t d, float eps, bool bf16,
                           hipStream_t st);
 hipError_t launch_residual_add(const void* x, void* y, int64_t n, bool bf16, hipStream_t st);
+// out[c][r] = in[r][c] for a (rows x cols) bf16 matrix (row pitches ldi, ldo
+// elements): the transposed operands of the reference's TPU launchers.
+hipError_t launch_transpose_bf16(const uint16_t* in, int64_t ldi, uint16_t* out, int64_t ldo, int rows, int cols,
+                                 hipStream_t st);
 // Persistent decode layer (T <= 128): token tiles of 16 * MT rows (MT = 1,
 // 2, 4 or 8), grid = CU count (at most kDlMaxGrid) when the kernel fits one
 // block per CU, else 0.
@@ -82,14 +87,15 @@ hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint1
                               hipStream_t st);
 // Split-K slices of the large-tile kernel in fragment order (out_frag):
 // out[m][n] = bf16(sum_s in[s * sstride + zb * bstride + frag(m, n)]) for
-// tiles of 256 x 32*fn with nw waves, batch entries zb (out batch stride
+// tiles of 256 x 32*fn with nw waves (kg 1) or 128 x 32*fn with K groups
+// (kg 2, nw 8: four wave tiles), batch entries zb (out batch stride
 // obstride elements); with `gate` (bf16 in the same fragment order),
 // out = bf16(SiLU(gate) * sum); with `resid` (bf16, row pitch ldo, batch
 // entry 0), out = bf16(resid + bf16(sum)), the MLP block's residual add.
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
                                    int batch, hipStream_t st, const uint16_t* gate = nullptr,
-                                   const uint16_t* resid = nullptr);
+                                   const uint16_t* resid = nullptr, int kg = 1);
 // fp8 x fp8 GEMM (gemm_f8f8.hpp), nw = 8 or 4 waves: splits > 1 writes fp32
 // fragment-order slices (256 x 128 tiles) for launch_reduce_frag_bf16 (fn 4, nw).
 struct F8Params;

@@ -6,9 +6,9 @@ namespace svdmlp {
 
 namespace {
 
-template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8, int NS = 4>
+template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8, int NS = 4, int KG = 1>
 hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
-  using C = BigCfg<FN, BK, EPI, F32, F8, NW, NS>;
+  using C = BigCfg<FN, BK, EPI, F32, F8, NW, NS, KG>;
   dim3 grid(p.mtiles * p.ntiles, splits, batch);
   hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(C::THREADS), 0, st, p);
   return hipGetLastError();
@@ -18,6 +18,13 @@ hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
 // each in 256-byte rows), the others 4.
 template <int FN, int EPI, bool F32 = false>
 hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st) {
+  // K groups (128-row tiles), natural-layout bf16 B, store epilogues: five
+  // 32 KB stages at 128 columns, four 40 KB stages at 192 (384-byte B rows):
+  // three or two stages in flight (with three 48 KB stages of 512-byte rows
+  // the 192-column tiles waited on their operands)
+  if constexpr ((FN == 4 || FN == 6) && EPI == BEPI_STORE) {
+    if (d.kg == 2) return go<FN, false, EPI, F32, false, 8, FN == 4 ? 5 : 4, 2>(p, splits, batch, st);
+  }
   if constexpr (FN == 8 && EPI == BEPI_STORE) {  // 4-wave instances: natural layout, STORE
     if (d.nw == 4 && !d.b_kc)
       return d.fp8 ? go<FN, false, EPI, F32, true, 4>(p, splits, batch, st)
@@ -57,12 +64,14 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
                                                                int64_t bstride, uint16_t* out, int64_t ldo,
                                                                int64_t obstride, int M, int N, int mtiles, int nw,
                                                                const uint16_t* gate, const uint16_t* resid) {
+  // tiles of (nw / 2) x 2 wave tiles: 256 rows (8 waves of 64, 4 of 128) or
+  // 128 (the K-group tiles' four wave tiles of 64)
   constexpr int ROWS = 16 * FM, COLS = 16 * FN, PITCH = COLS + 8;  // staged row pitch (elements)
   constexpr int Q = FM * FN * 64;                                   // float4s per wave tile
   __shared__ __attribute__((aligned(16))) uint16_t tile[ROWS * PITCH];
   const int zb = blockIdx.y;
   const int unit = blockIdx.x, wave = unit % nw, t_lin = unit / nw;
-  const int m0 = (t_lin % mtiles) * 256 + (wave >> 1) * ROWS;
+  const int m0 = (t_lin % mtiles) * ((nw >> 1) * ROWS) + (wave >> 1) * ROWS;
   const int n0 = (t_lin / mtiles) * (2 * COLS) + (wave & 1) * COLS;
   const float* src = in + (int64_t)zb * bstride + (int64_t)unit * Q * 4 + 4 * threadIdx.x;
   static_assert(Q % 256 == 0, "whole rounds");
@@ -123,7 +132,14 @@ hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstri
 
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
-                                   int batch, hipStream_t st, const uint16_t* gate, const uint16_t* resid) {
+                                   int batch, hipStream_t st, const uint16_t* gate, const uint16_t* resid, int kg) {
+  if (kg == 2) {  // 128-row K-group tiles: four 64-row wave tiles per tile
+    if (nw != 8) return hipErrorInvalidValue;
+    if (fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, 4, batch, gate, resid, st);
+    if (fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, 4, batch, gate, resid, st);
+    return hipErrorInvalidValue;
+  }
+  if (kg != 1) return hipErrorInvalidValue;
   if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
   if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
@@ -135,6 +151,10 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
 
 hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st,
                       const char** why) {
+  if (d.kg != 1 && !(d.kg == 2 && (d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE && !d.fp8 && !d.b_kc && d.nw == 8)) {
+    *why = "big GEMM: K groups take natural-layout bf16 B, store epilogues and 128 x 128 or 128 x 192 tiles";
+    return hipErrorInvalidValue;
+  }
   if (d.fn == 8) return go_e<8>(d, p, splits, batch, st, why);
   if (d.fn == 7) return go_e<7>(d, p, splits, batch, st, why);
   if (d.fn == 6) return go_e<6>(d, p, splits, batch, st, why);

@@ -162,6 +162,18 @@ __device__ __forceinline__ u32x2 add_bf16x4(u32x2 a, u32x2 b) { return u32x2{add
 // 2 (k & 8) moves the second group to the other half.
 __device__ __forceinline__ int bnat_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
 
+// 32-byte unit swizzle of a natural-layout bf16 B row k of 384 bytes (the
+// 192-column K-group tiles: 12 units, so that four 40 KB stages fit LDS).
+// Row k starts at bank group 4 * (k & 1) (of eight 32-byte groups), and
+// physical unit p of row k lies in group (4k + p) mod 8.  A transposing
+// read's 32 lanes read one logical unit u of rows k0 + {0..3, 8..11}
+// (k0 a multiple of 4): XOR with s(k) in 0..3 keeps u inside its aligned
+// group of four (a permutation of the 12 units), and s takes four distinct
+// values over the even rows and over the odd rows of that set, so the eight
+// pieces land on eight distinct bank groups.  s(k + 4) = s(k) and
+// s(k + 32) = s(k), as the upper-half and second-K-group reads need.
+__device__ __forceinline__ int b384_swz(int k) { return ((k >> 1) & 1) | (((k >> 3) & 1) << 1); }
+
 // 16-byte chunk swizzle of an fp8 natural B row k of 256 bytes (one full
 // bank row): lanes 0-15 of a transposing read touch rows k0..k0+7 (bits 0-2
 // spread them over 8 chunks) and lanes 16-31 rows k0+8..k0+15 (bit 3, k & 8,
@@ -201,36 +213,52 @@ struct BigParams {
   int k_split;
 };
 
-template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8, int NS_ = 4>
+template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8, int NS_ = 4, int KG_ = 1>
 struct BigCfg {
-  // NW waves per block in a 2 (n) x NW/2 (m) arrangement: a wave's tile is
-  // (BM / (NW/2)) x 16*FN, i.e. 64 x 16*FN with 8 waves (two per SIMD) or
-  // 128 x 16*FN with 4 (one per SIMD, accumulators in AGPRs), which reads
-  // a third less from LDS per MFMA.
+  // NW waves per block.  KG = 1: a 2 (n) x NW/2 (m) arrangement over a
+  // 256-row tile: a wave's tile is (BM / (NW/2)) x 16*FN, i.e. 64 x 16*FN
+  // with 8 waves (two per SIMD) or 128 x 16*FN with 4 (one per SIMD,
+  // accumulators in AGPRs), which reads a third less from LDS per MFMA.
+  // KG = 2 (K groups): a 128-row tile; the 8 waves form two groups of four
+  // 64 x 16*FN wave tiles (2 x 2), group g taking the g-th 32-k half of
+  // every 64-k stage, and the two groups' sums are added through LDS at the
+  // end.  Each wave keeps the 8-wave tiles' MFMAs and fragment reads per
+  // step, while the block tile halves: twice the output tiles, so the rank
+  // stages need fewer K splits (or none).
   static constexpr int NW = NW_;
+  static constexpr int KG = KG_;
+  static constexpr int WT = NW / KG;                 // wave tiles per block
   static constexpr int THREADS = 64 * NW;
-  static constexpr int FM = 32 / NW, FN = FN_;  // per wave: 16*FM x 16*FN
+  static constexpr int BM = KG == 2 ? 128 : 256;
+  static constexpr int FM = BM / (WT / 2) / 16, FN = FN_;  // per wave: 16*FM x 16*FN
   static constexpr bool B_KC = B_KC_;
   static constexpr int EPI = EPI_;
   static constexpr bool OUT_F32 = OUT_F32_;
   // fp8 e4m3fn B in natural layout: 1-byte elements staged as they lie in
   // HBM, widened to bf16 after the transposing LDS read.
   static constexpr bool FP8_B = FP8_B_;
-  static constexpr int BM = 256, BN = 32 * FN, BK = 32;  // BK per stage
+  static constexpr int BN = 32 * FN, BK = 32 * KG;  // BK: k per stage
   static constexpr int STAGES = NS_;  // LDS stages: NS-2 in flight while one is read
-  static constexpr int A_BYTES = BM * 64;                      // 16 KB
-  // natural-layout B row per k: 256 bytes for fp8 and for bf16 tiles of at most 128 columns, else 512
-  static constexpr int B_PITCH = (FP8_B || (!B_KC && BN <= 128)) ? 256 : 512;
+  // A: BM rows of 64 bytes (32 k) per K group: 16 KB either way
+  static constexpr int A_SUB = BM * 64;
+  static constexpr int A_BYTES = A_SUB * KG;
+  // natural-layout B row per k: 256 bytes for fp8 and for bf16 tiles of at most 128 columns, 384 for the
+  // 192-column K-group tiles (b384_swz), else 512
+  static constexpr int B_PITCH = (FP8_B || (!B_KC && BN <= 128)) ? 256 : ((KG == 2 && BN == 192) ? 384 : 512);
   static constexpr int B_BYTES = B_KC ? 256 * 64 : BK * B_PITCH;  // 16 KB (256-byte rows: 8 KB; Linear: rows >= BN read zeros)
   static constexpr int STAGE = A_BYTES + B_BYTES;
   static constexpr int A_UNITS = A_BYTES / 1024 / NW;  // DMA instructions per wave: 2 (NW 4: 4)
-  static constexpr int B_UNITS = B_BYTES / 1024 / NW;  // 2 (256-byte rows: 1); NW 4: 4 (2)
+  static constexpr int B_UNITS = B_BYTES / 1024 / NW;  // 2 (256-byte rows: 1); NW 4: 4 (2); KG 2: twice
   static_assert(NW == 8 || NW == 4, "8 or 4 waves");
+  static_assert(KG == 1 || (KG == 2 && NW == 8 && !B_KC && !FP8_B && EPI == BEPI_STORE),
+                "K groups: 8 waves, natural-layout bf16 B, store epilogues");
   static_assert(A_UNITS * NW == 16 && B_UNITS * NW * 1024 == B_BYTES, "DMA instructions per wave and stage");
   static_assert(!(FP8_B && B_KC), "fp8 B is read in natural layout only");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");
   static_assert(B_KC ? BN <= 256 : true, "Linear-layout B tile holds at most 256 rows");
-  static_assert(STAGES >= 4 && STAGES * STAGE <= 160 * 1024, "LDS budget");
+  static_assert(STAGES >= 3 && STAGES * STAGE <= 160 * 1024, "LDS budget");
+  // K groups add their sums through LDS: half of each wave's fragments
+  static_assert(KG == 1 || NW * (FM / 2) * FN * 1024 <= STAGES * STAGE, "K-group exchange fits the stages' LDS");
 };
 
 template <class C>
@@ -270,8 +298,11 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lr = lane & 15, lg = lane >> 4;
-  const int wm0 = (wave >> 1) * (16 * FM);
-  const int wn0 = (wave & 1) * (BN / 2);
+  // wave tile wt of the block; K group kg (0 with KG = 1)
+  constexpr int WT = C::WT;
+  const int wt = wave % WT, kg = wave / WT;
+  const int wm0 = (wt >> 1) * (16 * FM);
+  const int wn0 = (wt & 1) * (BN / 2);
 
   const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
   const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
@@ -285,14 +316,16 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // either below kend or wholly past it; stages past it (the pipeline's
   // run-out) use a descriptor with no records and fetch zeros.
   // A: instruction i of this wave fills LDS rows 16*(wave + NW*i) + lane/4;
-  // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row).
+  // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row).  With K groups
+  // the A region of a stage is KG sub-tiles of BM = 128 rows (16 * NW), one
+  // per 32-k half: instruction i fills rows 16*wave + lane/4 of half i.
   const i32x4 r_none = make_rsrc_sgpr(p.a[zb], 0);
   const int a_row0 = 16 * wave + (lane >> 2);
   const int a_kk = 8 * ((lane & 3) ^ a_swz(a_row0));  // k within the stage
   uint32_t a_voff[C::A_UNITS];
 #pragma unroll
   for (int i = 0; i < C::A_UNITS; ++i) {
-    const int row = m0 + a_row0 + 16 * NW * i;
+    const int row = m0 + a_row0 + (C::KG == 1 ? 16 * NW * i : 0);
     a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
   }
   // B natural: instruction i fills LDS k-row 2*(wave + NW*i) + lane/32, slot
@@ -317,6 +350,17 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
       const int col = 16 * ((lane & 15) ^ f8nat_swz(kk));
       b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * (uint32_t)ldb + (uint32_t)(n0 + col) : kOOB;
     }
+  } else if constexpr (C::B_PITCH == 384) {
+    // 384-byte rows: instruction i fills bytes (wave + NW*i) KB .. +1 KB of
+    // the stage's B tile; the lane's 16 bytes are half (byte >> 4) & 1 of
+    // physical unit byte >> 5 of row byte_pos / 384
+#pragma unroll
+    for (int i = 0; i < C::B_UNITS; ++i) {
+      const int pos = (wave + NW * i) * 1024 + 16 * lane;
+      const int kk = pos / 384, byte = pos % 384;
+      const int col = 16 * ((byte >> 5) ^ b384_swz(kk)) + 8 * ((byte >> 4) & 1);
+      b_voff[i] = n0 + col < N ? (uint32_t)kk * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+    }
   } else {
     // instruction i fills RPI k-rows from RPI * (wave + NW * i), LPR lanes per
     // row (512-byte rows: 2 rows of 32 lanes; 256-byte rows: 4 of 16)
@@ -337,7 +381,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     const int k0 = kbeg + kt * BK;
     const bool live = k0 < kend;  // uniform
     if (d < C::A_UNITS) {
-      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
+      const uint32_t ksub = C::KG == 2 ? (uint32_t)(d * 64) : 0u;  // 32-k half of the stage (bytes)
+      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u + ksub, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
     } else {
       const int i = d - C::A_UNITS;
       const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)ldb : (uint32_t)k0 * ldb2);
@@ -350,7 +395,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // A: rows wm0 + 16i + lr share one swizzle; fragment i of stage s is at
   // a_rd + s * A_BYTES + 1 KB * i.
   const lds_cptr l0 = (lds_cptr)lds;
-  const lds_cptr a_rd = l0 + (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
+  // K group kg reads its 32-k half: A sub-tile kg, B k-rows 32*kg ..
+  const lds_cptr a_rd = l0 + kg * C::A_SUB + (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
   // B natural: the lane reads k rows k_lo = 8*lg + lr/4 (and k_lo + 4 for
   // the upper half, same swizzle) in 32-byte unit U = wn0/16 + j for
   // fragment j, stored at unit U ^ bnat_swz(k_lo): fragment j of stage s is
@@ -365,7 +411,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int u = (wn0 >> 4) + j;
-      b_rd[j] = l0 + B_REGION + k_lo * C::B_PITCH + ((u ^ bnat_swz(k_lo)) << 5) + ((lr & 3) << 3);
+      const int pu = C::B_PITCH == 384 ? (u ^ b384_swz(k_lo)) : (u ^ bnat_swz(k_lo));
+      b_rd[j] = l0 + B_REGION + (kg * 32 + k_lo) * C::B_PITCH + (pu << 5) + ((lr & 3) << 3);
     }
   }
   // fp8 B: lane s = lr of group lg points at k-row 8*lg + lr/2, bytes
@@ -481,6 +528,30 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   }
   wait_dma<0>();  // drain DMAs of stages past the end before the block exits
 
+  // K groups: add the two groups' sums.  Group g finishes fragment rows
+  // [g * FM/2, (g+1) * FM/2) of its wave tile: it stores the other half to
+  // LDS (1 KB per fragment, lane-contiguous) for its partner wave (same wave
+  // tile, other group) and adds the partner's half of its own rows.  fp32
+  // addition commutes, so both sides of a pair compute the same bits.
+  if constexpr (C::KG == 2) {
+    constexpr int H = FM / 2;
+    __syncthreads();  // every wave's reads of the last stages are done
+    SVDMLP_LDS char* const lw = (SVDMLP_LDS char*)lds;
+    SVDMLP_LDS char* const xw = lw + ((wt * 2 + kg) * H * FN) * 1024 + 16 * lane;  // this wave's outgoing half
+    const lds_cptr xr = l0 + ((wt * 2 + (kg ^ 1)) * H * FN) * 1024 + 16 * lane;     // the partner's
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if ((i / H) != kg) *reinterpret_cast<SVDMLP_LDS f32x4*>(xw + ((i % H) * FN + j) * 1024) = acc[i][j];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if ((i / H) == kg) acc[i][j] += *reinterpret_cast<const SVDMLP_LDS f32x4*>(xr + ((i % H) * FN + j) * 1024);
+  }
+
   // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
   const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
   char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
@@ -490,7 +561,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // 16 rows x 64 bytes per instruction; 8B layer: epilogue 9.1K -> 6K cycles)
   const bool ffrag = C::OUT_F32 && p.out_frag;
   // fragment-order element offset of this lane's block (0, 0)
-  const int64_t frag0 = ((((int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN)) * NW + wave) * FM * FN) * 256 + 4 * lane;
+  const int64_t frag0 = ((((int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN)) * WT + wt) * FM * FN) * 256 + 4 * lane;
   // SwiGLU: every gate value of the wave's tile is loaded before the first
   // h store (the stores could alias the loads as far as the compiler knows,
   // which would serialise one load round trip per fragment); the main
@@ -516,6 +587,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   }
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
+    if (C::KG == 2 && (i / (FM / 2)) != kg) continue;  // the partner wave's rows
     const int m = m0 + wm0 + 16 * i + lr;
     if (!FRAG && !ffrag && m >= p.M) continue;
 #pragma unroll

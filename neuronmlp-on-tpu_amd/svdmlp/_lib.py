@@ -46,6 +46,7 @@ EXPORTED = (
     "svdmlp_svd_mlp_ranks",
     "svdmlp_svd_mlp_block_ranks",
     "svdmlp_svd_mlp_noalloc",
+    "svdmlp_noalloc_status",
     "svdmlp_profile_enable",
     "svdmlp_profile_read",
     "svdmlp_stage_name",
@@ -99,6 +100,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                                                + [_i64] * 6 + [_i32, _i32, _u32, _vp, _sz, _vp])
     lib.svdmlp_svd_mlp_noalloc.restype = ctypes.c_int
     lib.svdmlp_svd_mlp_noalloc.argtypes = [_vp] * 7 + [_vp, _vp, _vp] + [_i64] * 5 + [_i32, _i32, _u32, _vp]
+    lib.svdmlp_noalloc_status.restype = ctypes.c_int
+    lib.svdmlp_noalloc_status.argtypes = [_i32, _i64, _vp]
     lib.svdmlp_profile_enable.restype = ctypes.c_int
     lib.svdmlp_profile_enable.argtypes = [ctypes.c_int]
     lib.svdmlp_profile_read.restype = ctypes.c_int

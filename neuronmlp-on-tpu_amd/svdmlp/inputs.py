@@ -84,3 +84,26 @@ def as_float32(a: np.ndarray, dtype: torch.dtype) -> np.ndarray:
     if dtype == torch.float32:
         return np.asarray(a, np.float32)
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dtype).float().numpy()
+
+
+def make_outlier_layer(shape: LayerShape, T: int, seed: int = 0, channels=((3, 1e3), (17, 3e3), (250, 1e2)),
+                       col_sigma: float = 1.0):
+    """A heavy-tailed stand-in for a real checkpoint's layer (no checkpoint is
+    available offline; the reference's real-layer check,
+    results/kernel_optimizations_1_4_20260916/real_layer0_S512_check.json:2-3,
+    reports a max |error| of 3.8e6 next to a relative error of 3.1e-3, i.e.
+    outputs in the millions).  x ~ N(0, 1) with a few hidden channels
+    (columns) scaled by 1e2..3e3, the massive-activation pattern of LLaMA
+    hidden states; every factor's columns multiplied by log-normal scales
+    exp(col_sigma * N(0, 1) - col_sigma^2) (heavy-tailed column norms, mean
+    square 1).  Float32, factors gate-first as make_factors."""
+    rng = np.random.default_rng(seed)
+    factors = list(make_factors(shape, rng=rng))
+    for i, f in enumerate(factors):
+        s = np.exp(col_sigma * rng.normal(size=f.shape[1]) - col_sigma * col_sigma).astype(np.float32)
+        factors[i] = (f * s[None, :]).astype(np.float32)
+    x = make_x(rng, T, shape.d)
+    for c, scale in channels:
+        if c < shape.d:
+            x[:, c] *= np.float32(scale)
+    return x, tuple(factors)

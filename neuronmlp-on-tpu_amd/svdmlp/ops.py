@@ -17,6 +17,7 @@ Every call goes to libsvdmlp.so; there is no CPU or PyTorch fallback.
 from __future__ import annotations
 
 import ctypes
+from collections import OrderedDict
 from dataclasses import dataclass
 
 import torch
@@ -410,9 +411,36 @@ def pad_rank(u, v, r: int):
     return up, vp
 
 
+# Zero-padded gate/up factors of the shapes whose kernels take one rank (the
+# SVDMLP_EUNSUP fallback), kept for the most recent layers: keyed by each
+# factor's storage address, version counter (bumped by in-place writes),
+# shape and dtype, so a layer called again reuses its padded copies instead
+# of allocating and copying them on every call.
+_PAD_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_PAD_CACHE_LAYERS = 8
+
+
+def _factor_key(f):
+    t = f.data if isinstance(f, QuantizedFactor) else f
+    k = (t.data_ptr(), t._version, tuple(t.shape), str(t.dtype))
+    if isinstance(f, QuantizedFactor):
+        k += (f.scale.data_ptr(), f.scale._version)
+    return k
+
+
 def _pad_branches(u_gate, v_gate, u_up, v_up):
     r = max(int(u_gate.shape[1]), int(u_up.shape[1]))
-    return (*pad_rank(u_gate, v_gate, r), *pad_rank(u_up, v_up, r))
+    key = tuple(_factor_key(f) for f in (u_gate, v_gate, u_up, v_up))
+    hit = _PAD_CACHE.get(key)
+    if hit is not None:
+        _PAD_CACHE.move_to_end(key)
+        return hit[1]
+    padded = (*pad_rank(u_gate, v_gate, r), *pad_rank(u_up, v_up, r))
+    # the originals are held too, so that their addresses are not reused while the entry lives
+    _PAD_CACHE[key] = ((u_gate, v_gate, u_up, v_up), padded)
+    while len(_PAD_CACHE) > _PAD_CACHE_LAYERS:
+        _PAD_CACHE.popitem(last=False)
+    return padded
 
 
 def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.Tensor | None = None,
@@ -420,9 +448,14 @@ def svd_mlp(x, u_gate, v_gate, u_up, v_up, u_down, v_down, *, workspace: torch.T
             fp8_activations: bool = False) -> torch.Tensor:
     """Full SVD SwiGLU block, fused_xuv(fused_gate_up(x)) with h rounded to
     x.dtype in between (kernels/reference.py:85-93).  The gate, up and down
-    ranks may all differ: the large-tile path (more than 128 tokens) runs
-    each branch at its own rank; other shapes zero-pad the smaller of the
-    gate and up branches, which does not change the result.
+    ranks may all differ: the persistent decode layer (bf16 natural-layout
+    factors, up to 128 tokens, ranks multiples of 128) and the large-tile
+    path (more than 64 tokens) run each branch at its own rank; the other
+    shapes (fp8 or Linear-layout factors at decode token counts, ranks the
+    decode layer's tiles do not divide) zero-pad the smaller of the gate and
+    up branches, which does not change the result but costs a padded copy of
+    both branches' factors (kept for the 8 most recent layers, so repeated
+    calls reuse it).
     ``workspace``/``out`` may be supplied to avoid per-call allocation (see
     :func:`svd_mlp_workspace`, with r the largest rank).  ``contracted``
     asks for the contracted layer (SVDMLP_CONTRACT: h kept inside the

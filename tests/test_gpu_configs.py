@@ -21,8 +21,10 @@ unrounded float64 chain: the GPU chain must be as close to it as the
 oracle's own bf16 chain is (within 25%).
 
 Config 5: the LLaMA3-70B-shape layer (T=2048, d=8192, ff=28672, r=5632) with
-fp8 e4m3 factors and per-output-channel fp32 scales, bf16 activations, on a
-row subset, <= 3e-2 against the oracle's math on the dequantized factors.
+fp8 e4m3 factors and per-output-channel fp32 scales, bf16 activations, on all
+2048 rows and three seeds (bench.py's layer and two more), <= 3e-2 against
+the oracle's math on the dequantized factors; with fp8 activations for h . Ud
+(SVDMLP_FP8_ACT) too, whose margin to 3e-2 is the narrowest on the path.
 """
 
 import math
@@ -94,16 +96,16 @@ def _dequant(qf):
     return table[qf.data.view(torch.uint8).cpu().numpy()] * qf.scale.cpu().numpy()[None, :]
 
 
-def test_config5_70b_fp8_full_shape(gpu):
+@pytest.mark.parametrize("seed", [5, 6, 7])   # 5: bench.py's fp8 layer (seed + 5, seed 0)
+def test_config5_70b_fp8_full_shape(gpu, seed):
     T, d, ff, r = 2048, 8192, 28672, 5632
     g = torch.Generator(device=gpu)
-    g.manual_seed(5)   # bench.py's fp8 layer (seed + 5, seed 0)
+    g.manual_seed(seed)
     fs = [_q(d, r, g, gpu), _q(r, ff, g, gpu), _q(d, r, g, gpu), _q(r, ff, g, gpu), _q(ff, r, g, gpu), _q(r, d, g, gpu)]
     x = torch.randn(T, d, generator=g, device=gpu, dtype=torch.float32).to(torch.bfloat16)
     y = ops.svd_mlp(x, *fs)
     h = ops.fused_gate_up(x, *fs[:4])
-    rows = np.r_[0, 1, 1024, 2047, np.random.default_rng(5).choice(np.arange(2, 2047), 8, replace=False)]
-    idx = torch.from_numpy(rows).to(gpu)
+    idx = torch.arange(T, device=gpu)   # every row
     xs = _np(x[idx])
     deq = [_dequant(f) for f in fs]
     h_ref = O.fused_gate_up_ref(xs, *deq[:4], dtype="bfloat16")
@@ -112,7 +114,8 @@ def test_config5_70b_fp8_full_shape(gpu):
     e_y = O.relative_l2(_np(y[idx]), y_ref)
     yd = ops.fused_xuv(h, *fs[4:])   # the down half as its own entry point, on the GPU's h
     e_d = O.relative_l2(_np(yd[idx]), O.fused_xuv_ref(_np(h[idx]), deq[4], deq[5], dtype="bfloat16"))
-    print(f"config 5 (70B fp8, T={T}): h rel_l2 {e_h:.3e}, layer {e_y:.3e}, down entry {e_d:.3e}")
+    print(f"config 5 (70B fp8, T={T}, seed {seed}, all rows): h rel_l2 {e_h:.3e}, layer {e_y:.3e}, "
+          f"down entry {e_d:.3e}")
     assert np.isfinite(_np(y)).all()
     assert e_h < FP8_TOL and e_y < FP8_TOL and e_d < FP8_TOL
     # fp8 activations for h . Ud (SVDMLP_FP8_ACT): h quantised per token row,

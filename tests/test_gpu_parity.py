@@ -763,8 +763,9 @@ def _two_rank_layer(d, ff, r_g, r_u, r_d, T, seed):
     return _rounded((inputs.make_x(rng, T, d), *f), torch.bfloat16)
 
 
-# T=8 and 96: decode shapes, where the host mirror zero-pads the smaller
-# branch; T=200: split gate/up XU.V passes (one row tile, K split in two per
+# T=8 and 96: decode shapes, the persistent decode layer with each branch at
+# its rank (phase-1 tiles of both branches, one-branch phase-2 units over
+# their own K); T=200: split gate/up XU.V passes (one row tile, K split in two per
 # branch); T=300: fragment-order g pass + SwiGLU pass at each branch's rank;
 # T=1024: split-K X.U with both branches' column tiles in one launch; ranks
 # that are no multiple of the 256-wide tile leave ragged last tiles per branch.
@@ -825,16 +826,19 @@ def test_distinct_gate_up_ranks_block_and_row_pitches(gpu):
 
 
 def test_distinct_gate_up_ranks_abi(gpu):
-    """svdmlp_svd_mlp_ranks runs two ranks on the large-tile path and returns
-    SVDMLP_EUNSUP, with a message, where only one rank is taken."""
+    """svdmlp_svd_mlp_ranks runs two ranks on the decode layer and the
+    large-tile path and returns SVDMLP_EUNSUP, with a message, where only one
+    rank is taken (decode shapes with an up rank the decode layer's 128-column
+    tiles do not divide)."""
     import ctypes
 
     from svdmlp import _lib
 
     lib = _lib.load()
-    d, ff, r_g, r_u, r_d = 1024, 2048, 512, 256, 384
+    d, ff, r_d = 1024, 2048, 384
     ws = None
-    for T, want in ((8, _lib.SVDMLP_EUNSUP), (300, _lib.SVDMLP_OK)):
+    for T, (r_g, r_u), want in ((8, (512, 320), _lib.SVDMLP_EUNSUP), (8, (512, 256), _lib.SVDMLP_OK),
+                                (300, (512, 256), _lib.SVDMLP_OK)):
         xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 970)
         t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
         y = torch.zeros((T, d), dtype=torch.bfloat16, device=gpu)
@@ -845,9 +849,44 @@ def test_distinct_gate_up_ranks_abi(gpu):
                                       torch.cuda.current_stream(gpu).cuda_stream)
         assert rc == want
         if want == _lib.SVDMLP_EUNSUP:
-            assert "large-tile path only" in lib.svdmlp_last_error().decode()
+            assert "persistent decode layer" in lib.svdmlp_last_error().decode()
         else:
             assert _rel(_np(y), O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
+        if T <= 128 and want == _lib.SVDMLP_OK:
+            assert _barrier_state(ws) == (3, 0) and not any(_tile_counters(ws))   # one decode-layer launch
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_distinct_gate_up_ranks_decode_8b(gpu, T):
+    """LLaMA3-8B decode with a gate rank, an up rank and a down rank drawn
+    from BASELINE config 4's menu {2048, ..., 3072}: the layer and the MLP
+    block each run as one decode-layer launch with every branch at its own
+    rank (no zero padding, no allocation with a workspace and out), match
+    the oracle and replay bitwise."""
+    d, ff, r_g, r_u, r_d = 4096, 14336, 2304, 3072, 2560
+    xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 980 + T)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    gain = np.random.default_rng(5).uniform(0.9, 1.1, size=d).astype(np.float32)
+    g = torch.from_numpy(gain).to(gpu)
+    ws = ops.svd_mlp_workspace(t[0], r=max(r_g, r_u, r_d), ff=ff)
+    out = torch.empty((T, d), dtype=torch.bfloat16, device=gpu)
+    y0 = ops.svd_mlp(*t, workspace=ws, out=out).clone()
+    torch.cuda.synchronize(gpu)
+    before = torch.cuda.memory_allocated(gpu)
+    ops.svd_mlp(*t, workspace=ws, out=out)
+    torch.cuda.synchronize(gpu)
+    assert torch.cuda.memory_allocated(gpu) == before   # no padded copies, no allocation
+    ys = [y0, out.clone(), ops.svd_mlp(*t, workspace=ws, out=out).clone()]
+    assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
+    assert torch.equal(ys[0].view(torch.int16), ys[2].view(torch.int16))
+    assert _barrier_state(ws) == (9, 0) and not any(_tile_counters(ws))   # three launches of three barriers
+    err = _rel(_np(ys[0]), O.svd_mlp_ref(xb, *fb, dtype="bfloat16"))
+    print(f"two ranks 8B decode T={T} rel_l2={err:.3e}")
+    assert err < BF16_TOL
+    yb = _np(ops.svd_mlp_block(t[0], g, *t[1:], eps=1e-5, workspace=ws, out=out))
+    ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
+    assert _rel(yb, ref) < BF16_TOL and _rel(yb - xb, ref - xb) < BF16_TOL
+    assert _barrier_state(ws) == (13, 0)   # + one launch of four barriers (RMSNorm phase 0)
 
 
 # ---------------------------------------------------------------------------

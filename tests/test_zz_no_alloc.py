@@ -85,3 +85,93 @@ def test_noalloc_rejects_shapes_beyond_the_scratch(gpu):
     assert rc == _lib.SVDMLP_EINVAL
     msg = lib.svdmlp_last_error().decode()
     assert "fixed scratch" in msg and str(SCRATCH_BYTES) in msg
+
+
+def _noalloc(lib, x, fs, y, dims, dev):
+    T, d, ff, r_gu, r_d = dims
+    bf = _lib.SVDMLP_BF16
+    ld = _ld(fs)   # row pitches: the V factors may be row-padded
+    return lib.svdmlp_svd_mlp_noalloc(x.data_ptr(), *_ptrs(fs), None, ctypes.addressof(ld), y.data_ptr(), T, d, ff,
+                                      r_gu, r_d, bf, bf, 0, torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _status(lib, dev, reset=0, wait_bound=-1):
+    rc = lib.svdmlp_noalloc_status(reset, wait_bound, torch.cuda.current_stream(dev).cuda_stream)
+    assert rc in (0, 1), lib.svdmlp_last_error()
+    return rc
+
+
+def test_noalloc_timeout_poisons_output_and_status_resets(gpu):
+    """A noalloc call whose grid-barrier waits give up (forced from the host
+    with a wait bound of one poll, so every block still runs to its end)
+    writes NaN into y; the scratch's flag stays set, so the next call writes
+    NaN as well, until svdmlp_noalloc_status resets the scratch; then calls
+    compute again (MFMA decode layer, 8 tokens)."""
+    lib = _lib.load()
+    shape, T = inputs.LayerShape(1024, 2048, 512), 8
+    x, f = inputs.make_layer(shape, T=T, seed=93)
+    xb, *fb = [inputs.as_float32(a, torch.bfloat16) for a in (x, *f)]
+    xt = inputs.to_torch(xb, torch.bfloat16, gpu)
+    fs = [inputs.to_torch(a, torch.bfloat16, gpu) for a in fb]
+    dims = (T, shape.d, shape.ff, shape.r, shape.rd)
+    ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
+    y = torch.empty((T, shape.d), dtype=torch.bfloat16, device=gpu)
+
+    def run():
+        assert _noalloc(lib, xt, fs, y, dims, gpu) == 0, lib.svdmlp_last_error()
+        torch.cuda.synchronize(gpu)
+        return y.float().cpu().numpy()
+
+    assert O.relative_l2(run(), ref) < 1e-2
+    assert _status(lib, gpu) == 0
+    _status(lib, gpu, wait_bound=1)
+    assert np.isnan(run()).all()
+    assert _status(lib, gpu) == 1
+    _status(lib, gpu, wait_bound=0)      # the default bound again: the flag still poisons the result
+    assert np.isnan(run()).all()
+    assert _status(lib, gpu, reset=1) == 1   # reports, then zeroes the sync area
+    assert _status(lib, gpu) == 0
+    for _ in range(2):
+        assert O.relative_l2(run(), ref) < 1e-2
+    assert _status(lib, gpu) == 0
+
+
+def test_noalloc_graph_capture_replays(gpu):
+    """The noalloc entry point captured into a graph (torch.cuda.CUDAGraph):
+    every replay, with eager work and synchronisation between replays,
+    writes the eager call's bits, and eager calls change neither torch's
+    allocated bytes nor the device's free memory (hipMemGetInfo)."""
+    lib = _lib.load()
+    shape = inputs.LayerShape(1024, 2048, 512)
+    for T in (8, 1):   # the three-barrier MFMA decode layer, then the contracted one
+        x, f = inputs.make_layer(shape, T=T, seed=95 + T)
+        xb, *fb = [inputs.as_float32(a, torch.bfloat16) for a in (x, *f)]
+        xt = inputs.to_torch(xb, torch.bfloat16, gpu)
+        fs = [ops.pad_rows(a, 64) if i % 2 else a
+              for i, a in enumerate(inputs.to_torch(a, torch.bfloat16, gpu) for a in fb)]
+        dims = (T, shape.d, shape.ff, shape.r, shape.rd)
+        y_eager = torch.empty((T, shape.d), dtype=torch.bfloat16, device=gpu)
+        assert _noalloc(lib, xt, fs, y_eager, dims, gpu) == 0, lib.svdmlp_last_error()
+        torch.cuda.synchronize(gpu)
+        alloc0, free0 = torch.cuda.memory_allocated(gpu), torch.cuda.mem_get_info(gpu)[0]
+        for _ in range(3):
+            assert _noalloc(lib, xt, fs, y_eager, dims, gpu) == 0
+        torch.cuda.synchronize(gpu)
+        assert torch.cuda.memory_allocated(gpu) == alloc0 and torch.cuda.mem_get_info(gpu)[0] == free0
+        y = torch.full((T, shape.d), 3.0, dtype=torch.bfloat16, device=gpu)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            rc = _noalloc(lib, xt, fs, y, dims, gpu)
+        assert rc == 0, lib.svdmlp_last_error()
+        for i in range(3):
+            y.fill_(5.0)
+            torch.cuda.synchronize(gpu)
+            g.replay()
+            torch.cuda.synchronize(gpu)
+            assert torch.equal(y.view(torch.int16), y_eager.view(torch.int16)), (T, i)
+            assert _noalloc(lib, xt, fs, y_eager, dims, gpu) == 0   # eager work between replays
+            torch.cuda.synchronize(gpu)
+        err = O.relative_l2(y.float().cpu().numpy(), O.svd_mlp_ref(xb, *fb, dtype="bfloat16"))
+        assert err < 1e-2, (T, err)
+        del g
+    assert _status(lib, gpu) == 0
