@@ -367,6 +367,37 @@ def _bench_decode_ranks(torch, dev, stream, args, x, rates):
     return out
 
 
+# The reference's own standalone TPU launchers at its headline shape
+# (results/kernel_optimizations_1_4_20260916/real_layer0_S128.json, TPU v5e,
+# median host wall time of the optimized kernels): 8B factors, r=2816, S=128.
+REF_TPU_US_S128 = {"fused_mlp_up_T": 503.6, "fused_three_mm_XTUV": 339.3, "svd_mlp_with_fused_kernel": 698.1}
+
+
+def _bench_launchers(torch, dev, stream, args, layer, x, S=128):
+    """compat.fused_mlp_up_T ((I, S) output) and compat.fused_three_mm_XTUV
+    ((I, S) input) -- test_speedup.py:500-544 -- and their composition
+    (test_speedup.py:631-655) on the 8B factors at S=128, timed back to back
+    like the other lines (GPU only); the reference's TPU figures beside them
+    for context."""
+    from svdmlp import compat
+
+    xs = x[:S].contiguous()
+    ug, vg, uu, vu, ud, vd = layer
+    hT = compat.fused_mlp_up_T(xs, ug, vg, uu, vu)
+    out = {"S": S, "d": D, "ff": FF, "r": R, "reference_tpu_us": REF_TPU_US_S128}
+    calls = {
+        "fused_mlp_up_T": lambda i: compat.fused_mlp_up_T(xs, ug, vg, uu, vu),
+        "fused_three_mm_XTUV": lambda i: compat.fused_three_mm_XTUV(hT, ud, vd),
+        "svd_mlp_with_fused_kernel": lambda i: compat.svd_mlp_with_fused_kernel(xs, uu, vu, ug, vg, ud, vd),
+    }
+    flops = {"fused_mlp_up_T": 2.0 * S * 2 * R * (D + FF), "fused_three_mm_XTUV": 2.0 * S * R * (FF + D),
+             "svd_mlp_with_fused_kernel": 2.0 * S * 3 * R * (D + FF)}
+    for name, fn in calls.items():
+        ms, _ = _time_steps(torch, fn, 100, 20, stream)
+        out[name] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(flops[name] / (ms * 1e-3) / 1e12, 2)}
+    return out
+
+
 def _stack_inputs(torch, dev, args):
     from svdmlp import stack
 
@@ -582,6 +613,8 @@ def main(argv=None) -> int:
             record["decode_dense"] = _bench_decode(torch, dev, stream, args, dense, x, factor_bytes,
                                                    tokens=[t for t in (1, 8, 32, 64) if t <= x.shape[0]],
                                                    rates=rates, layout="natural")
+            if x.shape[0] >= 128:
+                record["launchers_s128"] = _bench_launchers(torch, dev, stream, args, dense[0], x)
             del dense
             record["decode_two_ranks"] = _bench_decode_ranks(torch, dev, stream, args, x, rates)
     if args.only in (None, "stack"):

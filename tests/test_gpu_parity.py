@@ -532,6 +532,12 @@ def test_transposed_launchers_bf16_8b_shape(gpu, layer8b):
     hb = inputs.as_float32(_np(hT).T, torch.bfloat16)
     assert _rel(_np(y), O.fused_xuv_ref(hb, f[4], f[5], "bfloat16")) < BF16_TOL
     assert _rel(_np(y), O.svd_mlp_ref(x, *f, dtype="bfloat16")) < BF16_TOL
+    # the transposed operands ride on the natural-layout kernels (one transpose
+    # pass each): bitwise the natural-layout entry points' results
+    h = ops.fused_gate_up(xt, *ft[:4])
+    assert torch.equal(hT.view(torch.int16), h.t().contiguous().view(torch.int16))
+    yn = ops.fused_xuv(hT.t().contiguous(), ft[4], ft[5])
+    assert torch.equal(y.view(torch.int16), yn.view(torch.int16))
 
 
 # ---------------------------------------------------------------------------
