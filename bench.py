@@ -105,7 +105,7 @@ def _stage_work(T):
     GEMM stage of the prefill layer, keyed by the library's stage names."""
     return {
         "gate_up_xu": (2.0 * T * D * 2 * R, 2 * (T * D + 2 * D * R + 2 * T * R),
-                       "big_gemm_kernel X.[Ug|Uu] (split-K fp32 slices)"),
+                       "big_gemm_kernel X.[Ug|Uu] (1024 tokens: 128x192 K-group tiles, no K split)"),
         "gate_up_xuv_g": (2.0 * T * R * FF, 2 * (T * R + R * FF + T * FF),
                           "big_gemm_kernel XUg.Vg -> bf16 g"),
         "gate_up_xuv_swiglu": (2.0 * T * R * FF, 2 * (T * R + R * FF + 2 * T * FF),
@@ -113,7 +113,7 @@ def _stage_work(T):
         "down_xu": (2.0 * T * FF * R, 2 * (T * FF + FF * R + T * R),
                     "big_gemm_kernel h.Ud (split-K fp32 slices)"),
         "down_xuv": (2.0 * T * R * D, 2 * (T * R + R * D + T * D),
-                     "big_gemm_kernel XUd.Vd (split-K fp32 slices)"),
+                     "big_gemm_kernel XUd.Vd (1024 tokens: 128x128 K-group tiles, no K split)"),
     }
 
 
