@@ -438,6 +438,7 @@ struct Tune {
   bool big = true;    // large-tile path enabled
   bool dlayer = true; // persistent decode layer enabled
   bool gusplit = true; // split-K gate/up XU.V passes at one row tile
+  bool dfn6 = true;    // h.Ud on 256 x 192 tiles where they need no K split and the model rates them cheaper
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -503,6 +504,7 @@ const Tune& tune() {
         if (k == "gusfn") r.gusfn = v;
         if (k == "gusp") r.gusp = v;
         if (k == "gusplit") r.gusplit = v != 0;
+        if (k == "dfn6") r.dfn6 = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -681,6 +683,23 @@ int gate_xu_fn(int64_t T, int64_t K, int64_t r, int batch, int64_t r1 = -1) {
   return c6 < c8 ? 6 : 8;
 }
 
+// Tile width (columns / 32) of the h.Ud stage: 256 x 256, or 256 x 192 where
+// those fill the CUs in one round without a K split and the model rates
+// them cheaper (tune().dfn6).  With splits the model misjudges the narrower
+// tile (8B layer, T=1024: 85.1 against 75.7-76.0 us measured for 256 x 256),
+// without them it saves the slices and their reduction: 70B fp8 layer,
+// T=2048, 240 blocks of 256 x 192 against 176 tiles of 256 x 256 in four
+// splits (704 blocks), h.Ud 521.5-525.7 + 39.5 us (reduction) against
+// 523.8-541.4 us.
+int down_xu_fn(int64_t T, int64_t K, int64_t N) {
+  const int fn = tune().s1;
+  if (fn != 8 || !tune().dfn6) return fn;
+  double c8 = 0.0, c6 = 0.0;
+  plan_ksplit(T, K, N, 8, 1, -1, &c8);
+  const int64_t ks6 = plan_ksplit(T, K, N, 6, 1, -1, &c6);
+  return (ks6 >= K && c6 < c8) ? 6 : 8;
+}
+
 int plan_splits(int64_t T, int64_t K, int64_t N, int fn, int batch, int kg) {
   const int64_t ks = plan_ksplit(T, K, N, fn, batch, -1, nullptr, kg);
   return (int)((K + ks - 1) / ks);
@@ -776,7 +795,7 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
            int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr,
            int64_t ldu = 0) {
-  const int fn1 = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : tune().s1;
+  const int fn1 = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : down_xu_fn(T, K, r);
   const RankPlan pl = plan_rank(T, K, r, fn1, batch, -1, !u_lin && c.wt == SVDMLP_BF16, stage);
   const int fn = pl.fn, kg = pl.kg;
   const int64_t bm = kg == 2 ? 128 : 256;
