@@ -235,3 +235,39 @@ def test_stack_flops_uses_drawn_ranks():
     want = sum(2 * T * ((rg + ru) * (d + ff) + rd * (ff + d)) for rg, ru, rd in (l.ranks for l in layers))
     assert stack.stack_flops(T, d, ff, layers) == want
     assert stack.stack_flops(T, d, ff, layers[1:]) == O.layer_flops(T, d, ff, 2816)
+
+
+def test_padded_branches_are_cached_per_layer():
+    """The zero-padding fallback (shapes whose kernels take one gate/up rank)
+    reuses a layer's padded copies on the next call, and makes new ones once
+    a factor is written in place (its version counter moves)."""
+    ops._PAD_CACHE.clear()
+    ug, vg, uu, vu = (torch.randn(16, 6), torch.randn(6, 12), torch.randn(16, 9), torch.randn(9, 12))
+    first = ops._pad_branches(ug, vg, uu, vu)
+    again = ops._pad_branches(ug, vg, uu, vu)
+    assert all(a is b for a, b in zip(first, again))
+    ug.mul_(2.0)   # in-place write: the cached padded copy is stale
+    fresh = ops._pad_branches(ug, vg, uu, vu)
+    assert fresh[0] is not first[0] and torch.equal(fresh[0][:, :6], ug)
+    for i in range(ops._PAD_CACHE_LAYERS + 3):   # bounded: the oldest layers are dropped
+        ops._pad_branches(torch.randn(16, 6), torch.randn(6, 12), uu, vu)
+    assert len(ops._PAD_CACHE) == ops._PAD_CACHE_LAYERS
+    ops._PAD_CACHE.clear()
+
+
+def test_outlier_layer_generator():
+    """inputs.make_outlier_layer: seeded; the listed hidden channels of x are
+    scaled by their factors; factor columns carry log-normal scales (a few
+    columns far above the median norm); shapes as make_layer."""
+    shape = inputs.LayerShape(512, 1024, 128)
+    x, f = inputs.make_outlier_layer(shape, 64, seed=5)
+    x2, f2 = inputs.make_outlier_layer(shape, 64, seed=5)
+    assert np.array_equal(x, x2) and all(np.array_equal(a, b) for a, b in zip(f, f2))
+    xb, fb = inputs.make_layer(shape, 64, seed=5)
+    assert x.shape == xb.shape and [a.shape for a in f] == [a.shape for a in fb]
+    col_rms = np.sqrt((x ** 2).mean(axis=0))
+    assert col_rms[17] > 1000 and col_rms[3] > 300 and col_rms[250] > 30
+    assert np.median(col_rms) < 2
+    for a in f:
+        norms = np.sqrt((a ** 2).sum(axis=0))
+        assert norms.max() > 5 * np.median(norms)
