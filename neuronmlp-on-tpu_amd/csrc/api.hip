@@ -439,6 +439,7 @@ struct Tune {
   bool dlayer = true; // persistent decode layer enabled
   bool gusplit = true; // split-K gate/up XU.V passes at one row tile
   bool dfn6 = true;    // h.Ud on 256 x 192 tiles where they need no K split and the model rates them cheaper
+  bool hblk = true;    // the fused layer's h in 16 x 16 block-major order between the u pass and h.Ud
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -505,6 +506,7 @@ const Tune& tune() {
         if (k == "gusp") r.gusp = v;
         if (k == "gusplit") r.gusplit = v != 0;
         if (k == "dfn6") r.dfn6 = v != 0;
+        if (k == "hblk") r.hblk = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -556,8 +558,10 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
              int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr, const uint16_t* resid = nullptr,
-             int kg = 1) {
+             int kg = 1, int out_blk = 0, int a_blk = 0) {
   BigParams p{};
+  p.out_blk = out_blk;
+  p.a_blk = a_blk;
   p.resid = resid;
   p.gfrag = gfrag;
   p.out_frag = out_frag;
@@ -792,9 +796,11 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
 // XU_b = A . U_b (b < batch) into bf16 ws.xu_bf16, batch stride T*r.  With
 // too few output tiles for the chip, K is split: each split writes an fp32
 // slice (plain stores) and one pass sums the slices in order into bf16.
+// a_blk: A (h of the fused layer) is 16 x 16 block-major (BigParams::a_blk).
 int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
            int T, int K, int r, int batch, char* ws, const Ws& L, const float* const* su = nullptr,
-           int64_t ldu = 0) {
+           int64_t ldu = 0, bool a_blk = false) {
+  if (a_blk) a_bytes = (int64_t)((T + 15) / 16 * 16) * K * 2;  // whole 16-row blocks
   const int fn1 = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : down_xu_fn(T, K, r);
   const RankPlan pl = plan_rank(T, K, r, fn1, batch, -1, !u_lin && c.wt == SVDMLP_BF16, stage);
   const int fn = pl.fn, kg = pl.kg;
@@ -816,14 +822,15 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
   const float* s1 = su && batch > 1 ? su[1] : s0;
   if (splits == 1)
     return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
-                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, nullptr, nullptr, kg);
+                    BEPI_STORE, K, xu, r, (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, nullptr, nullptr, kg, 0,
+                    a_blk);
   float* part = reinterpret_cast<float*>(ws + L.part);
   const int nw = kg == 2 ? 8 : big_nw(fn, BEPI_STORE, u_lin);
   if (kg == 2 || big_frag_reduce_ok(fn, nw)) {
     // slices in fragment order: per split, `batch` blocks of whole tiles
     const int64_t tp = (T + bm - 1) / bm * bm, np = ((int64_t)r + 32 * fn - 1) / (32 * fn) * (32 * fn), per = tp * np;
     int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn, BEPI_STORE, ks,
-                      part, r, per, nullptr, true, batch * per, s0, s1, 0, 1, nullptr, nullptr, kg);
+                      part, r, per, nullptr, true, batch * per, s0, s1, 0, 1, nullptr, nullptr, kg, 0, a_blk);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
     return check(launch_reduce_frag_bf16(part, splits, batch * per, per, xu, r, (int64_t)T * r, T, r, (int)(tp / bm),
@@ -832,7 +839,8 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
   }
   const int64_t slice = (int64_t)batch * T * r;
   int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u1, ldb, u_bytes, u_lin, T, r, K, batch, fn,
-                    BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice, s0, s1);
+                    BEPI_STORE, ks, part, r, (int64_t)T * r, nullptr, true, slice, s0, s1, 0, 0, nullptr, nullptr, 1, 0,
+                    a_blk);
   if (rc) return rc;
   StageScope fin(ST_FINALIZE, c.st);
   return check(launch_reduce_bf16(part, splits, slice, xu, slice, c.st), "split-K reduce");
@@ -841,10 +849,16 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
 // out = SiLU(XUg . Vg) * (XUu . Vu): a g pass (bf16 g to the workspace) and a
 // u pass whose epilogue applies SiLU(g) * u.
 // The up branch's rank r_u may differ from the gate branch's r (0: the same).
+// h_blk (optional): asks for h in 16 x 16 block-major order (the fused
+// layer's h.Ud stage reads it so: BigParams::a_blk) and reports whether the
+// pass wrote it so (the split passes at one or two row tiles write
+// row-major h).
 int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, const void* vg, const void* vu,
                bool v_lin, int T, int r, int ff, uint16_t* gbuf, void* out, float* part, int64_t part_cap,
                const float* s_vg = nullptr, const float* s_vu = nullptr, int64_t ldv = 0, int r_u = 0,
-               int64_t ldv_u = 0) {
+               int64_t ldv_u = 0, bool* h_blk = nullptr) {
+  const bool want_blk = h_blk && *h_blk && ff % 16 == 0;
+  if (h_blk) *h_blk = false;
   if (r_u <= 0) r_u = r;
   int fn = tune().s2fn;
   // 256 x 224 tiles (fn 7) leave most CUs idle at one or two 256-row tiles
@@ -883,8 +897,10 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,
                     1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);
   if (rc) return rc;
+  if (want_blk) *h_blk = true;
   return big_gemm(c, ST_GU_XUV, xu_u, nullptr, r_u, xuu_bytes, vu, nullptr, ldb_u, vu_bytes, v_lin, T, ff, r_u, 1,
-                  fn, BEPI_SWIGLU_MEM, r_u, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1);
+                  fn, BEPI_SWIGLU_MEM, r_u, out, ff, 0, gbuf, false, 0, s_vu, nullptr, 1, 0, nullptr, nullptr, 1,
+                  want_blk ? 1 : 0);
 }
 
 // fp8 activations for h . Ud (SVDMLP_FP8_ACT): h quantised to e4m3 per
@@ -1726,15 +1742,19 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
+    // h in 16 x 16 block-major order between the u pass and h.Ud (the fp8
+    // activation path quantises row-major h)
+    const bool f8a = fp8_act && f8_down_ok(T, ff, r_d, ld.ud);
+    bool hblk = !f8a && tune().hblk;
     if ((rc = big_swiglu(c, xu, xu + T * r_g, vg, vu, v_lin, (int)T, (int)r_g, (int)ff, gbuf, hbuf,
                          reinterpret_cast<float*>(ws + L.part), (int64_t)(L.norm - L.part), S[1], S[3], ld.v,
-                         (int)r_u, ld.vu)))
+                         (int)r_u, ld.vu, &hblk)))
       return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};
-    if (fp8_act && f8_down_ok(T, ff, r_d, ld.ud)) {
+    if (f8a) {
       if ((rc = f8_down_xu(c, hbuf, ud, S[4], ld.ud, (int)T, (int)ff, (int)r_d, ws, L))) return rc;
-    } else if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) {
+    } else if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud, hblk))) {
       return rc;
     }
     return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);
@@ -1830,14 +1850,17 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
     const uint16_t* xu = reinterpret_cast<const uint16_t*>(ws + L.xu_bf16);
     uint16_t* hbuf = reinterpret_cast<uint16_t*>(ws + L.h);
     uint16_t* gbuf = reinterpret_cast<uint16_t*>(ws + L.g);
+    const bool f8a = fp8_act && f8_down_ok(T, ff, r_d, ld.ud);
+    bool hblk = !f8a && tune().hblk;
     if ((rc = big_swiglu(c, xu, xu + T * r_gu, vg, vu, v_lin, T, r_gu, ff, gbuf, hbuf,
-                         reinterpret_cast<float*>(ws + L.part), (int64_t)(L.norm - L.part), S[1], S[3], ld.v)))
+                         reinterpret_cast<float*>(ws + L.part), (int64_t)(L.norm - L.part), S[1], S[3], ld.v, 0, 0,
+                         &hblk)))
       return rc;
     const void* ud1[1] = {ud};
     const float* sud[1] = {S[4]};
-    if (fp8_act && f8_down_ok(T, ff, r_d, ld.ud)) {
+    if (f8a) {
       if ((rc = f8_down_xu(c, hbuf, ud, S[4], ld.ud, (int)T, (int)ff, (int)r_d, ws, L))) return rc;
-    } else if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud))) {
+    } else if ((rc = big_xu(c, ST_D_XU, hbuf, ff, T * ff * 2, ud1, u_lin, T, ff, r_d, 1, ws, L, sud, ld.ud, hblk))) {
       return rc;
     }
     return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);

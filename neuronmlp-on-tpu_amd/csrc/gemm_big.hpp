@@ -202,6 +202,12 @@ struct BigParams {
   const float* scale[2]; // fp8 B: one fp32 scale per output column, per batch entry
   const uint16_t* resid; // bf16 STORE epilogue, batch entry 0 (the MLP block's last stage): out = bf16(resid + bf16(C)), row pitch ldo[0]
   int gfrag;             // BEPI_SWIGLU_MEM: gmem holds g in fragment order (BEPI_STORE_FRAG)
+  // 16 x 16 block-major bf16 (element (m, n) of a matrix with `cols` columns
+  // at ((m / 16) * (cols / 16) + n / 16) * 256 + (m % 16) * 16 + n % 16):
+  // out_blk -- the SwiGLU output h (cols = N[0]; one 512-byte block per
+  // fragment store); a_blk -- the A operand (cols = K), whose 16-row,
+  // 32-k DMA pieces are then 1 KB contiguous
+  int out_blk, a_blk;
   int out_frag;          // fp32 output (split-K slices) in fragment order, padded tiles included
   int M, K;
   int N[2];    // output columns per batch entry
@@ -326,7 +332,12 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 #pragma unroll
   for (int i = 0; i < C::A_UNITS; ++i) {
     const int row = m0 + a_row0 + (C::KG == 1 ? 16 * NW * i : 0);
-    a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
+    if (p.a_blk) {  // block (row / 16, k / 16), row % 16, k % 16 (k = a_kk within the stage)
+      const uint32_t blk = (uint32_t)(row >> 4) * (uint32_t)(p.K >> 4) + (uint32_t)(a_kk >> 4);
+      a_voff[i] = row < p.M ? (blk * 256u + (uint32_t)(row & 15) * 16u + (uint32_t)(a_kk & 15)) * 2u : kOOB;
+    } else {
+      a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
+    }
   }
   // B natural: instruction i fills LDS k-row 2*(wave + NW*i) + lane/32, slot
   // lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
@@ -381,8 +392,10 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     const int k0 = kbeg + kt * BK;
     const bool live = k0 < kend;  // uniform
     if (d < C::A_UNITS) {
-      const uint32_t ksub = C::KG == 2 ? (uint32_t)(d * 64) : 0u;  // 32-k half of the stage (bytes)
-      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 * 2u + ksub, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
+      // k0 * 2 bytes along a row-major row, k0 * 32 (two 512-byte blocks per 32 k) in block-major A
+      const uint32_t kshift = p.a_blk ? 5u : 1u;
+      const uint32_t ksub = C::KG == 2 ? (uint32_t)(d * 32) << kshift : 0u;  // 32-k half of the stage (bytes)
+      dma16(live ? ra : r_none, a_voff[d], ((uint32_t)k0 << kshift) + ksub, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
     } else {
       const int i = d - C::A_UNITS;
       const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)ldb : (uint32_t)k0 * ldb2);
@@ -616,7 +629,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         const u32x2 g = gv[i][j];
         const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
         const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) =
+        const int64_t ob = p.out_blk ? (((int64_t)(m >> 4) * (N >> 4) + (n >> 4)) * 256 + (m & 15) * 16 + (n & 15)) : o;
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + ob) =
             u32x2{pack_bf16x2(silu_f32(g0) * v.x, silu_f32(g1) * v.y),
                   pack_bf16x2(silu_f32(g2) * v.z, silu_f32(g3) * v.w)};
       } else {
