@@ -452,6 +452,9 @@ struct Tune {
   int kg = 1;          // K-group 128-row tiles for the rank stages: 0 never, 1 where the planner rates them cheaper, 2 always
   int kgw = 125;       // planner: cycles of a K-group 64-k step, percent of a 256-row tile's 32-k step
   int kgs = 7;         // stages that may take K-group tiles: 1 gate/up X.U, 2 h.Ud, 4 XU_d.Vd
+  // decode layer: most K splits of phases 1, 3, 4 (0: grid / tiles; dls4 -1:
+  // 4 at four token tiles, else grid / tiles)
+  int dls1 = 0, dls3 = 0, dls4 = -1;
 };
 
 const Tune& tune();
@@ -516,6 +519,9 @@ const Tune& tune() {
         if (k == "kg") r.kg = v;
         if (k == "kgw") r.kgw = v;
         if (k == "kgs") r.kgs = v;
+        if (k == "dls1") r.dls1 = v;
+        if (k == "dls3") r.dls3 = v;
+        if (k == "dls4") r.dls4 = v;
       }
       pos = end + 1;
     }
@@ -1092,8 +1098,9 @@ bool decode_layer_ok(const Common& c, int64_t T, int64_t d, int64_t ff, int64_t 
 // Split-K plan of one decode-layer phase: `tiles` 128-column tiles over K;
 // as many splits as keep tiles * splits within the grid, K per split a
 // multiple of 32.  Returns the K per split; *units = tiles * splits.
-int dl_plan(int64_t K, int64_t tiles, int grid, int* units) {
-  const int64_t s = std::max<int64_t>(1, grid / std::max<int64_t>(1, tiles));
+int dl_plan(int64_t K, int64_t tiles, int grid, int* units, int max_s = 0) {
+  int64_t s = std::max<int64_t>(1, grid / std::max<int64_t>(1, tiles));
+  if (max_s > 0) s = std::min<int64_t>(s, max_s);
   int64_t ks = ((K + s - 1) / s + 31) / 32 * 32;
   ks = std::min(ks, K);
   *units = (int)(tiles * ((K + ks - 1) / ks));
@@ -1148,7 +1155,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.r_gu = (int)r_gu;
   p.r_up = (int)r_u;
   p.r_d = (int)r_d;
-  p.ks1 = dl_plan(d, (r_gu + r_u) / 128, grid, &p.units1);
+  p.ks1 = dl_plan(d, (r_gu + r_u) / 128, grid, &p.units1, tune().dls1);
   p.units2 = (int)(ff / 64);
   // Phase 2 with one branch per unit over 128 columns (units 2t, 2t+1: g
   // and u of tile t) instead of both over 64; the pair meets through a tile
@@ -1163,8 +1170,13 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   const bool p2_pays = mt >= 2 || ld.dense;
   p.p2split = !contract && p2split_fits(d, ff, r_gu, r_d, grid, r_u) &&
               (two || tune().p2split >= 2 || (tune().p2split == 1 && p2_pays));
-  p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3);
-  p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4);
+  p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3, tune().dls3);
+  // Phase 4 at four token tiles (33-64 tokens) in at most 4 K splits: each
+  // tile's last split then sums 4 slices of 64 rows instead of 8, for a
+  // stream that is HBM-bound either way (8B layer, T=64: 90.5 -> 89.2 us;
+  // at 1-32 tokens 4 splits cost 0.5-1 us, their slices being small).
+  const int cap4 = tune().dls4 >= 0 ? tune().dls4 : (mt == 4 ? 4 : 0);
+  p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4, cap4);
   p.splits1 = p.units1 / (int)((r_gu + r_u) / 128);
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
