@@ -55,6 +55,9 @@ def _args(argv=None):
     p.add_argument("--layers", type=int, default=4, help="synthetic layers the steps rotate over")
     p.add_argument("--decode-steps", type=int, default=200)
     p.add_argument("--decode-tokens", type=int, nargs="*", default=[1, 2, 8, 32, 64])
+    p.add_argument("--no-decode-extra", action="store_true",
+                   help="decode: the padded-layout lines only (no dense-layout, launcher or two-rank lines), "
+                        "for profiler runs")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=("prefill", "decode", "stack", "fp8"), default=None,
@@ -612,7 +615,7 @@ def main(argv=None) -> int:
 
     if args.only in (None, "decode"):
         record["decode"] = _bench_decode(torch, dev, stream, args, layers, x, factor_bytes)
-        if args.weights_layout == "padded":
+        if args.weights_layout == "padded" and not args.no_decode_extra:
             # the dense natural-layout factors kernels/reference.py takes, at the
             # config-3 token counts, on the same box and HBM rates
             dense = [_layer_weights(torch, dev, args.seed + i) for i in range(args.layers)]
