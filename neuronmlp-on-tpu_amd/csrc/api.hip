@@ -440,6 +440,7 @@ struct Tune {
   bool gusplit = true; // split-K gate/up XU.V passes at one row tile
   bool dfn6 = true;    // h.Ud on 256 x 192 tiles where they need no K split and the model rates them cheaper
   bool hblk = true;    // the fused layer's h in 16 x 16 block-major order between the u pass and h.Ud
+  bool qblk = true;    // e4m3 h (SVDMLP_FP8_ACT) in 16 x 128 blocks between the quantisation and h.Ud
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -510,6 +511,7 @@ const Tune& tune() {
         if (k == "gusplit") r.gusplit = v != 0;
         if (k == "dfn6") r.dfn6 = v != 0;
         if (k == "hblk") r.hblk = v != 0;
+        if (k == "qblk") r.qblk = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -915,8 +917,8 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
 // scales to xu32 (unused on the large-tile path).
 bool f8_down_ok(int64_t T, int64_t ff, int64_t r_d, int64_t ldud) {
   const int64_t lim = (int64_t)1 << 31;  // 32-bit buffer offsets of e4m3 h and Ud
-  return T > kDecodeMaxT && ff % 128 == 0 && r_d % 16 == 0 && ldud % 16 == 0 && ff <= 32768 && T * ff < lim &&
-         ff * ldud < lim;
+  return T > kDecodeMaxT && ff % 128 == 0 && r_d % 16 == 0 && ldud % 16 == 0 && ff <= 32768 &&
+         (T + 15) / 16 * 16 * ff < lim && ff * ldud < lim;
 }
 
 int f8_down_xu(const Common& c, const uint16_t* h, const void* ud, const float* sud, int64_t ldud, int T, int ff,
@@ -926,15 +928,19 @@ int f8_down_xu(const Common& c, const uint16_t* h, const void* ud, const float* 
   uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
   const char* why = nullptr;
   int rc;
+  // e4m3 h in 16 x 128 blocks: each 128-k stage of 16 rows is one 2 KB run
+  // (the g region holds whole 256-row tiles, so the last block's rows fit)
+  const bool blk = tune().qblk;
   {
     StageScope ss(ST_QUANT, c.st);
-    rc = check(launch_quant_rows_e4m3(h, ff, hq, ff, hs, T, ff, c.st, &why), "e4m3 row quantisation", why);
+    rc = check(launch_quant_rows_e4m3(h, ff, hq, ff, hs, T, ff, c.st, &why, blk), "e4m3 row quantisation", why);
   }
   if (rc) return rc;
   F8Params p{};
   p.a = hq;
+  p.a_blk = blk ? 1 : 0;
   p.b = static_cast<const uint8_t*>(ud);
-  p.a_bytes = (uint32_t)((int64_t)T * ff);
+  p.a_bytes = (uint32_t)((int64_t)(blk ? (T + 15) / 16 * 16 : T) * ff);
   p.b_bytes = (uint32_t)((int64_t)ff * ldud);
   p.lda = ff;
   p.ldb = ldud;

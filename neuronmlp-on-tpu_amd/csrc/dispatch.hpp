@@ -101,8 +101,10 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
 struct F8Params;
 hipError_t launch_f8_gemm(const F8Params& p, int splits, int nw, hipStream_t st, const char** why);
 // e4m3fn row quantisation: q[m] = e4m3(h[m] * 448 / amax_m), s[m] = amax_m / 448.
+// blk: q in 16 x 128 blocks ((m, k) at ((m/16)*(n/128) + k/128)*2048 +
+// (m%16)*128 + k%128; n a multiple of 128, ldq unused), the fp8 GEMM's a_blk.
 hipError_t launch_quant_rows_e4m3(const uint16_t* h, int64_t ldh, uint8_t* q, int64_t ldq, float* s, int rows, int n,
-                                  hipStream_t st, const char** why);
+                                  hipStream_t st, const char** why, bool blk = false);
 hipError_t launch_finalize(const float* g, const float* u, int64_t ldi, uint16_t* out, int64_t ldo, int rows,
                            int cols, bool swiglu, bool out_t, hipStream_t st);
 

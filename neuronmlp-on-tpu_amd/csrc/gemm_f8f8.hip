@@ -12,7 +12,7 @@ namespace {
 // One block per row; each thread keeps its 8-element pieces in registers
 // between the amax and the conversion pass (n <= 8 * kF8Threads * kF8QPieces).
 __global__ __launch_bounds__(kF8Threads) void quant_rows_e4m3_kernel(const uint16_t* h, int64_t ldh, uint8_t* q,
-                                                                     int64_t ldq, float* s, int n) {
+                                                                     int64_t ldq, float* s, int n, int blk) {
   __shared__ float part[kF8Threads / 64];
   const int64_t row = blockIdx.x;
   const uint16_t* hr = h + row * ldh;
@@ -35,7 +35,8 @@ __global__ __launch_bounds__(kF8Threads) void quant_rows_e4m3_kernel(const uint1
   for (int w = 1; w < kF8Threads / 64; ++w) amax = fmaxf(amax, part[w]);
   const float inv = amax > 0.f ? 448.0f / amax : 1.0f;
   if (threadIdx.x == 0) s[row] = amax > 0.f ? amax / 448.0f : 1.0f;
-  uint8_t* qr = q + row * ldq;
+  // row-major, or 16 x 128 blocks (2 KB each; a thread's 8 bytes never cross one)
+  uint8_t* qr = blk ? q + (row >> 4) * (int64_t)(n >> 7) * 2048 + (row & 15) * 128 : q + row * ldq;
 #pragma unroll
   for (int i = 0; i < kF8QPieces; ++i) {
     const int e = 8 * ((int)threadIdx.x + kF8Threads * i);
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(kF8Threads) void quant_rows_e4m3_kernel(const uint1
                                                         __uint_as_float(x.z & 0xffff0000u) * inv, 0, false);
       o.y = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(x.w << 16) * inv,
                                                         __uint_as_float(x.w & 0xffff0000u) * inv, (int)o.y, true);
-      *reinterpret_cast<u32x2*>(qr + e) = o;
+      *reinterpret_cast<u32x2*>(qr + (blk ? (e >> 7) * 2048 + (e & 127) : e)) = o;
     }
   }
 }
@@ -79,13 +80,13 @@ hipError_t launch_f8_gemm(const F8Params& p, int splits, int nw, hipStream_t st,
 }
 
 hipError_t launch_quant_rows_e4m3(const uint16_t* h, int64_t ldh, uint8_t* q, int64_t ldq, float* s, int rows, int n,
-                                  hipStream_t st, const char** why) {
-  if (n % 8 || n > 8 * kF8Threads * kF8QPieces || ldh % 8 || ldq % 8) {
-    *why = "e4m3 row quantisation: row length a multiple of 8 and at most 32768, pitches multiples of 8";
+                                  hipStream_t st, const char** why, bool blk) {
+  if (n % 8 || n > 8 * kF8Threads * kF8QPieces || ldh % 8 || ldq % 8 || (blk && n % 128)) {
+    *why = "e4m3 row quantisation: row length a multiple of 8 (of 128 in blocks) and at most 32768, pitches multiples of 8";
     return hipErrorInvalidValue;
   }
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(quant_rows_e4m3_kernel, dim3(rows), dim3(kF8Threads), 0, st, h, ldh, q, ldq, s, n);
+  hipLaunchKernelGGL(quant_rows_e4m3_kernel, dim3(rows), dim3(kF8Threads), 0, st, h, ldh, q, ldq, s, n, blk ? 1 : 0);
   return hipGetLastError();
 }
 

@@ -51,6 +51,10 @@ struct F8Params {
   int M, N, K;
   int mtiles, ntiles;
   int k_split;  // K per split, a multiple of 128
+  // A in 16 x 128 blocks: (m, k) at ((m/16)*(K/128) + k/128)*2048 + (m%16)*128
+  // + k%128 (lda unused; a_bytes covers whole 16-row blocks).  A stage's 16
+  // rows are then one 2 KB run instead of 16 lines at the row pitch.
+  int a_blk;
 };
 
 constexpr int kF8Threads = 512;  // the row quantisation's block
@@ -119,7 +123,10 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
   for (int i = 0; i < A_UNITS; ++i) {
     const int row = 8 * (wave + NW * i) + (lane >> 3);
     const int lc = (lane & 7) ^ (row & 7);
-    a_voff[i] = m0 + row < p.M ? (uint32_t)((int64_t)(m0 + row) * p.lda) + 16u * (uint32_t)lc : kOOB;
+    const int m = m0 + row;
+    const uint32_t base = p.a_blk ? (uint32_t)((m >> 4) * (int64_t)(p.K >> 7) * 2048 + (m & 15) * 128)
+                                  : (uint32_t)((int64_t)m * p.lda);
+    a_voff[i] = m < p.M ? base + 16u * (uint32_t)lc : kOOB;
   }
 #pragma unroll
   for (int i = 0; i < B_UNITS; ++i) {
@@ -127,11 +134,12 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
     const int col = 16 * ((lane & 7) ^ f8b_swz(kr));
     b_voff[i] = n0 + col < p.N ? (uint32_t)((int64_t)kr * p.ldb) + (uint32_t)(n0 + col) : kOOB;
   }
+  const uint32_t a_kshift = p.a_blk ? 4u : 0u;  // k0 (a multiple of 128) -> its block's offset, k0 / 128 * 2048
   auto dma_one = [&](int kt, int s, int d) {
     const int k0 = kbeg + kt * kF8BK;
     const bool live = k0 < kend;  // uniform
     if (d < A_UNITS)
-      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0, lbase + s * kF8ABytes + (wave + NW * d) * 1024);
+      dma16(live ? ra : r_none, a_voff[d], (uint32_t)k0 << a_kshift, lbase + s * kF8ABytes + (wave + NW * d) * 1024);
     else
       dma16(live ? rb : r_none, b_voff[d - A_UNITS], (uint32_t)((int64_t)k0 * p.ldb),
             lbase + B_REGION + s * kF8BBytes + (wave + NW * (d - A_UNITS)) * 1024);
