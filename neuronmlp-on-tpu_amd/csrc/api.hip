@@ -441,6 +441,7 @@ struct Tune {
   bool dfn6 = true;    // h.Ud on 256 x 192 tiles where they need no K split and the model rates them cheaper
   bool hblk = true;    // the fused layer's h in 16 x 16 block-major order between the u pass and h.Ud
   bool qblk = true;    // e4m3 h (SVDMLP_FP8_ACT) in 16 x 128 blocks between the quantisation and h.Ud
+  bool f8tail = true;  // fp8 x fp8 h.Ud: whole rounds of tiles without a split, K splits for the rest only
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -512,6 +513,7 @@ const Tune& tune() {
         if (k == "dfn6") r.dfn6 = v != 0;
         if (k == "hblk") r.hblk = v != 0;
         if (k == "qblk") r.qblk = v != 0;
+        if (k == "f8tail") r.f8tail = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -953,39 +955,77 @@ int f8_down_xu(const Common& c, const uint16_t* h, const void* ud, const float* 
   p.ntiles = (r + kF8BN - 1) / kF8BN;
   // K splits: rounds of 256 blocks x (128-k steps x ~1100 cycles + ~20K per
   // block) + the fp32 slices written and read back (~2800 bytes per cycle),
-  // within the workspace's slice area
-  const int64_t per = (int64_t)p.mtiles * kF8BM * p.ntiles * kF8BN;
+  // within the workspace's slice area.  Either every tile in s splits, or
+  // (split tail) the first whole rounds of tiles (whole n-tile columns)
+  // without a split and only the remaining tiles in s splits, in a second
+  // launch: at the 70B shape (2048 tokens, 352 tiles) 256 tiles in one round
+  // and 96 in two splits (192 blocks), against 704 blocks in 2.75 rounds,
+  // with a quarter of the slices to sum.
+  const int64_t tile_elems = (int64_t)kF8BM * kF8BN;
+  const int64_t per = (int64_t)p.mtiles * p.ntiles * tile_elems;
   const int blocks = p.mtiles * p.ntiles, ksteps = ff / kF8BK;
-  int splits = 1;
+  const int64_t slice_cap = (int64_t)(L.norm - L.part);
+  auto round_cost = [&](int nblocks, int s) {
+    return (double)((nblocks + 255) / 256) * (((ksteps + s - 1) / s) * 1100.0 + 20000.0);
+  };
+  int splits = 1, head = 0;  // head: tiles run without a split ahead of the split launch (0: none)
   double best = 0;
   for (int s = 1; s <= 4; ++s) {
-    if (s > 1 && (int64_t)s * per * 4 > (int64_t)(L.norm - L.part)) break;
-    const int steps = (ksteps + s - 1) / s;
-    const double cost = (double)((blocks * s + 255) / 256) * (steps * 1100.0 + 20000.0) +
-                        (s > 1 ? (double)s * per * 8 / 2800.0 : 0.0);
+    if (s > 1 && (int64_t)s * per * 4 > slice_cap) break;
+    const double cost = round_cost(blocks * s, s) + (s > 1 ? (double)s * per * 8 / 2800.0 : 0.0);
     if (s == 1 || cost < best) {
       best = cost;
       splits = s;
     }
   }
+  const int full = blocks / 256 * 256 / p.mtiles * p.mtiles;  // whole rounds of whole n-tile columns
+  if (tune().f8tail && full > 0 && full < blocks) {
+    const int rem = blocks - full;
+    for (int s = 2; s <= 4; ++s) {
+      if ((int64_t)s * per * 4 > slice_cap) break;
+      const double cost = round_cost(full, 1) + round_cost(rem * s, s) + (double)s * rem * tile_elems * 8 / 2800.0;
+      if (cost < best) {
+        best = cost;
+        splits = s;
+        head = full;
+      }
+    }
+  }
+  const int nw = tune().f8nw;
+  if (head > 0) {  // the head tiles: one split, bf16 out
+    F8Params q = p;
+    q.tile0 = 0;
+    q.tiles = head;
+    q.k_split = ff;
+    q.out = xu;
+    q.ldo = r;
+    StageScope ss(ST_D_XU_F8, c.st);
+    if ((rc = check(launch_f8_gemm(q, 1, nw, c.st, &why), "fp8 x fp8 GEMM", why))) return rc;
+  }
+  p.tile0 = head;
+  p.tiles = blocks - head;
   p.k_split = ((ksteps + splits - 1) / splits) * kF8BK;
   splits = (ff + p.k_split - 1) / p.k_split;
   if (splits == 1) {
     p.out = xu;
     p.ldo = r;
     StageScope ss(ST_D_XU_F8, c.st);
-    return check(launch_f8_gemm(p, 1, tune().f8nw, c.st, &why), "fp8 x fp8 GEMM", why);
+    return check(launch_f8_gemm(p, 1, nw, c.st, &why), "fp8 x fp8 GEMM", why);
   }
   float* part = reinterpret_cast<float*>(ws + L.part);
   p.out = part;
   p.out_sstride = per;
   {
     StageScope ss(ST_D_XU_F8, c.st);
-    if ((rc = check(launch_f8_gemm(p, splits, tune().f8nw, c.st, &why), "fp8 x fp8 GEMM", why))) return rc;
+    if ((rc = check(launch_f8_gemm(p, splits, nw, c.st, &why), "fp8 x fp8 GEMM", why))) return rc;
   }
+  // the split tiles are whole n-tile columns from column n_base: their slices
+  // (indexed by the global tile) from tile `head` on, their output columns
+  // from n_base on
+  const int n_base = head / p.mtiles * kF8BN;
   StageScope fin(ST_FINALIZE, c.st);
-  return check(launch_reduce_frag_bf16(part, splits, per, per, xu, r, (int64_t)T * r, T, r, p.mtiles, p.ntiles, 4,
-                                       tune().f8nw, 1, c.st),
+  return check(launch_reduce_frag_bf16(part + head * tile_elems, splits, per, per, xu + n_base, r, (int64_t)T * r, T,
+                                       r - n_base, p.mtiles, p.ntiles - head / p.mtiles, 4, nw, 1, c.st),
                "split-K reduce");
 }
 

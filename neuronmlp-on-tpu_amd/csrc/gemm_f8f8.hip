@@ -64,7 +64,11 @@ hipError_t launch_f8_gemm(const F8Params& p, int splits, int nw, hipStream_t st,
     *why = "fp8 x fp8 GEMM: K and K per split multiples of 128, N and pitches multiples of 16, aligned scales";
     return hipErrorInvalidValue;
   }
-  const dim3 grid(p.mtiles * p.ntiles, splits);
+  if (p.tile0 < 0 || p.tiles < 1 || p.tile0 + p.tiles > p.mtiles * p.ntiles) {
+    *why = "fp8 x fp8 GEMM: the launch's tiles must lie within the mtiles x ntiles";
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid(p.tiles, splits);
   if (nw == 4) {
     if (splits > 1)
       hipLaunchKernelGGL((f8_gemm_kernel<true, 4>), grid, dim3(256), 0, st, p);

@@ -50,6 +50,9 @@ struct F8Params {
   int64_t out_sstride;  // floats between split-K slices
   int M, N, K;
   int mtiles, ntiles;
+  // this launch's tiles: tile0 .. tile0 + tiles - 1 of the mtiles x ntiles
+  // (tile = m-tile + mtiles * n-tile), each in every split
+  int tile0, tiles;
   int k_split;  // K per split, a multiple of 128
   // A in 16 x 128 blocks: (m, k) at ((m/16)*(K/128) + k/128)*2048 + (m%16)*128
   // + k%128 (lda unused; a_bytes covers whole 16-row blocks).  A stage's 16
@@ -93,11 +96,11 @@ __global__ __launch_bounds__(NW * 64, 1) void f8_gemm_kernel(F8Params p) {
   __shared__ __attribute__((aligned(1024))) char lds[NS * kF8Stage];
 
   const int nblk = gridDim.x * gridDim.y;
-  int vb = xcd_remap(blockIdx.x + gridDim.x * blockIdx.y, nblk);
-  const int m0 = (vb % p.mtiles) * kF8BM;
-  vb /= p.mtiles;
-  const int n0 = (vb % p.ntiles) * kF8BN;
-  const int split = vb / p.ntiles;
+  const int vb = xcd_remap(blockIdx.x + gridDim.x * blockIdx.y, nblk);
+  const int tile = p.tile0 + vb % p.tiles;
+  const int split = vb / p.tiles;
+  const int m0 = (tile % p.mtiles) * kF8BM;
+  const int n0 = (tile / p.mtiles) * kF8BN;
   const int kbeg = split * p.k_split;
   const int kend = min(p.K, kbeg + p.k_split);
   const int nk = (kend - kbeg + kF8BK - 1) / kF8BK;
