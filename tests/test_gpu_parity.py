@@ -572,12 +572,15 @@ def test_fp8_factors(gpu, T, shape):
 
 # fp8 activations for h . Ud (SVDMLP_FP8_ACT): T=256 one row tile, T=300
 # ragged rows, r_d = 288 a partial 128-column tile (the large-tile path takes
-# ranks in multiples of 32), T=1024 / ff = 4096 more k-steps per split; T=16
+# ranks in multiples of 32), T=1024 / ff = 4096 more k-steps per split; T=1700
+# / r_d = 5120 more 256 x 128 tiles than CUs (7 x 40): an unsplit launch of 252
+# tiles (36 whole n-tile columns) and a 28-tile tail in 4 K splits; T=16
 # (decode) runs as without the flag
 @pytest.mark.parametrize("T,shape", [
     (256, inputs.LayerShape(1024, 2048, 512)),
     (300, inputs.LayerShape(1024, 2048, 512, 288)),
     (1024, inputs.LayerShape(2048, 4096, 640, 384)),
+    (1700, inputs.LayerShape(5120, 4096, 512, 5120)),
     (16, inputs.LayerShape(1024, 2048, 512)),
 ])
 def test_fp8_activations_down_stage(gpu, T, shape):
