@@ -238,6 +238,10 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
   gu_split_plan(T, ff, &gfn, &gsp);
   if (gsp >= 2)
     part = std::max(part, (int64_t)gsp * ((T + 255) / 256 * 256) * ((ff + 32 * gfn - 1) / (32 * gfn) * (32 * gfn)) * 4);
+  // the gate/up X.U split tail (split_tail_plan): its compact slices hold at
+  // most one round of 256 x 256 tiles, wherever both branches' tiles at the
+  // largest rank exceed a round
+  if ((T + 255) / 256 * 2 * ((r + 255) / 256) > 256) part = std::max(part, (int64_t)256 * 256 * 256 * 4);
   std::lock_guard<std::mutex> lk(mu);
   if (memo.size() > 4096) memo.clear();
   memo[key] = part;
@@ -442,6 +446,7 @@ struct Tune {
   bool hblk = true;    // the fused layer's h in 16 x 16 block-major order between the u pass and h.Ud
   bool qblk = true;    // e4m3 h (SVDMLP_FP8_ACT) in 16 x 128 blocks between the quantisation and h.Ud
   bool f8tail = true;  // fp8 x fp8 h.Ud: whole rounds of tiles without a split, K splits for the rest only
+  bool xutail = true;  // gate/up X.U with 1-2 rounds of tiles: one round without a split, the rest split
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -514,6 +519,7 @@ const Tune& tune() {
         if (k == "hblk") r.hblk = v != 0;
         if (k == "qblk") r.qblk = v != 0;
         if (k == "f8tail") r.f8tail = v != 0;
+        if (k == "xutail") r.xutail = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -568,8 +574,10 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
              int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr, const uint16_t* resid = nullptr,
-             int kg = 1, int out_blk = 0, int a_blk = 0) {
+             int kg = 1, int out_blk = 0, int a_blk = 0, int tile0 = 0, int tiles = 0) {
   BigParams p{};
+  p.tile0 = tile0;
+  p.tiles = tiles;
   p.out_blk = out_blk;
   p.a_blk = a_blk;
   p.resid = resid;
@@ -750,6 +758,40 @@ RankPlan plan_rank(int64_t T, int64_t K, int64_t N, int fn1, int batch, int64_t 
   return best;
 }
 
+// Split tail of the two-entry X.U stage (256-row tiles, fn * 32 wide): with
+// more tiles than one round of blocks and fewer than two, the first whole
+// round of tiles (whole column tiles) runs without a K split and the rest
+// in s splits, one round at most, their fp32 slices (compact, at most one
+// round of tiles) summed by the reduction.  The head tile count, or 0 when
+// the plain plan (`plain_cost`, the planner's model) is as cheap or the
+// slices do not fit `cap` bytes; *tail_ks: K per split of the tail.  The
+// model's terms are plan_ksplit's.  8B shape, 4096 tokens, ranks
+// (2816, 3072): 368 tiles, 256 unsplit and 112 in two splits, against two
+// rounds of 256 and 112 blocks.
+int split_tail_plan(int64_t T, int64_t K, int64_t N, int64_t N1, int fn, double plain_cost, int64_t cap, int* tail_ks) {
+  if (!tune().xutail) return 0;
+  const int64_t cus = tune().split, bn = 32 * fn, mt = (T + 255) / 256;
+  const int64_t tiles = mt * ((N + bn - 1) / bn + (N1 + bn - 1) / bn);
+  const int64_t head = tiles / cus * cus / mt * mt, rem = tiles - head;
+  if (head <= 0 || rem <= 0 || head > cus) return 0;
+  const double c_step = 787.0 + 65.6 * fn, c_block = 20000.0;
+  const double c_slice = 0.0009 * (double)(256 * bn) * 4.0;  // per tile and split
+  const double head_cost = (double)(K / 32) * c_step + c_block;
+  double best = plain_cost;
+  int64_t got = 0;
+  for (int64_t s = 2; s <= 8; ++s) {
+    const int64_t ks = ((K + s - 1) / s + 31) / 32 * 32, sp = (K + ks - 1) / ks;
+    if (rem * sp > cus || sp * rem * 256 * bn * 4 > cap) break;
+    const double cost = head_cost + (double)(ks / 32) * c_step + c_block + (double)(sp * rem) * c_slice;
+    if (cost < best) {
+      best = cost;
+      got = head;
+      *tail_ks = (int)ks;
+    }
+  }
+  return (int)got;
+}
+
 // Row pitch (elements) of the factors as stored, natural layout: ug and uu
 // share one, vg and vu one, then ud and vd.  Dense factors have the row
 // length as pitch.
@@ -765,6 +807,42 @@ FactorLd dense_ld(int64_t d, int64_t ff, int64_t r_gu, int64_t r_d) { return Fac
 // entries' column tiles side by side) into bf16 ws.xu_bf16: (T, r) then
 // (T, r1).  Split-K as in big_xu when the fragment-order slices fit the
 // workspace's slice area, else one split.
+// The split-tail form of big_xu2 (split_tail_plan): tiles [0, head) in one
+// launch without a split, bf16 out; tiles [head, end) in splits of tail_ks
+// into compact fp32 slices; then each entry's split column tiles summed.
+int big_xu2_tail(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u,
+                 bool u_lin, int T, int K, int r, int r1, char* ws, const Ws& L, const float* s0, const float* s1,
+                 int64_t ldb0, int64_t ldb1, int64_t b0, int64_t b1, int fn, int head, int tail_ks) {
+  uint16_t* xu = reinterpret_cast<uint16_t*>(ws + L.xu_bf16);
+  const Entry1 e1{r1, ldb1, r1, b1};
+  const int bn = 32 * fn, mt = (T + 255) / 256;
+  const int nt0 = (r + bn - 1) / bn, nt1 = (r1 + bn - 1) / bn, tiles = mt * (nt0 + nt1), rem = tiles - head;
+  int rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, K, xu, r,
+                    (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, &e1, nullptr, 1, 0, 0, 0, head);
+  if (rc) return rc;
+  float* part = reinterpret_cast<float*>(ws + L.part);
+  const int64_t tile_elems = (int64_t)256 * bn;
+  const int64_t sstride = (int64_t)rem * tile_elems;  // compact slices: the tail's tiles, per split
+  if ((rc = big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, tail_ks,
+                     part, r, 0, nullptr, true, sstride, s0, s1, 0, 1, &e1, nullptr, 1, 0, 0, head, rem)))
+    return rc;
+  const int splits = (K + tail_ks - 1) / tail_ks;
+  const int nw = big_nw(fn, BEPI_STORE, u_lin);
+  StageScope fin(ST_FINALIZE, c.st);
+  const int c0 = head / mt;  // first split column tile (both entries' tiles counted)
+  if (c0 < nt0) {             // entry 0's split column tiles
+    rc = check(launch_reduce_frag_bf16(part, splits, sstride, 0, xu + (int64_t)c0 * bn, r, 0, T, r - c0 * bn, mt,
+                                       nt0 - c0, fn, nw, 1, c.st),
+               "split-K reduce");
+    if (rc) return rc;
+  }
+  const int c1 = std::max(0, c0 - nt0);  // entry 1's first split column tile
+  const int64_t off1 = (int64_t)std::max(0, nt0 - c0) * mt * tile_elems;
+  return check(launch_reduce_frag_bf16(part + off1, splits, sstride, 0, xu + (int64_t)T * r + (int64_t)c1 * bn, r1, 0,
+                                       T, r1 - c1 * bn, mt, nt1 - c1, fn, nw, 1, c.st),
+               "split-K reduce");
+}
+
 int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_bytes, const void* const* u, bool u_lin,
             int T, int K, int r, int r1, char* ws, const Ws& L, const float* const* su, int64_t ldu, int64_t ldu1) {
   const RankPlan pl = plan_rank(T, K, r, gate_xu_fn(T, K, r, 2, r1), 2, r1, !u_lin && c.wt == SVDMLP_BF16, stage);
@@ -785,6 +863,17 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
     splits = 1;
   }
   const Entry1 e1{r1, ldb1, r1, b1};
+  {  // split tail: a whole round of tiles without a K split, the rest split
+    const int fn1 = gate_xu_fn(T, K, r, 2, r1);
+    double plain = 0.0;
+    plan_ksplit(T, K, r, fn, 2, r1, &plain, kg);
+    int tail_ks = K;
+    const int head = big_frag_reduce_ok(fn1, big_nw(fn1, BEPI_STORE, u_lin))
+                         ? split_tail_plan(T, K, r, r1, fn1, plain, (int64_t)(L.norm - L.part), &tail_ks)
+                         : 0;
+    if (head > 0) return big_xu2_tail(c, stage, a, lda, a_bytes, u, u_lin, T, K, r, r1, ws, L, s0, s1, ldb0, ldb1, b0,
+                                      b1, fn1, head, tail_ks);
+  }
   if (splits == 1)
     return big_gemm(c, stage, a, a, lda, a_bytes, u[0], u[1], ldb0, b0, u_lin, T, r, K, 2, fn, BEPI_STORE, K, xu, r,
                     (int64_t)T * r, nullptr, false, 0, s0, s1, 0, 0, &e1, nullptr, kg);
@@ -813,6 +902,14 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
   if (a_blk) a_bytes = (int64_t)((T + 15) / 16 * 16) * K * 2;  // whole 16-row blocks
   const int fn1 = stage == ST_GU_XU ? gate_xu_fn(T, K, r, batch) : down_xu_fn(T, K, r);
   const RankPlan pl = plan_rank(T, K, r, fn1, batch, -1, !u_lin && c.wt == SVDMLP_BF16, stage);
+  if (stage == ST_GU_XU && batch == 2 && !a_blk) {  // the split tail runs in the two-entry form
+    double plain = 0.0;
+    plan_ksplit(T, K, r, pl.fn, 2, -1, &plain, pl.kg);
+    int tail_ks = K;
+    if (big_frag_reduce_ok(fn1, big_nw(fn1, BEPI_STORE, u_lin)) &&
+        split_tail_plan(T, K, r, r, fn1, plain, (int64_t)(L.norm - L.part), &tail_ks) > 0)
+      return big_xu2(c, stage, a, lda, a_bytes, u, u_lin, T, K, r, r, ws, L, su, ldu, ldu);
+  }
   const int fn = pl.fn, kg = pl.kg;
   const int64_t bm = kg == 2 ? 128 : 256;
   int ks = pl.ks;

@@ -9,7 +9,7 @@ namespace {
 template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8, int NS = 4, int KG = 1>
 hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
   using C = BigCfg<FN, BK, EPI, F32, F8, NW, NS, KG>;
-  dim3 grid(p.mtiles * p.ntiles, splits, batch);
+  dim3 grid(p.tiles > 0 ? p.tiles : p.mtiles * p.ntiles, splits, batch);
   hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(C::THREADS), 0, st, p);
   return hipGetLastError();
 }
@@ -151,6 +151,10 @@ hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride,
 
 hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batch, hipStream_t st,
                       const char** why) {
+  if (p.tiles < 0 || (p.tiles > 0 && (p.tile0 < 0 || p.tile0 + p.tiles > p.mtiles * p.ntiles))) {
+    *why = "big GEMM: the launch's tiles must lie within the mtiles x ntiles";
+    return hipErrorInvalidValue;
+  }
   if (d.kg != 1 && !(d.kg == 2 && (d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE && !d.fp8 && !d.b_kc && d.nw == 8)) {
     *why = "big GEMM: K groups take natural-layout bf16 B, store epilogues and 128 x 128 or 128 x 192 tiles";
     return hipErrorInvalidValue;

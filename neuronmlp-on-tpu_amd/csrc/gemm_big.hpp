@@ -216,6 +216,10 @@ struct BigParams {
   // tiles; > 0: the grid's z is 1, entry 0 has the first nt0 of the ntiles
   // column tiles and entry 1 the rest (entries of different widths).
   int nt0;
+  // tiles > 0: this launch runs tiles tile0 .. tile0 + tiles - 1 (tile = m-tile
+  // + mtiles * column tile, both entries' column tiles counted) in every
+  // split, its fragment-order outputs compact from tile0; 0: all mtiles x ntiles
+  int tile0, tiles;
   int k_split;
 };
 
@@ -284,10 +288,20 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // B (same n) in its L2.
   const int nblk = gridDim.x * gridDim.y * gridDim.z;
   int vb = xcd_remap(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), nblk);
-  const int m0 = (vb % p.mtiles) * BM;
-  vb /= p.mtiles;
-  int nt = vb % p.ntiles;
-  vb /= p.ntiles;
+  int m0, nt;
+  int ftile = -1;  // fragment-order tile index of a tile-range launch: compact from tile0
+  if (p.tiles > 0) {
+    ftile = vb % p.tiles;
+    const int t = p.tile0 + ftile;
+    vb /= p.tiles;
+    m0 = (t % p.mtiles) * BM;
+    nt = t / p.mtiles;
+  } else {
+    m0 = (vb % p.mtiles) * BM;
+    vb /= p.mtiles;
+    nt = vb % p.ntiles;
+    vb /= p.ntiles;
+  }
   const int split = vb % gridDim.y;
   int zb = vb / gridDim.y;
   if (p.nt0 > 0 && nt >= p.nt0) {
@@ -573,8 +587,11 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // fragment are contiguous with its neighbours' (the row-major stores write
   // 16 rows x 64 bytes per instruction; 8B layer: epilogue 9.1K -> 6K cycles)
   const bool ffrag = C::OUT_F32 && p.out_frag;
-  // fragment-order element offset of this lane's block (0, 0)
-  const int64_t frag0 = ((((int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN)) * WT + wt) * FM * FN) * 256 + 4 * lane;
+  // fragment-order element offset of this lane's block (0, 0): tiles in
+  // (m-tile, column tile) order per batch entry, or, in a tile-range launch,
+  // the launch's tiles in order from its first (entries included, out_bstride 0)
+  const int64_t ftl = ftile >= 0 ? (int64_t)ftile : (int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN);
+  const int64_t frag0 = ((ftl * WT + wt) * FM * FN) * 256 + 4 * lane;
   // SwiGLU: every gate value of the wave's tile is loaded before the first
   // h store (the stores could alias the loads as far as the compiler knows,
   // which would serialise one load round trip per fragment); the main

@@ -795,6 +795,30 @@ def test_distinct_gate_up_ranks(gpu, T, ranks):
     assert _rel(got, padded) < 5e-3
 
 
+# More gate/up X.U tiles than one round of blocks (12 row tiles of 256 at
+# 3000 tokens, 22-23 column tiles of 256 over both branches): one launch of
+# whole column tiles without a K split, then the remaining tiles in K splits
+# whose compact fp32 slices are summed per branch; equal ranks take the same
+# two-entry form.  (5632, 256): the split tail holds the last gate column tile
+# and the up branch's.  Ragged last row tile.
+@pytest.mark.parametrize("ranks", [(2816, 2816, 512), (2816, 3072, 512), (3072, 2560, 384), (5632, 256, 384)])
+def test_gate_up_split_tail(gpu, ranks):
+    from svdmlp import _lib
+
+    r_g, r_u, r_d = ranks
+    T, d, ff = 3000, 1024, 2048
+    xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 1300 + r_g + r_u)
+    t = [_to(a, torch.bfloat16, gpu) for a in (xb, *fb)]
+    ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
+    with _lib.StageProfile() as prof:
+        got = _np(ops.svd_mlp(*t))
+    err = _rel(got, ref)
+    print(f"split tail T={T} ranks={ranks} rel_l2={err:.3e} launches={ {k: v[1] for k, v in prof.result.items()} }")
+    assert err < BF16_TOL
+    assert prof.result["gate_up_xu"][1] == 2   # the unsplit head and the split tail
+    assert np.array_equal(got, _np(ops.svd_mlp(*t)))  # replays are bitwise identical
+
+
 def test_distinct_gate_up_ranks_fp8(gpu):
     T, d, ff, r_g, r_u, r_d = 300, 1024, 2048, 512, 256, 384
     xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 950)
