@@ -236,8 +236,9 @@ int64_t part_bytes(int64_t T, int64_t d, int64_t ff, int64_t r) {
   // split gate/up XU.V passes at one or two row tiles (big_swiglu)
   int gfn = 0, gsp = 0;
   gu_split_plan(T, ff, &gfn, &gsp);
+  // (both passes' slices, side by side)
   if (gsp >= 2)
-    part = std::max(part, (int64_t)gsp * ((T + 255) / 256 * 256) * ((ff + 32 * gfn - 1) / (32 * gfn) * (32 * gfn)) * 4);
+    part = std::max(part, (int64_t)2 * gsp * ((T + 255) / 256 * 256) * ((ff + 32 * gfn - 1) / (32 * gfn) * (32 * gfn)) * 4);
   // the gate/up X.U split tail (split_tail_plan): its compact slices hold at
   // most one round of 256 x 256 tiles, wherever both branches' tiles at the
   // largest rank exceed a round
@@ -447,6 +448,7 @@ struct Tune {
   bool qblk = true;    // e4m3 h (SVDMLP_FP8_ACT) in 16 x 128 blocks between the quantisation and h.Ud
   bool f8tail = true;  // fp8 x fp8 h.Ud: whole rounds of tiles without a split, K splits for the rest only
   bool xutail = true;  // gate/up X.U with 1-2 rounds of tiles: one round without a split, the rest split
+  bool gufuse = true;  // split gate/up XU.V passes: one reduction from both passes' slices
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -520,6 +522,7 @@ const Tune& tune() {
         if (k == "qblk") r.qblk = v != 0;
         if (k == "f8tail") r.f8tail = v != 0;
         if (k == "xutail") r.xutail = v != 0;
+        if (k == "gufuse") r.gufuse = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -984,21 +987,28 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
     fn = sfn;
     const int ks = (r / nsp + 31) / 32 * 32, splits = (r + ks - 1) / ks;
     const int ks_u = (r_u / nsp + 31) / 32 * 32, splits_u = (r_u + ks_u - 1) / ks_u;
+    // Both passes' slices side by side when the area holds them: one
+    // reduction then rounds g from its slices and applies SiLU(g) to the u
+    // sum (bitwise the two-reduction result, one launch and the bf16 g round
+    // trip fewer); else g is reduced to bf16 before the u pass reuses the area.
+    const bool fused = tune().gufuse && (int64_t)(splits + splits_u) * per * 4 <= part_cap;
+    float* upart = fused ? part + (int64_t)splits * per : part;
     int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
                       BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
     if (rc) return rc;
-    {
+    if (!fused) {
       StageScope fin(ST_FINALIZE, c.st);
       if ((rc = check(launch_reduce_bf16(part, splits, per, gbuf, per, c.st), "split-K reduce"))) return rc;
     }
     rc = big_gemm(c, ST_GU_XUV, xu_u, nullptr, r_u, xuu_bytes, vu, nullptr, ldb_u, vu_bytes, v_lin, T, ff, r_u, 1, fn,
-                  BEPI_STORE, ks_u, part, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
+                  BEPI_STORE, ks_u, upart, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
     if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
     const int mt = (T + 255) / 256;
-    return check(launch_reduce_frag_bf16(part, splits_u, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff, T,
-                                         ff, mt, (int)(per / (256 * mt) / (32 * fn)), fn, big_nw(fn, BEPI_STORE, v_lin), 1,
-                                         c.st, gbuf),
+    return check(launch_reduce_frag_bf16(upart, splits_u, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff,
+                                         T, ff, mt, (int)(per / (256 * mt) / (32 * fn)), fn,
+                                         big_nw(fn, BEPI_STORE, v_lin), 1, c.st, fused ? nullptr : gbuf, nullptr, 1,
+                                         fused ? part : nullptr, fused ? splits : 0),
                  "split-K SwiGLU reduce");
   }
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,

@@ -90,12 +90,16 @@ hipError_t launch_reduce_bf16(const float* in, int slices, int64_t stride, uint1
 // tiles of 256 x 32*fn with nw waves (kg 1) or 128 x 32*fn with K groups
 // (kg 2, nw 8: four wave tiles), batch entries zb (out batch stride
 // obstride elements); with `gate` (bf16 in the same fragment order),
-// out = bf16(SiLU(gate) * sum); with `resid` (bf16, row pitch ldo, batch
-// entry 0), out = bf16(resid + bf16(sum)), the MLP block's residual add.
+// out = bf16(SiLU(gate) * sum); with `gsl` (gsplits fp32 slices of the gate
+// in the same layout and slice stride), the gate is bf16(sum of its slices
+// in order) first, as launch_reduce_bf16 would round it; with `resid` (bf16,
+// row pitch ldo, batch entry 0), out = bf16(resid + bf16(sum)), the MLP
+// block's residual add.
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
                                    int batch, hipStream_t st, const uint16_t* gate = nullptr,
-                                   const uint16_t* resid = nullptr, int kg = 1);
+                                   const uint16_t* resid = nullptr, int kg = 1, const float* gsl = nullptr,
+                                   int gsplits = 0);
 // fp8 x fp8 GEMM (gemm_f8f8.hpp), nw = 8 or 4 waves: splits > 1 writes fp32
 // fragment-order slices (256 x 128 tiles) for launch_reduce_frag_bf16 (fn 4, nw).
 struct F8Params;

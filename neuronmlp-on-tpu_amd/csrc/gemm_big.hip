@@ -63,7 +63,8 @@ template <int FM, int FN>
 __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, int splits, int64_t sstride,
                                                                int64_t bstride, uint16_t* out, int64_t ldo,
                                                                int64_t obstride, int M, int N, int mtiles, int nw,
-                                                               const uint16_t* gate, const uint16_t* resid) {
+                                                               const uint16_t* gate, const uint16_t* resid,
+                                                               const float* gsl, int gsplits) {
   // tiles of (nw / 2) x 2 wave tiles: 256 rows (8 waves of 64, 4 of 128) or
   // 128 (the K-group tiles' four wave tiles of 64)
   constexpr int ROWS = 16 * FM, COLS = 16 * FN, PITCH = COLS + 8;  // staged row pitch (elements)
@@ -86,7 +87,19 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
 #pragma unroll
     for (int k = 0; k < PER; ++k) a[k] += b[k];
   }
-  if (gate) {  // SwiGLU: out = SiLU(g) * sum, g bf16 in the same fragment order
+  if (gsl) {  // SwiGLU with the gate as fp32 slices: g = bf16(sum in split order), then out = SiLU(g) * sum
+    const float* gp = gsl + (int64_t)zb * bstride + (int64_t)unit * Q * 4 + 4 * threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      f32x4 g = *reinterpret_cast<const f32x4*>(gp + 1024 * k);
+      for (int s = 1; s < gsplits; ++s) g += *reinterpret_cast<const f32x4*>(gp + s * sstride + 1024 * k);
+      const uint32_t g01 = pack_bf16x2(g.x, g.y), g23 = pack_bf16x2(g.z, g.w);
+      a[k].x *= silu_f32(bf16_bits_to_f32(g01 & 0xffffu));
+      a[k].y *= silu_f32(bf16_bits_to_f32(g01 >> 16));
+      a[k].z *= silu_f32(bf16_bits_to_f32(g23 & 0xffffu));
+      a[k].w *= silu_f32(bf16_bits_to_f32(g23 >> 16));
+    }
+  } else if (gate) {  // SwiGLU: out = SiLU(g) * sum, g bf16 in the same fragment order
     const uint16_t* gp = gate + (int64_t)zb * bstride + (int64_t)unit * Q * 4 + 4 * threadIdx.x;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
@@ -122,9 +135,9 @@ __global__ __launch_bounds__(256) void reduce_frag_bf16_kernel(const float* in, 
 template <int FM, int FN>
 hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out, int64_t ldo,
                      int64_t obstride, int M, int N, int mtiles, int ntiles, int nw, int batch, const uint16_t* gate,
-                     const uint16_t* resid, hipStream_t st) {
+                     const uint16_t* resid, hipStream_t st, const float* gsl, int gsplits) {
   hipLaunchKernelGGL((reduce_frag_bf16_kernel<FM, FN>), dim3(mtiles * ntiles * nw, batch), dim3(256), 0, st, in,
-                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw, gate, resid);
+                     splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, nw, gate, resid, gsl, gsplits);
   return hipGetLastError();
 }
 
@@ -132,20 +145,21 @@ hipError_t go_reduce(const float* in, int splits, int64_t sstride, int64_t bstri
 
 hipError_t launch_reduce_frag_bf16(const float* in, int splits, int64_t sstride, int64_t bstride, uint16_t* out,
                                    int64_t ldo, int64_t obstride, int M, int N, int mtiles, int ntiles, int fn, int nw,
-                                   int batch, hipStream_t st, const uint16_t* gate, const uint16_t* resid, int kg) {
+                                   int batch, hipStream_t st, const uint16_t* gate, const uint16_t* resid, int kg,
+                                   const float* gsl, int gsplits) {
   if (kg == 2) {  // 128-row K-group tiles: four 64-row wave tiles per tile
     if (nw != 8) return hipErrorInvalidValue;
-    if (fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, 4, batch, gate, resid, st);
-    if (fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, 4, batch, gate, resid, st);
+    if (fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, 4, batch, gate, resid, st, gsl, gsplits);
+    if (fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, 4, batch, gate, resid, st, gsl, gsplits);
     return hipErrorInvalidValue;
   }
   if (kg != 1) return hipErrorInvalidValue;
-  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
-  if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
-  if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
-  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
-  if (nw == 4 && fn == 4) return go_reduce<8, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
-  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st);
+  if (nw == 8 && fn == 8) return go_reduce<4, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st, gsl, gsplits);
+  if (nw == 8 && fn == 7) return go_reduce<4, 7>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st, gsl, gsplits);
+  if (nw == 8 && fn == 6) return go_reduce<4, 6>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st, gsl, gsplits);
+  if (nw == 8 && fn == 4) return go_reduce<4, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st, gsl, gsplits);
+  if (nw == 4 && fn == 4) return go_reduce<8, 4>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st, gsl, gsplits);
+  if (nw == 4 && fn == 8) return go_reduce<8, 8>(in, splits, sstride, bstride, out, ldo, obstride, M, N, mtiles, ntiles, nw, batch, gate, resid, st, gsl, gsplits);
   return hipErrorInvalidValue;
 }
 
