@@ -461,9 +461,9 @@ struct Tune {
   int kg = 1;          // K-group 128-row tiles for the rank stages: 0 never, 1 where the planner rates them cheaper, 2 always
   int kgw = 125;       // planner: cycles of a K-group 64-k step, percent of a 256-row tile's 32-k step
   int kgs = 7;         // stages that may take K-group tiles: 1 gate/up X.U, 2 h.Ud, 4 XU_d.Vd
-  // decode layer: most K splits of phases 1, 3, 4 (0: grid / tiles; dls4 -1:
-  // 4 at four token tiles, else grid / tiles)
-  int dls1 = 0, dls3 = 0, dls4 = -1;
+  // decode layer: most K splits of phases 1, 3, 4 (0: grid / tiles; -1: the
+  // defaults, dls3 8 at two token tiles, dls4 4 at four, else grid / tiles)
+  int dls1 = 0, dls3 = -1, dls4 = -1;
 };
 
 const Tune& tune();
@@ -1323,7 +1323,12 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   const bool p2_pays = mt >= 2 || ld.dense;
   p.p2split = !contract && p2split_fits(d, ff, r_gu, r_d, grid, r_u) &&
               (two || tune().p2split >= 2 || (tune().p2split == 1 && p2_pays));
-  p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3, tune().dls3);
+  // Phase 3 at two token tiles (17-32 tokens) in at most 8 K splits (176
+  // units instead of 242 at the 8B shape): T=32 75.4-75.5 -> 74.8-74.9 us
+  // padded, 79.7-79.8 -> 79.4-79.5 dense, T=17-24 0-0.6 us less; at four
+  // tiles 8 splits cost 0.8 us.
+  const int cap3 = tune().dls3 >= 0 ? tune().dls3 : (mt == 2 ? 8 : 0);
+  p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3, cap3);
   // Phase 4 at four token tiles (33-64 tokens) in at most 4 K splits: each
   // tile's last split then sums 4 slices of 64 rows instead of 8, for a
   // stream that is HBM-bound either way (8B layer, T=64: 90.5 -> 89.2 us;
