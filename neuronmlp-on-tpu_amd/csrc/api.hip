@@ -761,6 +761,12 @@ RankPlan plan_rank(int64_t T, int64_t K, int64_t N, int fn1, int batch, int64_t 
   return best;
 }
 
+// The split tail runs on the tile-range instance of the large-tile kernel:
+// 256 x 256 tiles of natural-layout bf16 B with 8 waves.
+bool xu_tail_ok(const Common& c, int fn, bool u_lin) {
+  return fn == 8 && c.wt == SVDMLP_BF16 && !u_lin && big_nw(fn, BEPI_STORE, u_lin) == 8;
+}
+
 // Split tail of the two-entry X.U stage (256-row tiles, fn * 32 wide): with
 // more tiles than one round of blocks and fewer than two, the first whole
 // round of tiles (whole column tiles) runs without a K split and the rest
@@ -871,7 +877,7 @@ int big_xu2(const Common& c, int stage, const void* a, int64_t lda, int64_t a_by
     double plain = 0.0;
     plan_ksplit(T, K, r, fn, 2, r1, &plain, kg);
     int tail_ks = K;
-    const int head = big_frag_reduce_ok(fn1, big_nw(fn1, BEPI_STORE, u_lin))
+    const int head = xu_tail_ok(c, fn1, u_lin)
                          ? split_tail_plan(T, K, r, r1, fn1, plain, (int64_t)(L.norm - L.part), &tail_ks)
                          : 0;
     if (head > 0) return big_xu2_tail(c, stage, a, lda, a_bytes, u, u_lin, T, K, r, r1, ws, L, s0, s1, ldb0, ldb1, b0,
@@ -909,8 +915,7 @@ int big_xu(const Common& c, int stage, const void* a, int64_t lda, int64_t a_byt
     double plain = 0.0;
     plan_ksplit(T, K, r, pl.fn, 2, -1, &plain, pl.kg);
     int tail_ks = K;
-    if (big_frag_reduce_ok(fn1, big_nw(fn1, BEPI_STORE, u_lin)) &&
-        split_tail_plan(T, K, r, r, fn1, plain, (int64_t)(L.norm - L.part), &tail_ks) > 0)
+    if (xu_tail_ok(c, fn1, u_lin) && split_tail_plan(T, K, r, r, fn1, plain, (int64_t)(L.norm - L.part), &tail_ks) > 0)
       return big_xu2(c, stage, a, lda, a_bytes, u, u_lin, T, K, r, r, ws, L, su, ldu, ldu);
   }
   const int fn = pl.fn, kg = pl.kg;

@@ -6,9 +6,9 @@ namespace svdmlp {
 
 namespace {
 
-template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8, int NS = 4, int KG = 1>
+template <int FN, bool BK, int EPI, bool F32 = false, bool F8 = false, int NW = 8, int NS = 4, int KG = 1, bool TR = false>
 hipError_t go(const BigParams& p, int splits, int batch, hipStream_t st) {
-  using C = BigCfg<FN, BK, EPI, F32, F8, NW, NS, KG>;
+  using C = BigCfg<FN, BK, EPI, F32, F8, NW, NS, KG, TR>;
   dim3 grid(p.tiles > 0 ? p.tiles : p.mtiles * p.ntiles, splits, batch);
   hipLaunchKernelGGL(big_gemm_kernel<C>, grid, dim3(C::THREADS), 0, st, p);
   return hipGetLastError();
@@ -25,7 +25,10 @@ hipError_t go_b(const BigDesc& d, const BigParams& p, int splits, int batch, hip
   if constexpr ((FN == 4 || FN == 6) && EPI == BEPI_STORE) {
     if (d.kg == 2) return go<FN, false, EPI, F32, false, 8, FN == 4 ? 5 : 4, 2>(p, splits, batch, st);
   }
-  if constexpr (FN == 8 && EPI == BEPI_STORE) {  // 4-wave instances: natural layout, STORE
+  if constexpr (FN == 8 && EPI == BEPI_STORE) {
+    // tile ranges (the X.U split tail): 256 x 256, natural-layout bf16 B, 8 waves
+    if (p.tiles > 0) return go<FN, false, EPI, F32, false, 8, 4, 1, true>(p, splits, batch, st);
+    // 4-wave instances: natural layout, STORE
     if (d.nw == 4 && !d.b_kc)
       return d.fp8 ? go<FN, false, EPI, F32, true, 4>(p, splits, batch, st)
                    : go<FN, false, EPI, F32, false, 4>(p, splits, batch, st);
@@ -167,6 +170,10 @@ hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batc
                       const char** why) {
   if (p.tiles < 0 || (p.tiles > 0 && (p.tile0 < 0 || p.tile0 + p.tiles > p.mtiles * p.ntiles))) {
     *why = "big GEMM: the launch's tiles must lie within the mtiles x ntiles";
+    return hipErrorInvalidValue;
+  }
+  if (p.tiles > 0 && !(d.fn == 8 && d.epi == BEPI_STORE && !d.fp8 && !d.b_kc && d.nw == 8 && d.kg == 1)) {
+    *why = "big GEMM: tile ranges take 256 x 256 tiles of natural-layout bf16 B with 8 waves and a store epilogue";
     return hipErrorInvalidValue;
   }
   if (d.kg != 1 && !(d.kg == 2 && (d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE && !d.fp8 && !d.b_kc && d.nw == 8)) {

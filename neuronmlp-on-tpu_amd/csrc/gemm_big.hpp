@@ -223,7 +223,8 @@ struct BigParams {
   int k_split;
 };
 
-template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8, int NS_ = 4, int KG_ = 1>
+template <int FN_, bool B_KC_, int EPI_, bool OUT_F32_, bool FP8_B_ = false, int NW_ = 8, int NS_ = 4, int KG_ = 1,
+          bool TR_ = false>
 struct BigCfg {
   // NW waves per block.  KG = 1: a 2 (n) x NW/2 (m) arrangement over a
   // 256-row tile: a wave's tile is (BM / (NW/2)) x 16*FN, i.e. 64 x 16*FN
@@ -237,6 +238,10 @@ struct BigCfg {
   // stages need fewer K splits (or none).
   static constexpr int NW = NW_;
   static constexpr int KG = KG_;
+  // TR: the launch may run a tile range (BigParams::tiles).  A separate
+  // instance: its block-to-tile arithmetic, compiled into every instance,
+  // cost the fp8-B ones ~20 VGPRs and the 256 x 256 fp8-B ones a spill.
+  static constexpr bool TR = TR_;
   static constexpr int WT = NW / KG;                 // wave tiles per block
   static constexpr int THREADS = 64 * NW;
   static constexpr int BM = KG == 2 ? 128 : 256;
@@ -288,12 +293,11 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // B (same n) in its L2.
   const int nblk = gridDim.x * gridDim.y * gridDim.z;
   int vb = xcd_remap(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), nblk);
-  int m0, nt;
-  int ftile = -1;  // fragment-order tile index of a tile-range launch: compact from tile0
-  if (p.tiles > 0) {
-    ftile = vb % p.tiles;
-    const int t = p.tile0 + ftile;
-    vb /= p.tiles;
+  int m0, nt, t = 0;
+  if constexpr (C::TR) {  // tile t = m-tile + mtiles * column tile, from tile0 (tiles 0: all of them)
+    const int ntl = p.tiles > 0 ? p.tiles : p.mtiles * p.ntiles;
+    t = p.tile0 + vb % ntl;
+    vb /= ntl;
     m0 = (t % p.mtiles) * BM;
     nt = t / p.mtiles;
   } else {
@@ -590,7 +594,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // fragment-order element offset of this lane's block (0, 0): tiles in
   // (m-tile, column tile) order per batch entry, or, in a tile-range launch,
   // the launch's tiles in order from its first (entries included, out_bstride 0)
-  const int64_t ftl = ftile >= 0 ? (int64_t)ftile : (int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN);
+  const int64_t ftl = C::TR && p.tiles > 0 ? (int64_t)(t - p.tile0) : (int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN);
   const int64_t frag0 = ((ftl * WT + wt) * FM * FN) * 256 + 4 * lane;
   // SwiGLU: every gate value of the wave's tile is loaded before the first
   // h store (the stores could alias the loads as far as the compiler knows,
