@@ -12,7 +12,9 @@ streams and device pointers are shared with PyTorch.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -24,6 +26,8 @@ CSRC = ROOT / "csrc"
 INCLUDE = ROOT.parent / "include"
 BUILD_DIR = ROOT / "_build"
 LIB_PATH = PKG_DIR / "libsvdmlp.so"
+# per-kernel registers, scratch and occupancy of the last build (the compiler's report)
+RESOURCES = BUILD_DIR / "resources.json"
 # the benchmark's streaming-read probe (csrc/probe/), its own library outside the SVD-MLP C ABI
 PROBE_SRC = CSRC / "probe" / "hbm_read.hip"
 PROBE_LIB = PKG_DIR / "libhbmread.so"
@@ -54,14 +58,39 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found; the SVD-MLP HIP library cannot be built")
 
 
-def _run(cmd: list[str]) -> None:
+# The compiler's per-kernel resource report (registers, scratch, occupancy):
+# collected into RESOURCES by build() and kept out of the build log.
+REMARK_FLAG = "-Rpass-analysis=kernel-resource-usage"
+_REMARK = re.compile(r"remark: (?:Function Name: (\S+)|\s+([^:]+): (\S+)) \[" + re.escape(REMARK_FLAG) + r"\]")
+
+
+def _run(cmd: list[str]) -> str:
+    """Run a build command; returns its output with the resource remarks, prints the rest."""
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    text = "\n".join(l for l in proc.stdout.splitlines() if noise not in l)
+    lines = [l for l in proc.stdout.splitlines() if noise not in l]
+    # (a remark on a kernel defined in a header comes with its include chain)
+    text = "\n".join(l for l in lines if REMARK_FLAG not in l and not l.startswith("In file included from"))
     if proc.returncode != 0:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{text}")
     if text.strip():
         print(text, file=sys.stderr)
+    return "\n".join(lines)
+
+
+def resources(text: str) -> dict[str, dict[str, str]]:
+    """Kernel (mangled name) -> the resource report's fields, from build output."""
+    out: dict[str, dict[str, str]] = {}
+    cur = None
+    for line in text.splitlines():
+        m = _REMARK.search(line)
+        if not m:
+            continue
+        if m.group(1):
+            cur = out.setdefault(m.group(1), {})
+        elif cur is not None:
+            cur[m.group(2).strip()] = m.group(3)
+    return out
 
 
 def sources() -> list[Path]:
@@ -80,14 +109,16 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
 
     def compile_one(pair):
         src, obj = pair
-        cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, REMARK_FLAG, "-fno-caret-diagnostics", "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), file=sys.stderr)
-        _run(cmd)
-        return obj
+        return resources(_run(cmd))
 
+    report: dict[str, dict[str, str]] = {}
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        list(pool.map(compile_one, zip(srcs, objs)))
+        for r in pool.map(compile_one, zip(srcs, objs)):
+            report.update(r)
+    RESOURCES.write_text(json.dumps(report, indent=1, sort_keys=True))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB_PATH)
