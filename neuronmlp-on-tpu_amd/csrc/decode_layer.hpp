@@ -97,6 +97,10 @@ struct DecLayerParams {
   // counter after phases 1, 3 and 4's.  Otherwise a unit computes both over
   // 64 columns.
   int p2split;
+  // Token tiles of 32 rows and more: split-K tiles combined by all their
+  // splits (dl_combine_dist), the phase-2 pairs' h written half by each
+  // unit (dl_swiglu_pair_dist).
+  int dist;
   // MLP block (null otherwise): y = bf16(resid + bf16(MLP)); with `gain`
   // (NORM instances) a phase 0 writes RMSNorm(x) to xn, which phase 1 reads
   // instead of x.
@@ -480,6 +484,97 @@ __device__ __forceinline__ void dl_swiglu_pair(const DlCtx& c, const DlUnit& U, 
   }
 }
 
+// Bounded wait of thread 0 until the tile counter `cnt` reads zero (the
+// last split's reset: see dl_combine_dist); a wait that gives up sets the
+// timeout flags as a grid-barrier wait does.
+__device__ __forceinline__ void dl_wait_reset(uint32_t* cnt, uint64_t* sync, uint32_t spin, int* bad) {
+  uint32_t polls = 0;
+  while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++polls >= spin) {
+      __hip_atomic_fetch_or(&sync[kDlFlag], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_or(&sync[kGvDone], kGvDoneBad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      dl_wait_vm<0>();
+      *bad = 1;
+      break;
+    }
+  }
+}
+
+// Arrival on a counter that `n` units share per launch: one atomic
+// increment that wraps to zero at the n-th arrival (global_atomic_inc with
+// limit n - 1), so the last arrival leaves the counter at zero for the next
+// use with no store of its own.  Returns whether this was the last arrival.
+__device__ __forceinline__ bool dl_arrive_wrap(uint32_t* cnt, int n) {
+  return __builtin_amdgcn_atomic_inc32(cnt, (uint32_t)n - 1u, __ATOMIC_RELAXED, "agent") == (uint32_t)n - 1u;
+}
+
+// dl_swiglu_pair with the pair's work halved (token tiles of 32 rows and
+// more): the g unit writes h for the first MT/2 16-row blocks, the u unit for
+// the rest.  Each unit stores the half of its tile that its partner writes
+// (slice u, the same offsets), arrives on the pair's counter (the second
+// arrival wraps it to zero, which releases the first, dl_wait_reset), loads
+// its partner's half of its own rows and writes them: the same fp32
+// operands, so the same bits.  (The first to arrive issuing the next
+// phase's first weight DMAs before it waits, as dl_combine_dist does, cost
+// 0.3-0.5 us at 32-128 tokens.)  8B layer, against dl_swiglu_pair, with
+// dl_combine_dist for the split phases: T=64 86.9 -> 86.3 us, T=128 121.1
+// -> 120.2 us.
+template <int MT>
+__device__ __forceinline__ void dl_swiglu_pair_dist(const DlCtx& c, const DlUnit& U, const f32x4 (&acc)[MT], int u,
+                                                    uint32_t* cnt, float* slices, int* flag, uint16_t* h,
+                                                    uint64_t* sync, uint32_t spin, int* bad) {
+  static_assert(MT >= 2 && MT % 2 == 0, "whole 16-row blocks per half");
+  constexpr int HALF = MT / 2;
+  const int own = u & 1;  // this unit writes blocks own * HALF ..
+  const int n = U.n0 + 64 * (c.wave >> 2) + 16 * (c.wave & 3) + 4 * c.lg;
+  const __amdgpu_buffer_rsrc_t rs = dl_slice_rsrc<MT>(slices);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    if ((mt >= HALF) == (own != 0)) continue;  // the partner's blocks only
+    const uint32_t off = 16 * mt + c.lr < c.T ? (uint32_t)(((u * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y),
+                                                 __float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)},
+                                           rs, off, 0, kDlSc1);
+  }
+  dl_wait_vm<0>();
+  dl_block_sync();
+  if (threadIdx.x == 0) *flag = dl_arrive_wrap(cnt, 2);
+  dl_block_sync();
+  if (!*flag) {
+    if (threadIdx.x == 0) dl_wait_reset(cnt, sync, spin, bad);
+    dl_block_sync();
+  }
+  // this unit's blocks own * HALF .. own * HALF + HALF - 1, with compile-time
+  // indices into acc (a runtime index would put acc in scratch memory)
+  auto finish = [&](auto base) {
+    constexpr int B0 = decltype(base)::value;
+    u32x4 v[HALF];
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+      const int mt = B0 + i;
+      const uint32_t off =
+          16 * mt + c.lr < c.T ? (uint32_t)((((u ^ 1) * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+      v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kDlSc1);
+    }
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+      const int m = 16 * (B0 + i) + c.lr;
+      if (m < c.T) {
+        const f32x4 o = f32x4{__uint_as_float(v[i].x), __uint_as_float(v[i].y), __uint_as_float(v[i].z),
+                              __uint_as_float(v[i].w)};
+        const f32x4 g = B0 ? o : acc[B0 + i], uv = B0 ? acc[B0 + i] : o;
+        dl_store8(h + (int64_t)m * U.ldo + n, u32x2{dl_pack_bf16x2(silu_f32(g.x) * uv.x, silu_f32(g.y) * uv.y),
+                                                    dl_pack_bf16x2(silu_f32(g.z) * uv.z, silu_f32(g.w) * uv.w)});
+      }
+    }
+  };
+  if (own)
+    finish(std::integral_constant<int, HALF>{});
+  else
+    finish(std::integral_constant<int, 0>{});
+}
+
 // Split-K combination of unit u = tile + split * nt (splits per tile) into
 // the bf16 tile at `dst` (row pitch U.ldo, columns from U.n0).  Lane layout
 // of acc: D[n = 4*lg + t][m = lr] of each 16-row block mt.
@@ -578,6 +673,92 @@ __device__ __forceinline__ void dl_combine(const DlCtx& c, const DlUnit& U, f32x
       dl_store8(dst + (int64_t)m * U.ldo + n, poison ? u32x2{kNaN2, kNaN2} : v);
     }
   }
+}
+
+// Split-K combination shared by all splits of the tile (token tiles of 32
+// rows and more, whose slices are 16 KB and larger: one block summing every
+// split took 3-5 us per phase at 64 rows).  Every unit stores its slice and
+// counts its arrival on the tile's counter, as in dl_combine; the last
+// arrival wraps the counter to zero, and that zero releases the tile's
+// other splits, which poll for it (the counter receives no other arrival in
+// the launch, so it stays zero).  Split s then sums share s of the tile's
+// float4 elements (16 * MT rows x 128 columns, in slice order) over every
+// split in split order, 0 + s_0 + s_1 + ..., the same additions as one block
+// summing the whole tile, so the result is bitwise that of dl_combine, and
+// rounds them to dst.  `pre()` is run by every split but the last before it
+// polls: it may issue the next phase's first weight DMAs, so the weight
+// stream goes on while the split waits, and returns whether it did, which
+// this function returns (the grid barrier then issues none).  y (`out_y`) is poisoned as in
+// dl_combine: this block's own give-ups (`bad`, read after the wait) and the
+// timeout flag read after the release.
+template <int MT, class Pre>
+__device__ __forceinline__ bool dl_combine_dist(const DlCtx& c, const DlUnit& U, const f32x4 (&acc)[MT], int u,
+                                                int nt, int splits, uint32_t* cnt, float* slices, int* flag,
+                                                uint16_t* dst, bool out_y, int* bad, uint64_t* sync, uint32_t spin,
+                                                const uint16_t* resid, const Pre& pre) {
+  const __amdgpu_buffer_rsrc_t rs = dl_slice_rsrc<MT>(slices);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint32_t off = 16 * mt + c.lr < c.T ? (uint32_t)(((u * MT + mt) * 2048 + 4 * threadIdx.x) * 4) : kDlPastSlices;
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{__float_as_uint(acc[mt].x), __float_as_uint(acc[mt].y),
+                                                 __float_as_uint(acc[mt].z), __float_as_uint(acc[mt].w)},
+                                           rs, off, 0, kDlSc1);
+  }
+  dl_wait_vm<0>();
+  dl_block_sync();
+  if (threadIdx.x == 0) *flag = dl_arrive_wrap(cnt, splits);
+  dl_block_sync();
+  bool issued = false;
+  if (!*flag) {
+    issued = pre();
+    if (threadIdx.x == 0) dl_wait_reset(cnt, sync, spin, bad);
+    dl_block_sync();
+  }
+  const bool poison = out_y && (*bad != 0 || __hip_atomic_load(&sync[kDlFlag], __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT) != 0);
+  const int tile = u % nt, s = u / nt;
+  constexpr int TOTAL = MT * 512;  // float4 elements of a tile
+  const int share = (TOTAL + splits - 1) / splits;
+  const int e1 = min(TOTAL, (s + 1) * share);
+  constexpr int SB = 8;  // slices in flight per element
+  for (int e = s * share + (int)threadIdx.x; e < e1; e += kDlThreads) {
+    const int mt = e >> 9, t = e & 511;  // element e: the lane t of block mt in every slice
+    const int m = 16 * mt + (t & 15);
+    if (m >= c.T) continue;
+    f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < splits; s0 += SB) {
+      u32x4 v[SB];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const uint32_t off =
+            s0 + i < splits ? (uint32_t)((((tile + (s0 + i) * nt) * MT + mt) * 2048 + 4 * t) * 4) : kDlPastSlices;
+        v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kDlSc1);
+      }
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        if (s0 + i < splits) {
+          sum.x += __uint_as_float(v[i].x);
+          sum.y += __uint_as_float(v[i].y);
+          sum.z += __uint_as_float(v[i].z);
+          sum.w += __uint_as_float(v[i].w);
+        }
+      }
+    }
+    // column of lane t: wave t / 64, lane group (t % 64) / 16
+    const int w = t >> 6;
+    const int n = U.n0 + 64 * (w >> 2) + 16 * (w & 3) + 4 * ((t & 63) >> 4);
+    u32x2 v = u32x2{dl_pack_bf16x2(sum.x, sum.y), dl_pack_bf16x2(sum.z, sum.w)};
+    if (resid && !poison) {
+      const u32x2 xr = *reinterpret_cast<const u32x2*>(resid + (int64_t)m * U.ldo + n);
+      v = u32x2{dl_pack_bf16x2(__uint_as_float(xr.x << 16) + __uint_as_float(v.x << 16),
+                               __uint_as_float(xr.x & 0xffff0000u) + __uint_as_float(v.x & 0xffff0000u)),
+                dl_pack_bf16x2(__uint_as_float(xr.y << 16) + __uint_as_float(v.y << 16),
+                               __uint_as_float(xr.y & 0xffff0000u) + __uint_as_float(v.y & 0xffff0000u))};
+    }
+    constexpr uint32_t kNaN2 = 0x7fc07fc0u;
+    dl_store8(dst + (int64_t)m * U.ldo + n, poison ? u32x2{kNaN2, kNaN2} : v);
+  }
+  return issued;
 }
 
 // Phase 0 of the MLP block: row `row` of x normalised into xn,
@@ -977,8 +1158,30 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       }
     }
   };
-  auto grid_sync = [&](int next_phase) {
-    dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] { prefetch_w(next_phase); });
+  // pre_done: the block already issued those DMAs (dl_combine_dist)
+  auto grid_sync = [&](int next_phase, bool pre_done = false) {
+    dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] {
+      if (!pre_done) prefetch_w(next_phase);
+    });
+  };
+  // Split-K combination of unit u of a split phase: by all the tile's
+  // splits (dl_combine_dist) or by its last one (dl_combine); `next` is the
+  // phase whose first weight stages a waiting split issues (0: none).
+  auto combine = [&](const DlUnit& U, f32x4(&acc)[MT], int u, int nt, int splits, int cnt_base, bool out_y,
+                     int next) -> bool {
+    uint32_t* cnt = dl_tile_counter(p.sync, cnt_base + u % nt);
+    const uint16_t* resid = out_y ? static_cast<const uint16_t*>(p.resid) : nullptr;
+    if constexpr (MT >= 2) {
+      if (p.dist && splits > 1)
+        return dl_combine_dist<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, bad, p.sync,
+                                   spin_lds ? *spin_lds : spin, resid, [&] {
+                                     if (next == 0 || u + G < units[next - 1]) return false;
+                                     prefetch_w(next);
+                                     return true;
+                                   });
+    }
+    dl_combine<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, out_y && *bad != 0, p.sync, resid);
+    return false;
   };
 
   const int nt1 = p.r_gu / 128 + p.r_up / 128, nt3 = p.r_d / 128, nt4 = p.d / 128;
@@ -992,16 +1195,16 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
 
   // ---- phase 1: XU_g, XU_u = X . [Ug | Uu] -> bf16 XU ----
+  bool pre2 = false;
   for (int u = b; u < units[1]; u += G) {
     DlUnit U;
     unit_of(1, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, NORM && u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt1, p.splits1, dl_tile_counter(p.sync, u % nt1), p.slices, flag, U.dst, false,
-                   false, p.sync);
+    pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2);
   }
   dl_wait_vm<0>();
-  grid_sync(2);
+  grid_sync(2, pre2);
 
   if constexpr (CONTRACT) {
     // ---- phases 2 and 3 contracted: unit b < units2 keeps its h strip in
@@ -1033,7 +1236,14 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       unit_of(2, u, U);
       f32x4 acc[MT];
       dl_run<MT, false>(c, U, u == b, acc);
-      dl_swiglu_pair<MT>(c, U, acc, u, dl_tile_counter(p.sync, nt1 + nt3 + nt4 + (u >> 1)), p.slices, flag, p.h);
+      uint32_t* pcnt = dl_tile_counter(p.sync, nt1 + nt3 + nt4 + (u >> 1));
+      if constexpr (MT >= 2) {
+        if (p.dist) {
+          dl_swiglu_pair_dist<MT>(c, U, acc, u, pcnt, p.slices, flag, p.h, p.sync, spin_lds ? *spin_lds : spin, bad);
+          continue;
+        }
+      }
+      dl_swiglu_pair<MT>(c, U, acc, u, pcnt, p.slices, flag, p.h);
     }
   } else {
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
@@ -1069,16 +1279,16 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   grid_sync(3);
 
   // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
+  bool pre4 = false;
   for (int u = b; u < units[3]; u += G) {
     DlUnit U;
     unit_of(3, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt3, p.splits3, dl_tile_counter(p.sync, nt1 + u % nt3), p.slices, flag, U.dst,
-                   false, false, p.sync);
+    pre4 = combine(U, acc, u, nt3, p.splits3, nt1, false, 4);
   }
   dl_wait_vm<0>();
-  grid_sync(4);
+  grid_sync(4, pre4);
   }
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
@@ -1087,8 +1297,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(4, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    dl_combine<MT>(c, U, acc, u, nt4, p.splits4, dl_tile_counter(p.sync, nt1 + nt3 + u % nt4), p.slices, flag, U.dst,
-                   true, *bad != 0, p.sync, static_cast<const uint16_t*>(p.resid));
+    combine(U, acc, u, nt4, p.splits4, nt1 + nt3, true, 0);
   }
 }
 
