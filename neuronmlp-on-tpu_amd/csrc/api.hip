@@ -1336,11 +1336,13 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   // tiles 8 splits cost 0.8 us.
   const int cap3 = tune().dls3 >= 0 ? tune().dls3 : (mt == 2 ? 8 : 0);
   p.ks3 = dl_plan(ff, r_d / 128, grid, &p.units3, cap3);
-  // Phase 4 at four token tiles (33-64 tokens) in at most 4 K splits: each
-  // tile's last split then sums 4 slices of 64 rows instead of 8, for a
-  // stream that is HBM-bound either way (8B layer, T=64: 90.5 -> 89.2 us;
-  // at 1-32 tokens 4 splits cost 0.5-1 us, their slices being small).
-  const int cap4 = tune().dls4 >= 0 ? tune().dls4 : (mt == 4 ? 4 : 0);
+  // Phase 4 at four token tiles (33-64 tokens) in at most 4 K splits when one
+  // block sums each tile: it then sums 4 slices of 64 rows instead of 8, for
+  // a stream that is HBM-bound either way (8B layer, T=64: 90.5 -> 89.2 us;
+  // at 1-32 tokens 4 splits cost 0.5-1 us, their slices being small).  With
+  // the tiles summed by all their splits (dldist) 8 splits pay: T=48 81.6 ->
+  // 80.5 us, T=64 unchanged.
+  const int cap4 = tune().dls4 >= 0 ? tune().dls4 : (mt == 4 && !tune().dldist ? 4 : 0);
   p.ks4 = dl_plan(r_d, d / 128, grid, &p.units4, cap4);
   p.splits1 = p.units1 / (int)((r_gu + r_u) / 128);
   p.splits3 = p.units3 / (int)(r_d / 128);
