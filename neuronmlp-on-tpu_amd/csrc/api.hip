@@ -464,6 +464,7 @@ struct Tune {
   // decode layer: most K splits of phases 1, 3, 4 (0: grid / tiles; -1: the
   // defaults, dls3 8 at two token tiles, dls4 4 at four, else grid / tiles)
   int dls1 = 0, dls3 = -1, dls4 = -1;
+  bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
   bool dldist = true;  // decode layer, 32+ token rows: split-K tiles and phase-2 pairs finished by all their units
 };
 
@@ -537,6 +538,7 @@ const Tune& tune() {
         if (k == "dls3") r.dls3 = v;
         if (k == "dls4") r.dls4 = v;
         if (k == "dldist") r.dldist = v != 0;
+        if (k == "dlpff") r.dlpff = v != 0;
       }
       pos = end + 1;
     }
@@ -1348,6 +1350,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
+  p.pf_full = tune().dlpff;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;
   p.ld_uu = (int)(ld.uu ? ld.uu : ld.u);

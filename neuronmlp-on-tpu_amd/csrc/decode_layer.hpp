@@ -101,6 +101,10 @@ struct DecLayerParams {
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
   // unit (dl_swiglu_pair_dist).
   int dist;
+  // The weight prefetch at a grid barrier fills all NS ring slots (the last
+  // one where the unit has that many stages), not NS - 1 (DlDepth::PF_FULL
+  // instances only).
+  int pf_full;
   // MLP block (null otherwise): y = bf16(resid + bf16(MLP)); with `gain`
   // (NORM instances) a phase 0 writes RMSNorm(x) to xn, which phase 1 reads
   // instead of x.
@@ -127,6 +131,10 @@ template <int MT>
 struct DlDepth {
   static constexpr int KC = MT == 8 ? 1 : 2;
   static constexpr int NS = MT == 1 ? 6 : 4;
+  // The weight prefetch at a grid barrier fills all NS ring slots rather
+  // than NS - 1 (DecLayerParams::pf_full): 8B layer at 128 tokens 119.7 ->
+  // 118.5 us; at 1-64 tokens 0.2-0.4 us slower, so only eight token tiles.
+  static constexpr bool PF_FULL = MT == 8;
 };
 
 // fp32 -> bf16 round to nearest even in integer form (NaN stays NaN): the
@@ -280,6 +288,7 @@ struct DlCtx {
   lds_cptr l0;
   int wave, lane, lr, lg, T;
   int a_cached;  // DecLayerParams::a_cached
+  int pf_full;   // DecLayerParams::pf_full
 };
 
 // 32-byte unit swizzle of weight row k (128-byte rows, two per 64-bank
@@ -309,6 +318,22 @@ __device__ __forceinline__ void dl_dma_w(const DlCtx& c, const DlUnit& U, int j,
     dma16(rs, voff, live ? (uint32_t)k0 * (uint32_t)U.ldb * 2u : 0u,
           c.lbase + L::W_OFF + slot * L::W_SLOT + kc * kDlWStage + sub * 4096 + (c.wave & 3) * 1024);
   }
+}
+
+// Stages of unit U in the ring (KC 32-k chunks each).
+template <int MT>
+__device__ __forceinline__ int dl_stages(const DlUnit& U) {
+  return (U.ke - U.kb + 32 * DlLds<MT>::KC - 1) / (32 * DlLds<MT>::KC);
+}
+
+// The weight DMAs of a stage that was issued already (KC per wave, as
+// dl_dma_w), fetching nothing into the dummy slot: the memory counter then
+// counts the same operations per step.
+template <int MT>
+__device__ __forceinline__ void dl_dma_w_none(const DlCtx& c, const void* any) {
+  using L = DlLds<MT>;
+#pragma unroll
+  for (int kc = 0; kc < L::KC; ++kc) dma16(make_rsrc_sgpr(any, 0u), kOOB, 0u, c.lbase + L::DUMMY_OFF);
 }
 
 // Activation DMAs of stage j into ring slot `slot` (CNT_A per wave):
@@ -372,7 +397,11 @@ struct DlNoRunOut {
 // Runs one unit: returns the accumulators (lane: D[n = 4*lg + t][m = lr] of
 // each 16-row block mt).  `prefetched`: every wave already issued its
 // weight DMAs of stages 0..NS-2 (at the grid barrier), so every wave's order
-// is W(0..NS-2), A(0..NS-2), then (W, A) per step.  Otherwise the first
+// is W(0..NS-2), A(0..NS-2), then (W, A) per step; with c.pf_full and more
+// than NS - 1 stages it also issued W(NS-1) there, and step 0 issues KC
+// DMAs that fetch nothing in its place (the same count, so the same waits,
+// which only ever need the A of their stage: every W is issued before it).
+// Otherwise the first
 // stages go out as (W, A) pairs, so stage 0 is usable as soon as its own
 // pair lands rather than after every CU's whole first burst (8B layer: T=8
 // 74.6 -> 72.0 us, T=64 103.7 -> 102.7 us), and every wait is the steady
@@ -411,7 +440,9 @@ __device__ __forceinline__ void dl_run(const DlCtx& c, const DlUnit& U, bool pre
       dl_wait_vm<(NS - 2) * S::P>();
     dl_block_sync();
     const int sn = j + NS - 1, slot_n = sn % NS;
-    if (RunOut::kActive && sn >= nk)
+    if (DlDepth<MT>::PF_FULL && j == 0 && prefetched && c.pf_full && sn < nk)
+      dl_dma_w_none<MT>(c, U.b0);  // issued with the prefetch at the grid barrier
+    else if (RunOut::kActive && sn >= nk)
       run_out(sn - nk, slot_n);
     else
       dl_dma_w<MT, DUAL>(c, U, sn, slot_n);
@@ -1060,6 +1091,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   c.lg = c.lane >> 4;
   c.T = p.T;
   c.a_cached = p.a_cached;
+  c.pf_full = p.pf_full;
   int* const flag = reinterpret_cast<int*>(lds + L::FLAG_OFF);
   int* const bad = reinterpret_cast<int*>(lds + L::BAD_OFF);
   uint32_t* const spin_lds = MT >= 4 ? reinterpret_cast<uint32_t*>(lds + L::SPIN_OFF) : nullptr;
@@ -1158,7 +1190,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     if (b < units[phase]) {
       DlUnit U;
       unit_of(phase, b, U);
-      for (int s = 0; s < NS - 1; ++s) {
+      // the last ring slot too (pf_full) where the unit has that stage: dl_run
+      // then issues no weights at its step 0
+      const int ns = DlDepth<MT>::PF_FULL && p.pf_full && NS - 1 < dl_stages<MT>(U) ? NS : NS - 1;
+      for (int s = 0; s < ns; ++s) {
         if (phase == 2 && !p.p2split)
           dl_dma_w<MT, true>(c, U, s, s);
         else
