@@ -465,6 +465,7 @@ struct Tune {
   // defaults, dls3 8 at two token tiles, dls4 4 at four, else grid / tiles)
   int dls1 = 0, dls3 = -1, dls4 = -1;
   bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
+  bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
   bool dldist = true;  // decode layer, 32+ token rows: split-K tiles and phase-2 pairs finished by all their units
 };
 
@@ -538,6 +539,7 @@ const Tune& tune() {
         if (k == "dls3") r.dls3 = v;
         if (k == "dls4") r.dls4 = v;
         if (k == "dldist") r.dldist = v != 0;
+        if (k == "dlready") r.dlready = v != 0;
         if (k == "dlpff") r.dlpff = v != 0;
       }
       pos = end + 1;
@@ -1350,6 +1352,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
+  p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlMaxFlags;
   p.pf_full = tune().dlpff;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;

@@ -97,6 +97,9 @@ struct DecLayerParams {
   // counter after phases 1, 3 and 4's.  Otherwise a unit computes both over
   // 64 columns.
   int p2split;
+  // Phase 4 waits for its XU_d tiles' ready flags (kDlMaxFlags tiles at
+  // most) instead of a grid barrier: the contracted layer and one token tile.
+  int xd_ready;
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
   // unit (dl_swiglu_pair_dist).
@@ -208,6 +211,42 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
         __hip_atomic_fetch_or(&sync[kGvDone], kGvDoneBad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         dl_wait_vm<0>();  // both flags complete before anything this block writes next
         *bad = 1;
+        break;
+      }
+    }
+  }
+  dl_block_sync();
+}
+
+// Tile t's ready flag set to `epoch` by thread 0, once every wave of the
+// block has completed its stores of the tile (vmcnt(0) then the barrier).
+__device__ __forceinline__ void dl_set_ready(uint64_t* sync, int t, uint64_t epoch) {
+  dl_wait_vm<0>();
+  dl_block_sync();
+  if (threadIdx.x == 0) __hip_atomic_store(dl_ready_flag(sync, t), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded wait until the ready flags of tiles t0..t1 (at most 64) hold
+// `epoch`: lane i of wave 0 polls tile t0 + i.  A wait that gives up sets the
+// timeout flags as a grid-barrier wait does.
+__device__ __forceinline__ void dl_wait_ready(uint64_t* sync, int t0, int t1, uint64_t epoch, uint32_t spin,
+                                              int* bad) {
+  if (threadIdx.x < 64) {
+    const int t = t0 + (int)threadIdx.x;
+    bool done = t > t1;
+    uint32_t polls = 0;
+    while (true) {
+      if (!done)
+        done = __hip_atomic_load(dl_ready_flag(sync, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+      if (__builtin_amdgcn_read_exec() == __ballot(done)) break;  // every lane's tile is ready
+      __builtin_amdgcn_s_sleep(1);
+      if (++polls >= spin) {
+        if (threadIdx.x == 0) {
+          __hip_atomic_fetch_or(&sync[kDlFlag], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_or(&sync[kGvDone], kGvDoneBad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          dl_wait_vm<0>();
+          *bad = 1;
+        }
         break;
       }
     }
@@ -1011,7 +1050,8 @@ __device__ __forceinline__ void dl_contract_down(const DlCtx& c, const DecLayerP
 constexpr uint32_t kDlFarArrivals = 16;
 template <int MT>
 __device__ __forceinline__ void dl_contract_combine(const DlCtx& c, const DecLayerParams& p, char* lds, int j, int U2,
-                                                    int cnt0, uint32_t spin_reg, const uint32_t* spin_lds, int* bad) {
+                                                    int cnt0, uint32_t spin_reg, const uint32_t* spin_lds, int* bad,
+                                                    uint64_t epoch) {
   using L = DlLds<MT>;
   static_assert(kDlThreads == 512, "16 groups of 32 threads");
   if (threadIdx.x == 0) {
@@ -1076,11 +1116,15 @@ __device__ __forceinline__ void dl_contract_combine(const DlCtx& c, const DecLay
     dl_store8(p.xd16 + (int64_t)m * p.r_d + 128 * j + 4 * q,
               u32x2{dl_pack_bf16x2(tot.x, tot.y), dl_pack_bf16x2(tot.z, tot.w)});
   }
+  if (epoch) dl_set_ready(p.sync, j, epoch);
 }
 
 template <int MT, bool CONTRACT = false, bool NORM = false>
 __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerParams p) {
   using L = DlLds<MT>;
+  // ready flags: where one block writes each XU_d tile (the contracted
+  // layer's combiners; phase 3's last split at one token tile)
+  constexpr bool XD_READY = CONTRACT || MT == 1;
   __shared__ __attribute__((aligned(1024))) char lds[L::BYTES];
   DlCtx c;
   c.lbase = lds_addr(lds);
@@ -1108,6 +1152,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // Generation at launch start: it cannot advance before every block has
   // arrived at barrier 1, which each block does only after this read.
   const uint64_t gen0 = __hip_atomic_load(&p.sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // XU_d tiles' ready flags in place of the grid barrier before phase 4
+  // (DecLayerParams::xd_ready): this launch's epoch, else 0
+  const uint64_t epoch = (XD_READY && p.xd_ready) ? gen0 + 1 : 0;
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
@@ -1266,10 +1313,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       dl_contract_h<MT>(c, lds, acc);
       dl_contract_down<MT>(c, p, lds, b, U2, nt3, nt1, nk % NS);
     } else if (b < U2 + nt3) {
-      dl_contract_combine<MT>(c, p, lds, b - U2, U2, nt1, spin, spin_lds, bad);
+      dl_contract_combine<MT>(c, p, lds, b - U2, U2, nt1, spin, spin_lds, bad, epoch);
     }
     dl_wait_vm<0>();
-    grid_sync(4);
+    if (epoch)
+      prefetch_w(4);  // phase 4 waits for its XU_d tiles' ready flags instead of a grid barrier
+    else
+      grid_sync(4);
   } else {
   if (p.p2split) {
     // ---- phase 2, one branch per unit: g or u of 128 columns; the second
@@ -1329,15 +1379,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
     pre4 = combine(U, acc, u, nt3, p.splits3, nt1, false, 4);
+    if (epoch && (p.splits3 == 1 || *flag)) dl_set_ready(p.sync, u % nt3, epoch);  // this block wrote the tile
   }
   dl_wait_vm<0>();
-  grid_sync(4, pre4);
+  if (epoch)
+    prefetch_w(4);
+  else
+    grid_sync(4, pre4);
   }
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
   for (int u = b; u < units[4]; u += G) {
     DlUnit U;
     unit_of(4, u, U);
+    if (epoch) dl_wait_ready(p.sync, U.kb / 128, (U.ke - 1) / 128, epoch, spin_lds ? *spin_lds : spin, bad);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
     combine(U, acc, u, nt4, p.splits4, nt1 + nt3, true, 0);

@@ -46,6 +46,20 @@ __device__ __forceinline__ uint32_t* dl_tile_counter(uint64_t* sync, int t) {
 }
 
 
+// Ready flags of the decode layer's XU_d tiles (in place of the grid barrier
+// before its phase 4): words 1..15 of the 16 group-counter lines, which the
+// barrier's counters (word 0) leave free; tile t at line t % 16, word
+// 1 + t / 16, so the pollers of different tiles read different lines.  A
+// flag holds the epoch of the launch that wrote its tile (its generation at
+// launch start plus one: every launch that uses the flags still passes a
+// grid barrier, so the generation, read before any block's first barrier
+// arrival, differs from launch to launch and is the same for all blocks of
+// one).
+constexpr int kDlMaxFlags = kDlGroups * (kDlLine - 1);
+__device__ __forceinline__ uint64_t* dl_ready_flag(uint64_t* sync, int t) {
+  return sync + (t % kDlGroups) * kDlLine + 1 + t / kDlGroups;
+}
+
 // Cache-policy bits of a device-scope (sc1) buffer access: coherent across
 // XCDs without cache maintenance.
 constexpr int kDlSc1 = 16;

@@ -50,6 +50,14 @@ def _contracted(shape, T, padded=False):
             and shape.ff // 64 + shape.rd // 128 <= 256 and (padded or not _p2split_fits(shape)))
 
 
+def _dl_barriers(T, contracted):
+    """Grid barriers of one persistent MFMA decode-layer launch (without the
+    MLP block's RMSNorm phase): the contracted layer 1 (phase 4 waits for its
+    XU_d tiles' ready flags), the three-phase-barrier layer 2 at one 16-row
+    token tile (ready flags before phase 4 too) and 3 from two tiles up."""
+    return 1 if contracted else (2 if T <= 16 else 3)
+
+
 def _gemv_layer(shape, T):
     """Whether a dense bf16 call at decode shapes runs the streaming-GEMV
     layer by default (up to 2 tokens, where neither MFMA layer runs)."""
@@ -274,8 +282,8 @@ def test_decode_layer_workspace_reuse(gpu, shape, Ts):
         y = _np(ops.svd_mlp(t[0][:T].contiguous(), *t[1:], workspace=ws))
         err = _rel(y, O.svd_mlp_ref(xb[:T], *fb, dtype="bfloat16"))
         assert err < BF16_TOL, (T, err)
-        # contracted layer: 2 barriers, GEMV layer: 4, MFMA layer: 3
-        gen += 2 if _contracted(shape, T) else (4 if _gemv_layer(shape, T) else 3)
+        # GEMV layer: 4 barriers, the MFMA layers _dl_barriers
+        gen += 4 if _gemv_layer(shape, T) else _dl_barriers(T, _contracted(shape, T))
         assert _barrier_state(ws) == (gen, 0), T
         assert not any(_tile_counters(ws)), T
 
@@ -454,7 +462,7 @@ def test_contracted_decode_layer_8b(gpu, layer8b, T):
     """The contracted decode layer (each block's h strip kept in LDS and
     multiplied by its Ud rows; the (T, r_d) partials of XU_d summed in unit
     order by dedicated blocks) against the oracle, bitwise on replay, with
-    dense and row-padded factors: one launch with two grid barriers per call,
+    dense and row-padded factors: one launch with one grid barrier per call,
     every tile counter back at zero."""
     shape, f, ft = layer8b
     xt = _to(_x(T, shape.d, 600 + T), torch.bfloat16, gpu)
@@ -462,7 +470,7 @@ def test_contracted_decode_layer_8b(gpu, layer8b, T):
     for fs in (ft, [ops.pad_rows(a, 64) if i % 2 else a for i, a in enumerate(ft)]):
         ws = ops.svd_mlp_workspace(xt, r=shape.r, ff=shape.ff)
         ys = [ops.svd_mlp(xt, *fs, workspace=ws, contracted=True).clone() for _ in range(3)]
-        assert _barrier_state(ws) == (6, 0) and not any(_tile_counters(ws))
+        assert _barrier_state(ws) == (3 * _dl_barriers(T, True), 0) and not any(_tile_counters(ws))
         for y in ys[1:]:
             assert torch.equal(y.view(torch.int16), ys[0].view(torch.int16))
         err = _rel(_np(ys[0]), ref)
@@ -488,7 +496,7 @@ def test_contracted_svd_mlp_entry(gpu, shape, T):
     ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
     y = _np(ops.svd_mlp(*t, workspace=ws, contracted=True))
     if T <= 128:
-        assert _barrier_state(ws)[0] == (2 if T <= 4 else 3) and not any(_tile_counters(ws))
+        assert _barrier_state(ws)[0] == _dl_barriers(T, T <= 4) and not any(_tile_counters(ws))
     ref = O.svd_mlp_ref(xb, *fb, dtype="bfloat16")
     assert _rel(y, ref) < BF16_TOL
     assert _rel(_np(pallas_ops.contracted_svd_mlp(*t)), ref) < BF16_TOL
@@ -708,8 +716,8 @@ def test_mlp_block_fused_into_decode_layer(gpu, layer8b, T, padded):
     assert _rel(runs[0], ref) < BF16_TOL
     assert _rel(runs[0] - xb, ref - xb) < BF16_TOL, _rel(runs[0] - xb, ref - xb)
     assert np.array_equal(runs[0], runs[1])
-    # two launches: 2 or 3 barriers each, plus the one after phase 0; counters back at zero
-    per = (2 if _contracted(shape, T, padded=padded) else 3) + 1
+    # two launches: _dl_barriers each, plus the one after phase 0; counters back at zero
+    per = _dl_barriers(T, _contracted(shape, T, padded=padded)) + 1
     assert _barrier_state(ws) == (2 * per, 0) and not any(_tile_counters(ws))
 
 
@@ -886,7 +894,8 @@ def test_distinct_gate_up_ranks_abi(gpu):
         else:
             assert _rel(_np(y), O.svd_mlp_ref(xb, *fb, dtype="bfloat16")) < BF16_TOL
         if T <= 128 and want == _lib.SVDMLP_OK:
-            assert _barrier_state(ws) == (3, 0) and not any(_tile_counters(ws))   # one decode-layer launch
+            # one decode-layer launch
+            assert _barrier_state(ws) == (_dl_barriers(T, False), 0) and not any(_tile_counters(ws))
 
 
 @pytest.mark.parametrize("T", [1, 8, 64])
@@ -912,14 +921,15 @@ def test_distinct_gate_up_ranks_decode_8b(gpu, T):
     ys = [y0, out.clone(), ops.svd_mlp(*t, workspace=ws, out=out).clone()]
     assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
     assert torch.equal(ys[0].view(torch.int16), ys[2].view(torch.int16))
-    assert _barrier_state(ws) == (9, 0) and not any(_tile_counters(ws))   # three launches of three barriers
+    assert _barrier_state(ws) == (3 * _dl_barriers(T, False), 0) and not any(_tile_counters(ws))   # three launches
     err = _rel(_np(ys[0]), O.svd_mlp_ref(xb, *fb, dtype="bfloat16"))
     print(f"two ranks 8B decode T={T} rel_l2={err:.3e}")
     assert err < BF16_TOL
     yb = _np(ops.svd_mlp_block(t[0], g, *t[1:], eps=1e-5, workspace=ws, out=out))
     ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
     assert _rel(yb, ref) < BF16_TOL and _rel(yb - xb, ref - xb) < BF16_TOL
-    assert _barrier_state(ws) == (13, 0)   # + one launch of four barriers (RMSNorm phase 0)
+    # + one launch with the RMSNorm phase 0's barrier
+    assert _barrier_state(ws) == (4 * _dl_barriers(T, False) + 1, 0)
 
 
 # ---------------------------------------------------------------------------
@@ -991,8 +1001,9 @@ def test_padded_factor_rows(gpu, T):
     ws = ops.svd_mlp_workspace(t[0], r=max(shape.r, shape.rd), ff=shape.ff)
     err = _rel(_np(ops.svd_mlp(t[0], *padded, workspace=ws)), ref)
     assert err < BF16_TOL, err
-    if T <= 128:   # one MFMA decode-layer launch (2 barriers contracted, else 3), counters back at zero
-        assert _barrier_state(ws) == (2 if _contracted(shape, T, padded=True) else 3, 0) and not any(_tile_counters(ws))
+    if T <= 128:   # one MFMA decode-layer launch (_dl_barriers), counters back at zero
+        assert (_barrier_state(ws) == (_dl_barriers(T, _contracted(shape, T, padded=True)), 0)
+                and not any(_tile_counters(ws)))
     dense = _np(ops.svd_mlp(*t))
     # the same math; split-K partials are summed in other orders on the
     # paths the two layouts take, so roundings may differ
