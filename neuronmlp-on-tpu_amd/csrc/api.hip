@@ -1352,7 +1352,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
-  p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlMaxFlags;
+  p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlRowFlag0;
   p.pf_full = tune().dlpff;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;

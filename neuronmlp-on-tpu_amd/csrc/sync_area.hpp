@@ -46,8 +46,8 @@ __device__ __forceinline__ uint32_t* dl_tile_counter(uint64_t* sync, int t) {
 }
 
 
-// Ready flags of the decode layer's XU_d tiles (in place of the grid barrier
-// before its phase 4): words 1..15 of the 16 group-counter lines, which the
+// Ready flags of the decode layer's XU_d tiles and RMSNorm rows (in place of
+// the grid barriers before its phases 4 and 1): words 1..15 of the 16 group-counter lines, which the
 // barrier's counters (word 0) leave free; tile t at line t % 16, word
 // 1 + t / 16, so the pollers of different tiles read different lines.  A
 // flag holds the epoch of the launch that wrote its tile (its generation at
@@ -56,6 +56,9 @@ __device__ __forceinline__ uint32_t* dl_tile_counter(uint64_t* sync, int t) {
 // arrival, differs from launch to launch and is the same for all blocks of
 // one).
 constexpr int kDlMaxFlags = kDlGroups * (kDlLine - 1);
+// Flags kDlRowFlag0 + m: row m of the MLP block's RMSNorm output written
+// (phase 0); XU_d tiles use the flags below kDlRowFlag0.
+constexpr int kDlRowFlag0 = kDlMaxFlags - 128;
 __device__ __forceinline__ uint64_t* dl_ready_flag(uint64_t* sync, int t) {
   return sync + (t % kDlGroups) * kDlLine + 1 + t / kDlGroups;
 }

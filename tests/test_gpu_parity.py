@@ -716,8 +716,8 @@ def test_mlp_block_fused_into_decode_layer(gpu, layer8b, T, padded):
     assert _rel(runs[0], ref) < BF16_TOL
     assert _rel(runs[0] - xb, ref - xb) < BF16_TOL, _rel(runs[0] - xb, ref - xb)
     assert np.array_equal(runs[0], runs[1])
-    # two launches: _dl_barriers each, plus the one after phase 0; counters back at zero
-    per = _dl_barriers(T, _contracted(shape, T, padded=padded)) + 1
+    # two launches of _dl_barriers each (phase 0's rows signal phase 1 by ready flags); counters back at zero
+    per = _dl_barriers(T, _contracted(shape, T, padded=padded))
     assert _barrier_state(ws) == (2 * per, 0) and not any(_tile_counters(ws))
 
 
@@ -928,8 +928,8 @@ def test_distinct_gate_up_ranks_decode_8b(gpu, T):
     yb = _np(ops.svd_mlp_block(t[0], g, *t[1:], eps=1e-5, workspace=ws, out=out))
     ref = O.mlp_block_ref(xb, gain, fb, eps=1e-5, dtype="bfloat16")
     assert _rel(yb, ref) < BF16_TOL and _rel(yb - xb, ref - xb) < BF16_TOL
-    # + one launch with the RMSNorm phase 0's barrier
-    assert _barrier_state(ws) == (4 * _dl_barriers(T, False) + 1, 0)
+    # + one launch of the block (its RMSNorm phase 0 signals phase 1 by ready flags)
+    assert _barrier_state(ws) == (4 * _dl_barriers(T, False), 0)
 
 
 # ---------------------------------------------------------------------------
