@@ -466,6 +466,7 @@ struct Tune {
   int dls1 = 0, dls3 = -1, dls4 = -1;
   bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
   bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
+  bool dlxu = true;     // decode layer: phase 2 waits for its XU tiles' ready flags, not a grid barrier
   bool dldist = true;  // decode layer, 32+ token rows: split-K tiles and phase-2 pairs finished by all their units
 };
 
@@ -539,6 +540,7 @@ const Tune& tune() {
         if (k == "dls3") r.dls3 = v;
         if (k == "dls4") r.dls4 = v;
         if (k == "dldist") r.dldist = v != 0;
+        if (k == "dlxu") r.dlxu = v != 0;
         if (k == "dlready") r.dlready = v != 0;
         if (k == "dlpff") r.dlpff = v != 0;
       }
@@ -1353,6 +1355,19 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
   p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlRowFlag0;
+  // XU tiles' flags after the XU_d tiles'; the contracted layer needs the XU_d
+  // flags as well (it then waits on no grid barrier and arrives at its end)
+  p.xu_flag0 = (int)(r_d / 128);
+  // (the shared split-K combination of phase 1 counts a second round of
+  // arrivals on counters after every other tile counter of the layer)
+  p.cnt2 = (int)((r_gu + r_u) / 128 + r_d / 128 + d / 128 + (p.p2split ? ff / 128 : 0));
+  // From two token tiles up only: with ready flags instead of the barrier
+  // 8B T=32 / 64 / 128 -0.35 / -0.7 / -0.3 us, but the contracted layer at T=1
+  // +1.5 us and the one-tile layer +0.3 us (224 blocks polling all 44 tiles'
+  // flags while the last phase-1 tiles are still combined).
+  p.xu_ready = mt >= 2 && tune().dlxu && (r_gu + r_u) / 128 <= 128 &&
+               r_d / 128 + (r_gu + r_u) / 128 <= kDlRowFlag0 && (!contract || p.xd_ready) &&
+               (!p.dist || p.cnt2 + (r_gu + r_u) / 128 <= kDlMaxTiles);
   p.pf_full = tune().dlpff;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;

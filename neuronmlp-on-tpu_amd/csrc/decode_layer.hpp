@@ -100,6 +100,10 @@ struct DecLayerParams {
   // Phase 4 waits for its XU_d tiles' ready flags (kDlMaxFlags tiles at
   // most) instead of a grid barrier: the contracted layer and one token tile.
   int xd_ready;
+  // Phase 2 waits for the XU tiles' ready flags (flags xu_flag0 .. xu_flag0 +
+  // tiles - 1) instead of a grid barrier
+  int xu_ready, xu_flag0;
+  int cnt2;  // first of phase 1's second-round tile counters (dl_combine_dist with ready flags)
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
   // unit (dl_swiglu_pair_dist).
@@ -220,10 +224,13 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
 
 // Tile t's ready flag set to `epoch` by thread 0, once every wave of the
 // block has completed its stores of the tile (vmcnt(0) then the barrier).
-__device__ __forceinline__ void dl_set_ready(uint64_t* sync, int t, uint64_t epoch) {
+__device__ __forceinline__ void dl_set_ready(uint64_t* flag, uint64_t epoch) {
   dl_wait_vm<0>();
   dl_block_sync();
-  if (threadIdx.x == 0) __hip_atomic_store(dl_ready_flag(sync, t), epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void dl_set_ready(uint64_t* sync, int t, uint64_t epoch) {
+  dl_set_ready(dl_ready_flag(sync, t), epoch);
 }
 
 // Bounded wait until the ready flags of tiles t0..t1 (at most 128) hold
@@ -255,6 +262,26 @@ __device__ __forceinline__ void dl_wait_ready(uint64_t* sync, int t0, int t1, ui
     }
   }
   dl_block_sync();
+}
+
+// The arrival half of dl_grid_sync, with no wait: the generation advances
+// once every block has arrived.  A launch whose blocks otherwise wait only
+// on ready flags arrives here at its end, so that the generation (the
+// flags' epoch) still differs from launch to launch.
+__device__ __forceinline__ void dl_grid_arrive(uint64_t* sync) {
+  dl_block_sync();
+  if (threadIdx.x == 0) {
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t g = b % kDlGroups;
+    const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
+    const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
+    const uint64_t a = __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((a + 1) % gsize == 0) {
+      const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((r + 1) % ngroups == 0)
+        __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // Buffer descriptor of the split-K slice area (kDlMaxGrid units of MT
@@ -768,7 +795,8 @@ template <int MT, class Pre>
 __device__ __forceinline__ bool dl_combine_dist(const DlCtx& c, const DlUnit& U, const f32x4 (&acc)[MT], int u,
                                                 int nt, int splits, uint32_t* cnt, float* slices, int* flag,
                                                 uint16_t* dst, bool out_y, int* bad, uint64_t* sync, uint32_t spin,
-                                                const uint16_t* resid, const Pre& pre) {
+                                                const uint16_t* resid, const Pre& pre, uint64_t* ready = nullptr,
+                                                uint64_t epoch = 0, uint32_t* cnt2 = nullptr) {
   const __amdgpu_buffer_rsrc_t rs = dl_slice_rsrc<MT>(slices);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -830,6 +858,16 @@ __device__ __forceinline__ bool dl_combine_dist(const DlCtx& c, const DlUnit& U,
     }
     constexpr uint32_t kNaN2 = 0x7fc07fc0u;
     dl_store8(dst + (int64_t)m * U.ldo + n, poison ? u32x2{kNaN2, kNaN2} : v);
+  }
+  if (ready) {
+    // a second round of arrivals, each after the split's share is stored,
+    // the last of which marks the tile ready: on a counter of its own (on
+    // `cnt` a split could arrive again before a slower one saw the first
+    // round's zero, which that one would then never see)
+    dl_wait_vm<0>();
+    dl_block_sync();
+    if (threadIdx.x == 0 && dl_arrive_wrap(cnt2, splits))
+      __hip_atomic_store(ready, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   return issued;
 }
@@ -1158,6 +1196,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // XU_d tiles' ready flags in place of the grid barrier before phase 4
   // (DecLayerParams::xd_ready): this launch's epoch, else 0
   const uint64_t epoch = (XD_READY && p.xd_ready) ? gen0 + 1 : 0;
+  // XU tiles' ready flags in place of the grid barrier before phase 2
+  // (DecLayerParams::xu_ready)
+  const uint64_t xu_epoch = (MT >= 2 && p.xu_ready) ? gen0 + 1 : 0;  // (the launcher sets it from two tiles up)
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
@@ -1261,7 +1302,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // splits (dl_combine_dist) or by its last one (dl_combine); `next` is the
   // phase whose first weight stages a waiting split issues (0: none).
   auto combine = [&](const DlUnit& U, f32x4(&acc)[MT], int u, int nt, int splits, int cnt_base, bool out_y,
-                     int next) -> bool {
+                     int next, uint64_t* ready = nullptr) -> bool {
     uint32_t* cnt = dl_tile_counter(p.sync, cnt_base + u % nt);
     const uint16_t* resid = out_y ? static_cast<const uint16_t*>(p.resid) : nullptr;
     if constexpr (MT >= 2) {
@@ -1271,9 +1312,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
                                      if (next == 0 || u + G < units[next - 1]) return false;
                                      prefetch_w(next);
                                      return true;
-                                   });
+                                   }, ready, xu_epoch, dl_tile_counter(p.sync, p.cnt2 + u % nt));
     }
     dl_combine<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, out_y && *bad != 0, p.sync, resid);
+    if (ready && (splits == 1 || *flag)) dl_set_ready(ready, xu_epoch);  // this block wrote the tile
     return false;
   };
 
@@ -1299,10 +1341,27 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     f32x4 acc[MT];
     if (NORM && u == b) dl_wait_ready(p.sync, kDlRowFlag0, kDlRowFlag0 + T - 1, gen0 + 1, spin_lds ? *spin_lds : spin, bad);
     dl_run<MT, false>(c, U, NORM && u == b, acc);
-    pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2);
+    pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2,
+                   xu_epoch ? dl_ready_flag(p.sync, p.xu_flag0 + u % nt1) : nullptr);
   }
   dl_wait_vm<0>();
-  grid_sync(2, pre2);
+  if (xu_epoch) {
+    if (!pre2) prefetch_w(2);
+  } else {
+    grid_sync(2, pre2);
+  }
+  // phase 2's units read every XU tile of their branch (both branches: -1):
+  // wait for their ready flags instead of a grid barrier, once per branch
+  int xu_seen = 0;
+  auto wait_xu = [&](int br) {
+    if (!xu_epoch) return;
+    const int need = br < 0 ? 3 : 1 << br;
+    if ((xu_seen & need) == need) return;
+    const int pg = p.r_gu / 128;
+    dl_wait_ready(p.sync, p.xu_flag0 + (br == 1 ? pg : 0), p.xu_flag0 + (br == 0 ? pg : nt1) - 1, xu_epoch,
+                  spin_lds ? *spin_lds : spin, bad);
+    xu_seen |= need;
+  };
 
   if constexpr (CONTRACT) {
     // ---- phases 2 and 3 contracted: unit b < units2 keeps its h strip in
@@ -1312,6 +1371,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     if (b < U2) {
       DlUnit U;
       unit_of(2, b, U);
+      wait_xu(-1);
       f32x4 acc[MT];
       // the down half's first NS - 1 stages stream in during the gate/up
       // run-out (the launcher checks that the gate/up rank has >= NS - 1 stages)
@@ -1335,6 +1395,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     for (int u = b; u < units[2]; u += G) {
       DlUnit U;
       unit_of(2, u, U);
+      wait_xu(u & 1);
       f32x4 acc[MT];
       dl_run<MT, false>(c, U, u == b, acc);
       uint32_t* pcnt = dl_tile_counter(p.sync, nt1 + nt3 + nt4 + (u >> 1));
@@ -1351,6 +1412,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   for (int u = b; u < units[2]; u += G) {
     DlUnit U;
     unit_of(2, u, U);
+    wait_xu(-1);
     f32x4 acc[MT];
     dl_run<MT, true>(c, U, u == b, acc);
     // waves 4..7 hold u, waves 0..3 g, for the same lanes' (m, n)
@@ -1404,6 +1466,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
     combine(U, acc, u, nt4, p.splits4, nt1 + nt3, true, 0);
+  }
+  // the contracted layer with both flag sets waits on no grid barrier: an
+  // arrival at the end advances the generation, the flags' epoch
+  if constexpr (CONTRACT) {
+    if (xu_epoch) dl_grid_arrive(p.sync);
   }
 }
 

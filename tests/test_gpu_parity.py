@@ -51,11 +51,13 @@ def _contracted(shape, T, padded=False):
 
 
 def _dl_barriers(T, contracted):
-    """Grid barriers of one persistent MFMA decode-layer launch (without the
-    MLP block's RMSNorm phase): the contracted layer 1 (phase 4 waits for its
-    XU_d tiles' ready flags), the three-phase-barrier layer 2 at one 16-row
-    token tile (ready flags before phase 4 too) and 3 from two tiles up."""
-    return 1 if contracted else (2 if T <= 16 else 3)
+    """Grid barriers of one persistent MFMA decode-layer launch on the 8B and
+    test shapes (phase 1 waits for the RMSNorm rows' ready flags in the MLP
+    block): the contracted layer 1 (phase 4 waits for its XU_d tiles' ready
+    flags), the four-phase layer at one 16-row token tile 2 (before phases 2
+    and 3; phase 4 waits for ready flags) and from two tiles up 2 (before
+    phases 3 and 4; phase 2 waits for its XU tiles' ready flags)."""
+    return 1 if contracted else 2
 
 
 def _gemv_layer(shape, T):
