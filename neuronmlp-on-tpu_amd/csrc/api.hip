@@ -467,6 +467,7 @@ struct Tune {
   bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
   bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
   bool dlxu = true;     // decode layer: phase 2 waits for its XU tiles' ready flags, not a grid barrier
+  bool dlxu1 = true;    // decode layer at one token tile: phase 2 waits for one "XU complete" flag
   bool dldist = true;  // decode layer, 32+ token rows: split-K tiles and phase-2 pairs finished by all their units
 };
 
@@ -540,6 +541,7 @@ const Tune& tune() {
         if (k == "dls3") r.dls3 = v;
         if (k == "dls4") r.dls4 = v;
         if (k == "dldist") r.dldist = v != 0;
+        if (k == "dlxu1") r.dlxu1 = v != 0;
         if (k == "dlxu") r.dlxu = v != 0;
         if (k == "dlready") r.dlready = v != 0;
         if (k == "dlpff") r.dlpff = v != 0;
@@ -1368,6 +1370,13 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.xu_ready = mt >= 2 && tune().dlxu && (r_gu + r_u) / 128 <= 128 &&
                r_d / 128 + (r_gu + r_u) / 128 <= kDlRowFlag0 && (!contract || p.xd_ready) &&
                (!p.dist || p.cnt2 + (r_gu + r_u) / 128 <= kDlMaxTiles);
+  // One token tile (four-phase layer): one flag for all of XU (mode 2), stored
+  // by the last of the phase-1 tiles' writers to count down on one counter
+  // (T=2-16 -0.7 us, the MLP block -0.8 to -1.2 us).  Not in the contracted
+  // layer, which would then wait on no barrier and end in an arrival whose
+  // atomics the last blocks wait for (T=1 +0.85 us).
+  if (mt == 1 && !contract && tune().dlxu1 && p.xd_ready && r_d / 128 < kDlRowFlag0 && p.cnt2 < kDlMaxTiles)
+    p.xu_ready = 2;
   p.pf_full = tune().dlpff;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;

@@ -102,7 +102,7 @@ struct DecLayerParams {
   int xd_ready;
   // Phase 2 waits for the XU tiles' ready flags (flags xu_flag0 .. xu_flag0 +
   // tiles - 1) instead of a grid barrier
-  int xu_ready, xu_flag0;
+  int xu_ready, xu_flag0;  // xu_ready: 0 barrier, 1 a flag per XU tile, 2 one flag for all of XU
   int cnt2;  // first of phase 1's second-round tile counters (dl_combine_dist with ready flags)
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
@@ -1198,7 +1198,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   const uint64_t epoch = (XD_READY && p.xd_ready) ? gen0 + 1 : 0;
   // XU tiles' ready flags in place of the grid barrier before phase 2
   // (DecLayerParams::xu_ready)
-  const uint64_t xu_epoch = (MT >= 2 && p.xu_ready) ? gen0 + 1 : 0;  // (the launcher sets it from two tiles up)
+  // 1: one flag per XU tile (from two token tiles up), 2: one flag for all
+  // of XU, stored by the last of the tiles' writers to count down (one tile)
+  const uint64_t xu_epoch = ((MT >= 2 && p.xu_ready == 1) || (MT == 1 && !CONTRACT && p.xu_ready == 2)) ? gen0 + 1 : 0;
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
@@ -1315,7 +1317,17 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
                                    }, ready, xu_epoch, dl_tile_counter(p.sync, p.cnt2 + u % nt));
     }
     dl_combine<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, out_y && *bad != 0, p.sync, resid);
-    if (ready && (splits == 1 || *flag)) dl_set_ready(ready, xu_epoch);  // this block wrote the tile
+    if (ready && (splits == 1 || *flag)) {  // this block wrote the tile
+      if (MT == 1 && p.xu_ready == 2) {
+        // one flag for all tiles: the last writer to arrive stores it
+        dl_wait_vm<0>();
+        dl_block_sync();
+        if (threadIdx.x == 0 && dl_arrive_wrap(dl_tile_counter(p.sync, p.cnt2), nt))
+          __hip_atomic_store(ready, xu_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        dl_set_ready(ready, xu_epoch);
+      }
+    }
     return false;
   };
 
@@ -1342,7 +1354,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     if (NORM && u == b) dl_wait_ready(p.sync, kDlRowFlag0, kDlRowFlag0 + T - 1, gen0 + 1, spin_lds ? *spin_lds : spin, bad);
     dl_run<MT, false>(c, U, NORM && u == b, acc);
     pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2,
-                   xu_epoch ? dl_ready_flag(p.sync, p.xu_flag0 + u % nt1) : nullptr);
+                   xu_epoch ? dl_ready_flag(p.sync, p.xu_flag0 + (MT == 1 ? 0 : u % nt1)) : nullptr);
   }
   dl_wait_vm<0>();
   if (xu_epoch) {
@@ -1358,8 +1370,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     const int need = br < 0 ? 3 : 1 << br;
     if ((xu_seen & need) == need) return;
     const int pg = p.r_gu / 128;
-    dl_wait_ready(p.sync, p.xu_flag0 + (br == 1 ? pg : 0), p.xu_flag0 + (br == 0 ? pg : nt1) - 1, xu_epoch,
-                  spin_lds ? *spin_lds : spin, bad);
+    if (MT == 1)
+      dl_wait_ready(p.sync, p.xu_flag0, p.xu_flag0, xu_epoch, spin_lds ? *spin_lds : spin, bad);
+    else
+      dl_wait_ready(p.sync, p.xu_flag0 + (br == 1 ? pg : 0), p.xu_flag0 + (br == 0 ? pg : nt1) - 1, xu_epoch,
+                    spin_lds ? *spin_lds : spin, bad);
     xu_seen |= need;
   };
 
