@@ -1370,11 +1370,12 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.xu_ready = mt >= 2 && tune().dlxu && (r_gu + r_u) / 128 <= 128 &&
                r_d / 128 + (r_gu + r_u) / 128 <= kDlRowFlag0 && (!contract || p.xd_ready) &&
                (!p.dist || p.cnt2 + (r_gu + r_u) / 128 <= kDlMaxTiles);
-  // One token tile (four-phase layer): one flag for all of XU (mode 2), stored
-  // by the last of the phase-1 tiles' writers to count down on one counter
-  // (T=2-16 -0.7 us, the MLP block -0.8 to -1.2 us).  Not in the contracted
-  // layer, which would then wait on no barrier and end in an arrival whose
-  // atomics the last blocks wait for (T=1 +0.85 us).
+  // One token tile (four-phase layer): one flag for all of XU (mode 2),
+  // stored by the last of the phase-1 tiles' writers to count down on one
+  // counter (T=2-16 -0.7 us, the MLP block -0.8 to -1.2 us).  Not in the
+  // contracted layer, which then waits on no grid barrier and needs an
+  // arrival-only one for the flags' epoch: T=1 +0.85 us with it at the
+  // launch's end (the last blocks wait for its atomics), +0.35 us after phase 1.
   if (mt == 1 && !contract && tune().dlxu1 && p.xd_ready && r_d / 128 < kDlRowFlag0 && p.cnt2 < kDlMaxTiles)
     p.xu_ready = 2;
   p.pf_full = tune().dlpff;

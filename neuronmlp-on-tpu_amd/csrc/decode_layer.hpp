@@ -264,26 +264,6 @@ __device__ __forceinline__ void dl_wait_ready(uint64_t* sync, int t0, int t1, ui
   dl_block_sync();
 }
 
-// The arrival half of dl_grid_sync, with no wait: the generation advances
-// once every block has arrived.  A launch whose blocks otherwise wait only
-// on ready flags arrives here at its end, so that the generation (the
-// flags' epoch) still differs from launch to launch.
-__device__ __forceinline__ void dl_grid_arrive(uint64_t* sync) {
-  dl_block_sync();
-  if (threadIdx.x == 0) {
-    const uint32_t G = gridDim.x, b = blockIdx.x;
-    const uint32_t g = b % kDlGroups;
-    const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
-    const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
-    const uint64_t a = __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((a + 1) % gsize == 0) {
-      const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if ((r + 1) % ngroups == 0)
-        __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
 // Buffer descriptor of the split-K slice area (kDlMaxGrid units of MT
 // 16-row blocks, 2048 floats each), the cache-policy bits of a device-scope
 // (sc1) buffer access, and an offset past every record.
@@ -1481,11 +1461,6 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
     combine(U, acc, u, nt4, p.splits4, nt1 + nt3, true, 0);
-  }
-  // the contracted layer with both flag sets waits on no grid barrier: an
-  // arrival at the end advances the generation, the flags' epoch
-  if constexpr (CONTRACT) {
-    if (xu_epoch) dl_grid_arrive(p.sync);
   }
 }
 
