@@ -468,6 +468,7 @@ struct Tune {
   bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
   bool dlxu = true;     // decode layer: phase 2 waits for its XU tiles' ready flags, not a grid barrier
   bool dlxu1 = true;    // decode layer at one token tile: phase 2 waits for one "XU complete" flag
+  bool dlp4n = true;    // decode layer at one token tile: phase 4 as 16-column units without a K split
   bool dldist = true;  // decode layer, 32+ token rows: split-K tiles and phase-2 pairs finished by all their units
 };
 
@@ -541,6 +542,7 @@ const Tune& tune() {
         if (k == "dls3") r.dls3 = v;
         if (k == "dls4") r.dls4 = v;
         if (k == "dldist") r.dldist = v != 0;
+        if (k == "dlp4n") r.dlp4n = v != 0;
         if (k == "dlxu1") r.dlxu1 = v != 0;
         if (k == "dlxu") r.dlxu = v != 0;
         if (k == "dlready") r.dlready = v != 0;
@@ -1357,6 +1359,8 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
   p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlRowFlag0;
+  p.p4narrow = mt == 1 && p.xd_ready && tune().dlp4n && d / 16 == grid && r_d % 32 == 0 &&
+               r_d / 32 <= kDlNarrowMaxChunks && r_d * 32 <= 96 * 1024;
   // XU tiles' flags after the XU_d tiles'; the contracted layer needs the XU_d
   // flags as well (it then waits on no grid barrier and arrives at its end)
   p.xu_flag0 = (int)(r_d / 128);

@@ -102,7 +102,11 @@ struct DecLayerParams {
   int xd_ready;
   // Phase 2 waits for the XU tiles' ready flags (flags xu_flag0 .. xu_flag0 +
   // tiles - 1) instead of a grid barrier
-  int xu_ready, xu_flag0;  // xu_ready: 0 barrier, 1 a flag per XU tile, 2 one flag for all of XU
+  int xu_ready, xu_flag0;
+  // Phase 4 at one token tile as 16-column units over the whole rank, one per
+  // block (dl_narrow_unit): grid == d / 16, r_d a multiple of 32, at most
+  // kDlNarrowMaxChunks 32-k chunks, with the XU_d tiles' ready flags
+  int p4narrow;  // xu_ready: 0 barrier, 1 a flag per XU tile, 2 one flag for all of XU
   int cnt2;  // first of phase 1's second-round tile counters (dl_combine_dist with ready flags)
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
@@ -852,6 +856,111 @@ __device__ __forceinline__ bool dl_combine_dist(const DlCtx& c, const DlUnit& U,
   return issued;
 }
 
+// ---------------------------------------------------------------------------
+// Phase 4 at one token tile without a K split (DecLayerParams::p4narrow):
+// block b owns 16 columns of y over the whole rank, so no block waits for
+// another's partial sums at the end.  Its Vd strip (r_d k-rows x 32 bytes,
+// 88 KB at the 8B shape) is brought into LDS whole, by DMAs issued as soon
+// as the block's previous phase ends; once the XU_d tiles' ready flags are
+// set, each wave loads its 1/8 of the k range of XU_d straight into
+// registers (16 bytes per lane and 32-k chunk, the MFMA's B operand: rows
+// past T are zeros, not loaded) and runs its MFMAs, and the 8 waves' sums
+// are added through LDS in wave order.
+// ---------------------------------------------------------------------------
+
+// Columns of block b: 16-column tile c = 4q + r, where the four tiles of a
+// 64-column group q (one 128-byte piece of a Vd row) go to blocks on one XCD
+// (block b runs on XCD b % 8), so that XCD's L2 fetches each line once.
+__device__ __forceinline__ int dl_narrow_tile(int b, int G) {
+  if (G != 256) return b;
+  const int x = b % 8, rest = b / 8, r = rest % 4, qh = rest / 4;
+  return 4 * (x + 8 * qh) + r;
+}
+
+// LDS byte of (k-row, 16-byte half) of the strip: 32-byte rows, 1 KB per
+// 32-k chunk, bit 7 flipped for rows whose bit 3 is set.  A transposing
+// read's lanes 0-15 touch rows k0..k0+3 and lanes 16-31 rows k0+8..k0+11:
+// 128 bytes each, which the flip puts on the two halves of the 64 banks.
+__device__ __forceinline__ uint32_t dl_narrow_swz(uint32_t o) { return o ^ (((o >> 8) & 1u) << 7); }
+
+constexpr int kDlNarrowMaxChunks = 128;  // r_d <= 4096
+
+// DMAs of the strip of columns n0..n0+15 into LDS bytes [0, r_d * 32):
+// chunk ch (32 k-rows) by wave ch % 8, one 1 KB instruction each.
+__device__ __forceinline__ void dl_narrow_dma(const DlCtx& c, const DecLayerParams& p, int n0) {
+  const int nch = p.r_d / 32;
+  const i32x4 rs = make_rsrc_sgpr(p.vd, (uint32_t)((int64_t)p.r_d * p.ld_vd * 2));
+  const uint32_t ol = dl_narrow_swz(16u * (uint32_t)c.lane);  // logical byte of the lane's LDS slot
+  const uint32_t row = ol >> 5, half = (ol >> 4) & 1u;
+  const uint32_t voff = row * (uint32_t)p.ld_vd * 2u + (uint32_t)(n0 + 8 * (int)half) * 2u;
+  for (int ch = c.wave; ch < nch; ch += 8)
+    dma16(rs, voff, (uint32_t)(32 * ch) * (uint32_t)p.ld_vd * 2u, c.lbase + 1024u * (uint32_t)ch);
+}
+
+// The unit: the strip's DMAs were issued (dl_narrow_dma) and the XU_d
+// tiles are ready.  y (row pitch d) = bf16 of the sum, with `resid` added
+// as in dl_combine; NaN where `poison`.
+__device__ __forceinline__ void dl_narrow_unit(const DlCtx& c, const DecLayerParams& p, char* lds, int n0,
+                                               bool poison, const uint16_t* resid) {
+  const int nch = p.r_d / 32, per = (nch + 7) / 8;
+  const int ch0 = c.wave * per;
+  const int m = c.lr;
+  const bool live_row = m < c.T;
+  // XU_d rows through the caches where the workspace is 128-byte aligned (as
+  // the ring's activation DMAs), device-scope otherwise; rows past T and
+  // chunks past the wave's range read zeros (an offset past the records)
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc(p.xd16, 0, (int)((int64_t)c.T * p.r_d * 2), 0x00020000);
+  u32x4 fa[kDlNarrowMaxChunks / 8];
+#pragma unroll
+  for (int i = 0; i < kDlNarrowMaxChunks / 8; ++i) {
+    const int ch = ch0 + i;
+    if (i < per) {
+      const uint32_t off = (ch < nch && live_row) ? (uint32_t)(((int64_t)m * p.r_d + 32 * ch + 8 * c.lg) * 2) : kDlPastSlices;
+      fa[i] = c.a_cached ? __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0)
+                         : __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kDlSc1);
+    } else {
+      fa[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  dl_wait_vm<0>();  // the strip's DMAs and the loads above
+  dl_block_sync();
+  // transposing reads: lane s of group lg points at row 8 lg + s / 4 (+ 4 for
+  // the upper half) of the chunk, bytes 8 (s % 4)
+  const uint32_t lo_off = (uint32_t)(8 * c.lg + (c.lr >> 2)) * 32u + 8u * (uint32_t)(c.lr & 3);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kDlNarrowMaxChunks / 8; ++i) {
+    const int ch = ch0 + i;
+    if (i < per && ch < nch) {
+      const lds_cptr base = c.l0 + 1024 * ch;
+      const u32x2 lo = lds_read_tr(base + dl_narrow_swz(lo_off)), hi = lds_read_tr(base + dl_narrow_swz(lo_off + 128u));
+      acc = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, fa[i], acc, __bf16{});
+    }
+  }
+  // the 8 waves' sums, added in wave order through LDS (the strip is read)
+  dl_block_sync();
+  f32x4* part = reinterpret_cast<f32x4*>(lds);
+  part[c.wave * 64 + c.lane] = acc;
+  dl_block_sync();
+  if (c.wave == 0 && live_row) {
+    f32x4 tot = part[c.lane];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) tot += part[w * 64 + c.lane];
+    const int n = n0 + 4 * c.lg;
+    u32x2 v = u32x2{dl_pack_bf16x2(tot.x, tot.y), dl_pack_bf16x2(tot.z, tot.w)};
+    if (resid && !poison) {
+      const u32x2 xr2 = *reinterpret_cast<const u32x2*>(resid + (int64_t)m * p.d + n);
+      v = u32x2{dl_pack_bf16x2(__uint_as_float(xr2.x << 16) + __uint_as_float(v.x << 16),
+                               __uint_as_float(xr2.x & 0xffff0000u) + __uint_as_float(v.x & 0xffff0000u)),
+                dl_pack_bf16x2(__uint_as_float(xr2.y << 16) + __uint_as_float(v.y << 16),
+                               __uint_as_float(xr2.y & 0xffff0000u) + __uint_as_float(v.y & 0xffff0000u))};
+    }
+    constexpr uint32_t kNaN2 = 0x7fc07fc0u;
+    dl_store8(static_cast<uint16_t*>(p.y) + (int64_t)m * p.d + n, poison ? u32x2{kNaN2, kNaN2} : v);
+  }
+}
+
 // Phase 0 of the MLP block: row `row` of x normalised into xn,
 // bf16(gain * (x * rsqrt(mean(x^2) + eps))), LlamaRMSNorm's fp32 formula
 // (models/modeling_llama.py:257-262) rounded once.  Each thread holds 8
@@ -1274,6 +1383,15 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       }
     }
   };
+  // phase 4's first weights: the narrow unit's whole strip (p4narrow), else
+  // the ring's first stages
+  const bool narrow4 = MT == 1 && p.p4narrow;
+  auto prefetch4 = [&] {
+    if (narrow4)
+      dl_narrow_dma(c, p, 16 * dl_narrow_tile(b, G));
+    else
+      prefetch_w(4);
+  };
   // pre_done: the block already issued those DMAs (dl_combine_dist)
   auto grid_sync = [&](int next_phase, bool pre_done = false) {
     dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] {
@@ -1380,7 +1498,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     }
     dl_wait_vm<0>();
     if (epoch)
-      prefetch_w(4);  // phase 4 waits for its XU_d tiles' ready flags instead of a grid barrier
+      prefetch4();  // phase 4 waits for its XU_d tiles' ready flags instead of a grid barrier
     else
       grid_sync(4);
   } else {
@@ -1448,12 +1566,20 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   dl_wait_vm<0>();
   if (epoch)
-    prefetch_w(4);
+    prefetch4();
   else
     grid_sync(4, pre4);
   }
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
+  if (narrow4) {
+    if constexpr (MT == 1) {
+      dl_wait_ready(p.sync, 0, nt3 - 1, epoch, spin_lds ? *spin_lds : spin, bad);
+      // (read after every XU_d tile's flag: any wait that gave up set it before)
+      const bool poison = *bad != 0 || __hip_atomic_load(&p.sync[kDlFlag], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+      dl_narrow_unit(c, p, lds, 16 * dl_narrow_tile(b, G), poison, static_cast<const uint16_t*>(p.resid));
+    }
+  } else
   for (int u = b; u < units[4]; u += G) {
     DlUnit U;
     unit_of(4, u, U);
