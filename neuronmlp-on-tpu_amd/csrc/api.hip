@@ -1359,6 +1359,9 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
   p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlRowFlag0;
+  // Phase 4 at one token tile as 16-column units over the whole rank (T=1
+  // 66.3 -> 63.7 us, T=2 -1.1 us); from two tiles up each unit would load
+  // all of the (T, r_d) XU_d into registers: T=32 / 64 / 128 +4.5 / +5 / +11 us.
   p.p4narrow = mt == 1 && p.xd_ready && tune().dlp4n && d / 16 == grid && r_d % 32 == 0 &&
                r_d / 32 <= kDlNarrowMaxChunks && r_d * 32 <= 96 * 1024;
   // XU tiles' flags after the XU_d tiles'; the contracted layer needs the XU_d

@@ -899,54 +899,65 @@ __device__ __forceinline__ void dl_narrow_dma(const DlCtx& c, const DecLayerPara
 
 // The unit: the strip's DMAs were issued (dl_narrow_dma) and the XU_d
 // tiles are ready.  y (row pitch d) = bf16 of the sum, with `resid` added
-// as in dl_combine; NaN where `poison`.
+// as in dl_combine; NaN where `poison`.  The wave's chunks go in batches of
+// NB, whose MT * NB activation loads per lane (16) are in flight at once.
+template <int MT>
 __device__ __forceinline__ void dl_narrow_unit(const DlCtx& c, const DecLayerParams& p, char* lds, int n0,
                                                bool poison, const uint16_t* resid) {
+  constexpr int NB = 16 / MT;
   const int nch = p.r_d / 32, per = (nch + 7) / 8;
   const int ch0 = c.wave * per;
-  const int m = c.lr;
-  const bool live_row = m < c.T;
   // XU_d rows through the caches where the workspace is 128-byte aligned (as
   // the ring's activation DMAs), device-scope otherwise; rows past T and
   // chunks past the wave's range read zeros (an offset past the records)
   const __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc(p.xd16, 0, (int)((int64_t)c.T * p.r_d * 2), 0x00020000);
-  u32x4 fa[kDlNarrowMaxChunks / 8];
-#pragma unroll
-  for (int i = 0; i < kDlNarrowMaxChunks / 8; ++i) {
-    const int ch = ch0 + i;
-    if (i < per) {
-      const uint32_t off = (ch < nch && live_row) ? (uint32_t)(((int64_t)m * p.r_d + 32 * ch + 8 * c.lg) * 2) : kDlPastSlices;
-      fa[i] = c.a_cached ? __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0)
-                         : __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kDlSc1);
-    } else {
-      fa[i] = u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  dl_wait_vm<0>();  // the strip's DMAs and the loads above
-  dl_block_sync();
   // transposing reads: lane s of group lg points at row 8 lg + s / 4 (+ 4 for
   // the upper half) of the chunk, bytes 8 (s % 4)
   const uint32_t lo_off = (uint32_t)(8 * c.lg + (c.lr >> 2)) * 32u + 8u * (uint32_t)(c.lr & 3);
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[MT];
 #pragma unroll
-  for (int i = 0; i < kDlNarrowMaxChunks / 8; ++i) {
-    const int ch = ch0 + i;
-    if (i < per && ch < nch) {
-      const lds_cptr base = c.l0 + 1024 * ch;
-      const u32x2 lo = lds_read_tr(base + dl_narrow_swz(lo_off)), hi = lds_read_tr(base + dl_narrow_swz(lo_off + 128u));
-      acc = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, fa[i], acc, __bf16{});
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i0 = 0; i0 < per; i0 += NB) {
+    u32x4 fa[NB][MT];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int ch = ch0 + i0 + i, m = 16 * mt + c.lr;
+        const uint32_t off = (i0 + i < per && ch < nch && m < c.T)
+                                 ? (uint32_t)(((int64_t)m * p.r_d + 32 * ch + 8 * c.lg) * 2)
+                                 : kDlPastSlices;
+        fa[i][mt] = c.a_cached ? __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0)
+                               : __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, kDlSc1);
+      }
+    dl_wait_vm<0>();  // (the first batch: the strip's DMAs too)
+    if (i0 == 0) dl_block_sync();
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int ch = ch0 + i0 + i;
+      if (i0 + i < per && ch < nch) {
+        const lds_cptr base = c.l0 + 1024 * ch;
+        const u32x2 lo = lds_read_tr(base + dl_narrow_swz(lo_off)), hi = lds_read_tr(base + dl_narrow_swz(lo_off + 128u));
+        const u32x4 fb = u32x4{lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_chunk(fb, fa[i][mt], acc[mt], __bf16{});
+      }
     }
   }
   // the 8 waves' sums, added in wave order through LDS (the strip is read)
   dl_block_sync();
   f32x4* part = reinterpret_cast<f32x4*>(lds);
-  part[c.wave * 64 + c.lane] = acc;
-  dl_block_sync();
-  if (c.wave == 0 && live_row) {
-    f32x4 tot = part[c.lane];
 #pragma unroll
-    for (int w = 1; w < 8; ++w) tot += part[w * 64 + c.lane];
+  for (int mt = 0; mt < MT; ++mt) part[(c.wave * MT + mt) * 64 + c.lane] = acc[mt];
+  dl_block_sync();
+  // wave w finishes 16-row blocks w, w + 8, ... (MT <= 8: at most one)
+  for (int mt = c.wave; mt < MT; mt += 8) {
+    const int m = 16 * mt + c.lr;
+    if (m >= c.T) continue;
+    f32x4 tot = part[mt * 64 + c.lane];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) tot += part[(w * MT + mt) * 64 + c.lane];
     const int n = n0 + 4 * c.lg;
     u32x2 v = u32x2{dl_pack_bf16x2(tot.x, tot.y), dl_pack_bf16x2(tot.z, tot.w)};
     if (resid && !poison) {
@@ -1368,7 +1379,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   const int units[5] = {0, p.units1, p.units2, p.units3, p.units4};
   // The first NS - 1 weight stages of this block's first unit of `phase`,
   // issued at the barrier ahead of it, once the block has arrived.
-  auto prefetch_w = [&](int phase) {
+  // phase 4's first weights: the narrow unit's whole strip (p4narrow), else
+  // the ring's first stages
+  const bool narrow4 = MT == 1 && p.p4narrow;  // (from two tiles up every unit would load all of XU_d: T=64 +5 us)
+  auto prefetch_w_ring = [&](int phase) {
     if (b < units[phase]) {
       DlUnit U;
       unit_of(phase, b, U);
@@ -1383,15 +1397,13 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       }
     }
   };
-  // phase 4's first weights: the narrow unit's whole strip (p4narrow), else
-  // the ring's first stages
-  const bool narrow4 = MT == 1 && p.p4narrow;
-  auto prefetch4 = [&] {
-    if (narrow4)
+  auto prefetch_w = [&](int phase) {
+    if (phase == 4 && narrow4)
       dl_narrow_dma(c, p, 16 * dl_narrow_tile(b, G));
     else
-      prefetch_w(4);
+      prefetch_w_ring(phase);
   };
+  auto prefetch4 = [&] { prefetch_w(4); };
   // pre_done: the block already issued those DMAs (dl_combine_dist)
   auto grid_sync = [&](int next_phase, bool pre_done = false) {
     dl_grid_sync(p.sync, gen0, ++nbar, spin, spin_lds, bad, [&] {
@@ -1573,12 +1585,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----
   if (narrow4) {
-    if constexpr (MT == 1) {
-      dl_wait_ready(p.sync, 0, nt3 - 1, epoch, spin_lds ? *spin_lds : spin, bad);
-      // (read after every XU_d tile's flag: any wait that gave up set it before)
-      const bool poison = *bad != 0 || __hip_atomic_load(&p.sync[kDlFlag], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
-      dl_narrow_unit(c, p, lds, 16 * dl_narrow_tile(b, G), poison, static_cast<const uint16_t*>(p.resid));
-    }
+    if (epoch) dl_wait_ready(p.sync, 0, nt3 - 1, epoch, spin_lds ? *spin_lds : spin, bad);
+    // (read after every XU_d tile's flag or the barrier: any wait that gave up set it before)
+    const bool poison = *bad != 0 || __hip_atomic_load(&p.sync[kDlFlag], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    dl_narrow_unit<MT>(c, p, lds, 16 * dl_narrow_tile(b, G), poison, static_cast<const uint16_t*>(p.resid));
   } else
   for (int u = b; u < units[4]; u += G) {
     DlUnit U;
