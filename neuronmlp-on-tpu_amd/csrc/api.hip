@@ -466,6 +466,7 @@ struct Tune {
   int dls1 = 0, dls3 = -1, dls4 = -1;
   bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
   bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
+  bool dlready3 = true; // ... also from two token tiles up (XU_d tiles written by all their splits)
   bool dlxu = true;     // decode layer: phase 2 waits for its XU tiles' ready flags, not a grid barrier
   bool dlxu1 = true;    // decode layer at one token tile: phase 2 waits for one "XU complete" flag
   bool dlp4n = true;    // decode layer at one token tile: phase 4 as 16-column units without a K split
@@ -546,6 +547,7 @@ const Tune& tune() {
         if (k == "dlxu1") r.dlxu1 = v != 0;
         if (k == "dlxu") r.dlxu = v != 0;
         if (k == "dlready") r.dlready = v != 0;
+        if (k == "dlready3") r.dlready3 = v != 0;
         if (k == "dlpff") r.dlpff = v != 0;
       }
       pos = end + 1;
@@ -1358,7 +1360,16 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.splits3 = p.units3 / (int)(r_d / 128);
   p.splits4 = p.units4 / (int)(d / 128);
   p.dist = mt >= 2 && tune().dldist;
-  p.xd_ready = (contract || mt == 1) && tune().dlready && r_d / 128 <= kDlRowFlag0;
+  // (the shared split-K combinations count a second round of arrivals on
+  // counters after every other tile counter of the layer: phase 1's XU
+  // tiles, then phase 3's XU_d tiles)
+  p.cnt2 = (int)((r_gu + r_u) / 128 + r_d / 128 + d / 128 + (p.p2split ? ff / 128 : 0));
+  // From two token tiles up the XU_d tiles are written by all their splits,
+  // whose second arrivals set the flag (8B layer, padded V rows, two
+  // alternating runs: T=17 / 32 / 64 / 128 72.5 / 74.0 / 85.1 / 118.9 ->
+  // 71.4 / 72.7 / 83.1 / 115.8 us; the 8-tile instance +5 VGPRs).
+  p.xd_ready = (contract || mt == 1 || (p.dist && tune().dlready3 && p.cnt2 + (r_gu + r_u) / 128 + r_d / 128 <= kDlMaxTiles)) &&
+               tune().dlready && r_d / 128 <= kDlRowFlag0;
   // Phase 4 at one token tile as 16-column units over the whole rank (T=1
   // 66.3 -> 63.7 us, T=2 -1.1 us); from two tiles up each unit would load
   // all of the (T, r_d) XU_d into registers: T=32 / 64 / 128 +4.5 / +5 / +11 us.
@@ -1367,9 +1378,6 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   // XU tiles' flags after the XU_d tiles'; the contracted layer needs the XU_d
   // flags as well (it then waits on no grid barrier and arrives at its end)
   p.xu_flag0 = (int)(r_d / 128);
-  // (the shared split-K combination of phase 1 counts a second round of
-  // arrivals on counters after every other tile counter of the layer)
-  p.cnt2 = (int)((r_gu + r_u) / 128 + r_d / 128 + d / 128 + (p.p2split ? ff / 128 : 0));
   // From two token tiles up only: with ready flags instead of the barrier
   // 8B T=32 / 64 / 128 -0.35 / -0.7 / -0.3 us, but the contracted layer at T=1
   // +1.5 us and the one-tile layer +0.3 us (224 blocks polling all 44 tiles'

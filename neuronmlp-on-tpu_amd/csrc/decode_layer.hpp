@@ -98,7 +98,8 @@ struct DecLayerParams {
   // 64 columns.
   int p2split;
   // Phase 4 waits for its XU_d tiles' ready flags (kDlMaxFlags tiles at
-  // most) instead of a grid barrier: the contracted layer and one token tile.
+  // most) instead of a grid barrier: the contracted layer, one token tile,
+  // and from two tiles up with the tiles written by all their splits (dist).
   int xd_ready;
   // Phase 2 waits for the XU tiles' ready flags (flags xu_flag0 .. xu_flag0 +
   // tiles - 1) instead of a grid barrier
@@ -107,7 +108,9 @@ struct DecLayerParams {
   // block (dl_narrow_unit): grid == d / 16, r_d a multiple of 32, at most
   // kDlNarrowMaxChunks 32-k chunks, with the XU_d tiles' ready flags
   int p4narrow;  // xu_ready: 0 barrier, 1 a flag per XU tile, 2 one flag for all of XU
-  int cnt2;  // first of phase 1's second-round tile counters (dl_combine_dist with ready flags)
+  // First of the second-round tile counters of dl_combine_dist with ready
+  // flags: phase 1's XU tiles, then phase 3's XU_d tiles.
+  int cnt2;
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
   // unit (dl_swiglu_pair_dist).
@@ -1263,9 +1266,6 @@ __device__ __forceinline__ void dl_contract_combine(const DlCtx& c, const DecLay
 template <int MT, bool CONTRACT = false, bool NORM = false>
 __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerParams p) {
   using L = DlLds<MT>;
-  // ready flags: where one block writes each XU_d tile (the contracted
-  // layer's combiners; phase 3's last split at one token tile)
-  constexpr bool XD_READY = CONTRACT || MT == 1;
   __shared__ __attribute__((aligned(1024))) char lds[L::BYTES];
   DlCtx c;
   c.lbase = lds_addr(lds);
@@ -1295,7 +1295,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   const uint64_t gen0 = __hip_atomic_load(&p.sync[kDlGen], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // XU_d tiles' ready flags in place of the grid barrier before phase 4
   // (DecLayerParams::xd_ready): this launch's epoch, else 0
-  const uint64_t epoch = (XD_READY && p.xd_ready) ? gen0 + 1 : 0;
+  const uint64_t epoch = p.xd_ready ? gen0 + 1 : 0;
   // XU tiles' ready flags in place of the grid barrier before phase 2
   // (DecLayerParams::xu_ready)
   // 1: one flag per XU tile (from two token tiles up), 2: one flag for all
@@ -1413,8 +1413,11 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // Split-K combination of unit u of a split phase: by all the tile's
   // splits (dl_combine_dist) or by its last one (dl_combine); `next` is the
   // phase whose first weight stages a waiting split issues (0: none).
+  // `ready`: the tile's ready flag, set to `rep` once the tile is written; a
+  // tile that all its splits write counts their second arrivals on the
+  // counters from `cnt2` (phase 1: the XU tiles, phase 3: the XU_d tiles).
   auto combine = [&](const DlUnit& U, f32x4(&acc)[MT], int u, int nt, int splits, int cnt_base, bool out_y,
-                     int next, uint64_t* ready = nullptr) -> bool {
+                     int next, uint64_t* ready = nullptr, uint64_t rep = 0, int cnt2 = 0) -> bool {
     uint32_t* cnt = dl_tile_counter(p.sync, cnt_base + u % nt);
     const uint16_t* resid = out_y ? static_cast<const uint16_t*>(p.resid) : nullptr;
     if constexpr (MT >= 2) {
@@ -1424,7 +1427,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
                                      if (next == 0 || u + G < units[next - 1]) return false;
                                      prefetch_w(next);
                                      return true;
-                                   }, ready, xu_epoch, dl_tile_counter(p.sync, p.cnt2 + u % nt));
+                                   }, ready, rep, dl_tile_counter(p.sync, cnt2 + u % nt));
     }
     dl_combine<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, out_y && *bad != 0, p.sync, resid);
     if (ready && (splits == 1 || *flag)) {  // this block wrote the tile
@@ -1464,7 +1467,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     if (NORM && u == b) dl_wait_ready(p.sync, kDlRowFlag0, kDlRowFlag0 + T - 1, gen0 + 1, spin_lds ? *spin_lds : spin, bad);
     dl_run<MT, false>(c, U, NORM && u == b, acc);
     pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2,
-                   xu_epoch ? dl_ready_flag(p.sync, p.xu_flag0 + (MT == 1 ? 0 : u % nt1)) : nullptr);
+                   xu_epoch ? dl_ready_flag(p.sync, p.xu_flag0 + (MT == 1 ? 0 : u % nt1)) : nullptr, xu_epoch,
+                   p.cnt2);
   }
   dl_wait_vm<0>();
   if (xu_epoch) {
@@ -1573,14 +1577,19 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     unit_of(3, u, U);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    pre4 = combine(U, acc, u, nt3, p.splits3, nt1, false, 4);
-    if (epoch && (p.splits3 == 1 || *flag)) dl_set_ready(p.sync, u % nt3, epoch);  // this block wrote the tile
+    // from two token tiles up every split writes a share of the tile: the
+    // last of their second arrivals sets its flag
+    const bool shared = MT >= 2 && p.dist && p.splits3 > 1;
+    pre4 = combine(U, acc, u, nt3, p.splits3, nt1, false, 4,
+                   epoch && shared ? dl_ready_flag(p.sync, u % nt3) : nullptr, epoch, p.cnt2 + nt1);
+    if (epoch && !shared && (p.splits3 == 1 || *flag)) dl_set_ready(p.sync, u % nt3, epoch);  // this block wrote the tile
   }
   dl_wait_vm<0>();
-  if (epoch)
-    prefetch4();
-  else
+  if (epoch) {
+    if (!pre4) prefetch4();
+  } else {
     grid_sync(4, pre4);
+  }
   }
 
   // ---- phase 4: y = bf16(XU_d . Vd) ----

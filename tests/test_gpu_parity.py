@@ -53,12 +53,12 @@ def _contracted(shape, T, padded=False):
 def _dl_barriers(T, contracted):
     """Grid barriers of one persistent MFMA decode-layer launch on the 8B and
     test shapes (phase 1 waits for the RMSNorm rows' ready flags in the MLP
-    block): the contracted layer keeps the one before phase 2 (1; phase 4
-    waits for its XU_d tiles' ready flags); the four-phase layer at one
-    16-row token tile the one before phase 3 (1; phase 2 waits for one flag
-    for all of XU, phase 4 for its XU_d tiles' flags), from two tiles up the
-    ones before phases 3 and 4 (2; phase 2 waits for its XU tiles' flags)."""
-    return 1 if contracted or T <= 16 else 2
+    block): the contracted layer keeps the one before phase 2 (phase 4
+    waits for its XU_d tiles' ready flags); the four-phase layer the one
+    before phase 3 (phase 2 waits for one flag for all of XU at one 16-row
+    token tile, for its XU tiles' flags from two tiles up; phase 4 for its
+    XU_d tiles' flags)."""
+    return 1
 
 
 def _gemv_layer(shape, T):
