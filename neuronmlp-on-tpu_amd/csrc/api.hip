@@ -280,7 +280,7 @@ Ws ws_layout(int64_t T, int64_t d, int64_t ff, int64_t r) {
   w.g = off;
   off += dec ? 0 : a256(((T + 255) / 256 * 256) * std::max((big + 223) / 224 * 224, (big + 255) / 256 * 256) * 2);
   w.slices = off;
-  off += T <= kDlMaxT ? a256((int64_t)kDlMaxGrid * decode_layer_mt((int)T) * 2048 * 4) : 0;
+  off += T <= kDlMaxT ? a256((int64_t)dl_slice_banks(decode_layer_mt((int)T)) * kDlMaxGrid * decode_layer_mt((int)T) * 2048 * 4) : 0;
   w.need = off;
   // the contracted layer's slices: one per (XU_d tile, h strip), T rows each
   w.cslices = off;

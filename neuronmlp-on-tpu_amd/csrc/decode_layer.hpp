@@ -81,7 +81,7 @@ struct DecLayerParams {
   uint16_t* xu16;  // bf16 gate/up rank intermediates: (T, r_gu) gate, then (T, r_up) up
   uint16_t* h;     // (T, ff) bf16
   uint16_t* xd16;  // (T, r_d) bf16 down rank intermediate
-  float* slices;   // split-K partial sums, MT * 2048 floats per unit (kDlMaxGrid units)
+  float* slices;   // split-K partial sums: dl_slice_banks(MT) banks of kDlMaxGrid units, MT * 2048 floats each
   float* cslices;  // contracted layer: partial XU_d tiles, (r_d / 128, units2, T, 128) fp32
   uint64_t* sync;  // barrier words, one per 128-byte line (kDl*), then split-K tile counters
   int T, d, ff, r_gu, r_d;
@@ -129,9 +129,22 @@ struct DecLayerParams {
 };
 
 constexpr int kDlThreads = 512;
-// Largest grid: a split-K phase has at most one unit per block, so the
-// slice area holds kDlMaxGrid units.
+// Largest grid: a split-K phase has at most one unit per block, so a slice
+// bank holds kDlMaxGrid units (MT * 2048 floats each).
 constexpr int kDlMaxGrid = 256;
+// Slice banks: unit u's slice is slice u of its phase's bank.  From two
+// token tiles up phases 2 and 4 use bank 1, phases 1 and 3 bank 0: their
+// units start on ready flags (not a grid barrier) while the previous phase's
+// slices may still be read (a split sums its share after the others move
+// on), and the grid barrier before phase 3 separates every reuse of a bank.
+// At one token tile one bank: phase 2 starts on the single "XU complete"
+// flag or a grid barrier, and phase 4 also waits for the flag of the tile
+// its block's phase-3 unit stored a slice for.  (8B layer, against one bank
+// without those waits, same box: T=48 / 64 / 100 79.2 / 83.4 / 107.7 ->
+// 77.8 / 82.5 / 107.0 us; the MLP block -0.5 to -1.3 us.)
+template <int MT>
+constexpr int kDlBank24 = MT >= 2 ? 1 : 0;
+__host__ __device__ constexpr int dl_slice_banks(int mt) { return mt >= 2 ? 2 : 1; }
 constexpr int kDlWStage = 8192;    // 32 k x 128 columns bf16
 // Ring geometry by token tile: a ring stage holds KC 32-k chunks (more
 // weight bytes per block barrier) and the ring holds NS stages, as far as
@@ -240,21 +253,24 @@ __device__ __forceinline__ void dl_set_ready(uint64_t* sync, int t, uint64_t epo
   dl_set_ready(dl_ready_flag(sync, t), epoch);
 }
 
-// Bounded wait until the ready flags of tiles t0..t1 (at most 128) hold
-// `epoch`: lane i of wave 0 polls tiles t0 + i and t0 + 64 + i.  A wait that
-// gives up sets the timeout flags as a grid-barrier wait does.
+// Bounded wait until the ready flags of tiles t0..t1 (at most 128), and of
+// tile tx unless negative, hold `epoch`: lane i of wave 0 polls tiles t0 + i
+// and t0 + 64 + i, lane 0 also tx.  A wait that gives up sets the timeout
+// flags as a grid-barrier wait does.
 __device__ __forceinline__ void dl_wait_ready(uint64_t* sync, int t0, int t1, uint64_t epoch, uint32_t spin,
-                                              int* bad) {
+                                              int* bad, int tx = -1) {
   if (threadIdx.x < 64) {
     const int t = t0 + (int)threadIdx.x;
-    bool done = t > t1, done2 = t + 64 > t1;
+    bool done = t > t1, done2 = t + 64 > t1, done3 = threadIdx.x != 0 || tx < 0;
     uint32_t polls = 0;
     while (true) {
       if (!done)
         done = __hip_atomic_load(dl_ready_flag(sync, t), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
       if (!done2)
         done2 = __hip_atomic_load(dl_ready_flag(sync, t + 64), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
-      done = done && done2;
+      if (!done3)
+        done3 = __hip_atomic_load(dl_ready_flag(sync, tx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+      done = done && done2 && done3;
       if (__builtin_amdgcn_read_exec() == __ballot(done)) break;  // every lane's tile is ready
       __builtin_amdgcn_s_sleep(1);
       if (++polls >= spin) {
@@ -1416,20 +1432,22 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // `ready`: the tile's ready flag, set to `rep` once the tile is written; a
   // tile that all its splits write counts their second arrivals on the
   // counters from `cnt2` (phase 1: the XU tiles, phase 3: the XU_d tiles).
+  // `bank`: the slice bank (DlSlices) of the phase.
   auto combine = [&](const DlUnit& U, f32x4(&acc)[MT], int u, int nt, int splits, int cnt_base, bool out_y,
-                     int next, uint64_t* ready = nullptr, uint64_t rep = 0, int cnt2 = 0) -> bool {
+                     int next, int bank, uint64_t* ready = nullptr, uint64_t rep = 0, int cnt2 = 0) -> bool {
     uint32_t* cnt = dl_tile_counter(p.sync, cnt_base + u % nt);
+    float* const slices = p.slices + (size_t)bank * kDlMaxGrid * MT * 2048;
     const uint16_t* resid = out_y ? static_cast<const uint16_t*>(p.resid) : nullptr;
     if constexpr (MT >= 2) {
       if (p.dist && splits > 1)
-        return dl_combine_dist<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, bad, p.sync,
+        return dl_combine_dist<MT>(c, U, acc, u, nt, splits, cnt, slices, flag, U.dst, out_y, bad, p.sync,
                                    spin_lds ? *spin_lds : spin, resid, [&] {
                                      if (next == 0 || u + G < units[next - 1]) return false;
                                      prefetch_w(next);
                                      return true;
                                    }, ready, rep, dl_tile_counter(p.sync, cnt2 + u % nt));
     }
-    dl_combine<MT>(c, U, acc, u, nt, splits, cnt, p.slices, flag, U.dst, out_y, out_y && *bad != 0, p.sync, resid);
+    dl_combine<MT>(c, U, acc, u, nt, splits, cnt, slices, flag, U.dst, out_y, out_y && *bad != 0, p.sync, resid);
     if (ready && (splits == 1 || *flag)) {  // this block wrote the tile
       if (MT == 1 && p.xu_ready == 2) {
         // one flag for all tiles: the last writer to arrive stores it
@@ -1466,7 +1484,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     f32x4 acc[MT];
     if (NORM && u == b) dl_wait_ready(p.sync, kDlRowFlag0, kDlRowFlag0 + T - 1, gen0 + 1, spin_lds ? *spin_lds : spin, bad);
     dl_run<MT, false>(c, U, NORM && u == b, acc);
-    pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2,
+    pre2 = combine(U, acc, u, nt1, p.splits1, 0, false, 2, 0,
                    xu_epoch ? dl_ready_flag(p.sync, p.xu_flag0 + (MT == 1 ? 0 : u % nt1)) : nullptr, xu_epoch,
                    p.cnt2);
   }
@@ -1530,11 +1548,12 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       uint32_t* pcnt = dl_tile_counter(p.sync, nt1 + nt3 + nt4 + (u >> 1));
       if constexpr (MT >= 2) {
         if (p.dist) {
-          dl_swiglu_pair_dist<MT>(c, U, acc, u, pcnt, p.slices, flag, p.h, p.sync, spin_lds ? *spin_lds : spin, bad);
+          dl_swiglu_pair_dist<MT>(c, U, acc, u, pcnt, p.slices + kDlBank24<MT> * kDlMaxGrid * MT * 2048, flag, p.h,
+                                  p.sync, spin_lds ? *spin_lds : spin, bad);
           continue;
         }
       }
-      dl_swiglu_pair<MT>(c, U, acc, u, pcnt, p.slices, flag, p.h);
+      dl_swiglu_pair<MT>(c, U, acc, u, pcnt, p.slices + kDlBank24<MT> * kDlMaxGrid * MT * 2048, flag, p.h);
     }
   } else {
   // ---- phase 2: h = bf16(SiLU(XU_g . Vg) * (XU_u . Vu)) ----
@@ -1580,7 +1599,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
     // from two token tiles up every split writes a share of the tile: the
     // last of their second arrivals sets its flag
     const bool shared = MT >= 2 && p.dist && p.splits3 > 1;
-    pre4 = combine(U, acc, u, nt3, p.splits3, nt1, false, 4,
+    pre4 = combine(U, acc, u, nt3, p.splits3, nt1, false, 4, 0,
                    epoch && shared ? dl_ready_flag(p.sync, u % nt3) : nullptr, epoch, p.cnt2 + nt1);
     if (epoch && !shared && (p.splits3 == 1 || *flag)) dl_set_ready(p.sync, u % nt3, epoch);  // this block wrote the tile
   }
@@ -1602,10 +1621,16 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   for (int u = b; u < units[4]; u += G) {
     DlUnit U;
     unit_of(4, u, U);
-    if (epoch) dl_wait_ready(p.sync, U.kb / 128, (U.ke - 1) / 128, epoch, spin_lds ? *spin_lds : spin, bad);
+    // with the XU_d tiles' flags at one token tile (one slice bank), also
+    // that of the tile this block's phase-3 unit stored a slice for: its flag
+    // is set once the tile's last split has read every slice, and this
+    // unit's slice reuses slice u
+    if (epoch)
+      dl_wait_ready(p.sync, U.kb / 128, (U.ke - 1) / 128, epoch, spin_lds ? *spin_lds : spin, bad,
+                    MT == 1 && !CONTRACT && u == b && b < units[3] ? b % nt3 : -1);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
-    combine(U, acc, u, nt4, p.splits4, nt1 + nt3, true, 0);
+    combine(U, acc, u, nt4, p.splits4, nt1 + nt3, true, 0, kDlBank24<MT>);
   }
 }
 
