@@ -467,6 +467,7 @@ struct Tune {
   bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
   bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
   bool dlready3 = true; // ... also from two token tiles up (XU_d tiles written by all their splits)
+  int dlh = 1;          // decode layer: phase 3 waits for its K split's h flag (1: eight token tiles, 2: from two)
   bool dlxu = true;     // decode layer: phase 2 waits for its XU tiles' ready flags, not a grid barrier
   bool dlxu1 = true;    // decode layer at one token tile: phase 2 waits for one "XU complete" flag
   bool dlp4n = true;    // decode layer at one token tile: phase 4 as 16-column units without a K split
@@ -548,6 +549,7 @@ const Tune& tune() {
         if (k == "dlxu") r.dlxu = v != 0;
         if (k == "dlready") r.dlready = v != 0;
         if (k == "dlready3") r.dlready3 = v != 0;
+        if (k == "dlh") r.dlh = v;
         if (k == "dlpff") r.dlpff = v != 0;
       }
       pos = end + 1;
@@ -1393,6 +1395,17 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   // launch's end (the last blocks wait for its atomics), +0.35 us after phase 1.
   if (mt == 1 && !contract && tune().dlxu1 && p.xd_ready && r_d / 128 < kDlRowFlag0 && p.cnt2 < kDlMaxTiles)
     p.xu_ready = 2;
+  // Phase 3 on its K splits' h flags instead of a grid barrier, at eight
+  // token tiles (65-128 tokens): flags after the XU tiles', counters after
+  // the second-round ones of phases 1 and 3.  8B layer, padded V rows, two
+  // alternating runs: T=100 / 128 107.2 / 115.1 -> 106.4 / 113.6 us; at two
+  // and four tiles, where a split's K range spans 14 (8 splits) or 10 pairs
+  // of phase-2 units, T=17 / 32 / 48 / 64 +1.0 / +1.0 / +0.4 / -0.2 us
+  // (SVDMLP_TUNE=dlh=2 takes them there too).
+  p.hf0 = p.xu_flag0 + (int)((r_gu + r_u) / 128);
+  p.hc0 = p.cnt2 + (int)((r_gu + r_u) / 128 + r_d / 128);
+  p.h_ready = (mt >= 8 ? tune().dlh >= 1 : mt >= 2 && tune().dlh >= 2) && p.dist && p.p2split && p.xu_ready == 1 &&
+              p.hf0 + p.splits3 <= kDlRowFlag0 && p.hc0 + p.splits3 <= kDlMaxTiles;
   p.pf_full = tune().dlpff;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;

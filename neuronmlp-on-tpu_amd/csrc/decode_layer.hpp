@@ -111,6 +111,13 @@ struct DecLayerParams {
   // First of the second-round tile counters of dl_combine_dist with ready
   // flags: phase 1's XU tiles, then phase 3's XU_d tiles.
   int cnt2;
+  // Phase 3 waits for one flag per K split (flag hf0 + split), set by the
+  // last of the phase-2 units writing h columns of that split to count down
+  // on counter hc0 + split, instead of a grid barrier (eight token tiles,
+  // one-branch pairs writing h half each, per-tile XU flags); the launch's
+  // one grid-barrier generation then comes from an arrival-only barrier
+  // after phase 1.
+  int h_ready, hf0, hc0;
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
   // unit (dl_swiglu_pair_dist).
@@ -240,6 +247,24 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
     }
   }
   dl_block_sync();
+}
+
+// Arrival at grid barrier k without waiting for it: the generation still
+// advances once every block has arrived (a launch whose blocks wait on ready
+// flags only, whose epoch is the generation at launch start plus one).
+__device__ __forceinline__ void dl_grid_arrive(uint64_t* sync) {
+  if (threadIdx.x == 0) {
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t g = b % kDlGroups;
+    const uint32_t gsize = G / kDlGroups + (g < G % kDlGroups ? 1u : 0u);
+    const uint32_t ngroups = G < (uint32_t)kDlGroups ? G : (uint32_t)kDlGroups;
+    const uint64_t a = __hip_atomic_fetch_add(&sync[g * kDlLine], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((a + 1) % gsize == 0) {
+      const uint64_t r = __hip_atomic_fetch_add(&sync[kDlRoot], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((r + 1) % ngroups == 0)
+        __hip_atomic_fetch_add(&sync[kDlGen], (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // Tile t's ready flag set to `epoch` by thread 0, once every wave of the
@@ -1317,6 +1342,9 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // 1: one flag per XU tile (from two token tiles up), 2: one flag for all
   // of XU, stored by the last of the tiles' writers to count down (one tile)
   const uint64_t xu_epoch = ((MT >= 2 && p.xu_ready == 1) || (MT == 1 && !CONTRACT && p.xu_ready == 2)) ? gen0 + 1 : 0;
+  // phase 3's K splits' h flags in place of the grid barrier before phase 3
+  // (DecLayerParams::h_ready)
+  const uint64_t h_epoch = (MT >= 2 && !CONTRACT && p.h_ready && xu_epoch) ? gen0 + 1 : 0;
 
   auto unit_of = [&](int phase, int u, DlUnit& U) {
     if (phase == 1) {
@@ -1491,6 +1519,10 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   dl_wait_vm<0>();
   if (xu_epoch) {
     if (!pre2) prefetch_w(2);
+    if (h_epoch) {  // no grid barrier in this launch: arrive at one for the generation
+      ++nbar;
+      dl_grid_arrive(p.sync);
+    }
   } else {
     grid_sync(2, pre2);
   }
@@ -1550,6 +1582,21 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
         if (p.dist) {
           dl_swiglu_pair_dist<MT>(c, U, acc, u, pcnt, p.slices + kDlBank24<MT> * kDlMaxGrid * MT * 2048, flag, p.h,
                                   p.sync, spin_lds ? *spin_lds : spin, bad);
+          if (h_epoch) {
+            // count down on the phase-3 K splits whose columns this pair's h
+            // covers (both units of a pair write h); the last of a split
+            // sets its flag
+            dl_wait_vm<0>();
+            dl_block_sync();
+            if (threadIdx.x == 0) {
+              for (int s = U.n0 / p.ks3; s < p.splits3 && s * p.ks3 < U.n0 + 128; ++s) {
+                const int kb = s * p.ks3, ke = min(p.ff, kb + p.ks3);
+                if (dl_arrive_wrap(dl_tile_counter(p.sync, p.hc0 + s), 2 * ((ke - 1) / 128 - kb / 128 + 1)))
+                  __hip_atomic_store(dl_ready_flag(p.sync, p.hf0 + s), h_epoch, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+              }
+            }
+          }
           continue;
         }
       }
@@ -1587,13 +1634,17 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   }
   }
   dl_wait_vm<0>();
-  grid_sync(3);
+  if (h_epoch)
+    prefetch_w(3);
+  else
+    grid_sync(3);
 
   // ---- phase 3: XU_d = h . Ud -> bf16 XU_d ----
   bool pre4 = false;
   for (int u = b; u < units[3]; u += G) {
     DlUnit U;
     unit_of(3, u, U);
+    if (h_epoch) dl_wait_ready(p.sync, p.hf0 + u / nt3, p.hf0 + u / nt3, h_epoch, spin_lds ? *spin_lds : spin, bad);
     f32x4 acc[MT];
     dl_run<MT, false>(c, U, u == b, acc);
     // from two token tiles up every split writes a share of the tile: the

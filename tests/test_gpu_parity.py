@@ -57,7 +57,8 @@ def _dl_barriers(T, contracted):
     waits for its XU_d tiles' ready flags); the four-phase layer the one
     before phase 3 (phase 2 waits for one flag for all of XU at one 16-row
     token tile, for its XU tiles' flags from two tiles up; phase 4 for its
-    XU_d tiles' flags)."""
+    XU_d tiles' flags), at eight tiles an arrival-only one after phase 1
+    (phase 3 waits for its K split's h flag)."""
     return 1
 
 
@@ -429,6 +430,8 @@ def test_decode_activation_reads_through_the_caches(gpu, T, padded):
 
 @pytest.mark.parametrize("shape,T,contracted", [
     (inputs.LayerShape(1024, 2048, 512), 8, False),        # MFMA decode layer
+    (inputs.LayerShape(1024, 2048, 512), 48, False),       # four token tiles: XU and XU_d tiles' ready flags
+    (inputs.LayerShape(1024, 2048, 512), 100, False),      # eight tiles: phase 3 on its K splits' h flags
     (inputs.LayerShape(1040, 2064, 400, 272), 1, False),   # streaming-GEMV layer
     (inputs.LayerShape(1040, 2064, 400, 272), 2, False),   # GEMV, ragged strips
     (inputs.LayerShape(1024, 2048, 512), 4, True),         # contracted layer (asked for): tile-combine waits too
