@@ -467,6 +467,13 @@ struct Tune {
   bool dlpff = true;   // decode layer: the weight prefetch at a grid barrier fills the whole ring
   bool dlready = true;  // decode layer: phase 4 waits for its XU_d tiles' ready flags, not a grid barrier
   bool dlready3 = true; // ... also from two token tiles up (XU_d tiles written by all their splits)
+  // decode layer: a split that waits for the tile's other splits issues the
+  // next phase's first weights before its share (bit 0: phase 1, bit 1:
+  // phase 3).  Phase 1's share first: its XU flags, which phase 2 waits for,
+  // are not queued behind 48 KB of DMAs per CU (8B layer, two alternating
+  // runs, 3 -> 2: T=64 82.2-82.3 -> 81.8-81.9, T=128 113.6-113.7 -> 112.9 us;
+  // phase 3's share first as well (0): no better)
+  int dlpre = 2;
   int dlh = 1;          // decode layer: phase 3 waits for its K split's h flag (1: eight token tiles, 2: from two)
   bool dlxu = true;     // decode layer: phase 2 waits for its XU tiles' ready flags, not a grid barrier
   bool dlxu1 = true;    // decode layer at one token tile: phase 2 waits for one "XU complete" flag
@@ -550,6 +557,7 @@ const Tune& tune() {
         if (k == "dlready") r.dlready = v != 0;
         if (k == "dlready3") r.dlready3 = v != 0;
         if (k == "dlh") r.dlh = v;
+        if (k == "dlpre") r.dlpre = v;
         if (k == "dlpff") r.dlpff = v != 0;
       }
       pos = end + 1;
@@ -1407,6 +1415,7 @@ int decode_layer(const Common& c, const void* x, const void* ug, const void* vg,
   p.h_ready = (mt >= 8 ? tune().dlh >= 1 : mt >= 2 && tune().dlh >= 2) && p.dist && p.p2split && p.xu_ready == 1 &&
               p.hf0 + p.splits3 <= kDlRowFlag0 && p.hc0 + p.splits3 <= kDlMaxTiles;
   p.pf_full = tune().dlpff;
+  p.pre_wait = tune().dlpre;
   p.ld_u = (int)ld.u;
   p.ld_v = (int)ld.v;
   p.ld_uu = (int)(ld.uu ? ld.uu : ld.u);

@@ -118,6 +118,10 @@ struct DecLayerParams {
   // one grid-barrier generation then comes from an arrival-only barrier
   // after phase 1.
   int h_ready, hf0, hc0;
+  // dl_combine_dist: a split that waits for the others issues the next
+  // phase's first weight stages before it waits (bit 0: phase 1, bit 1:
+  // phase 3), else once its share of the tile is written
+  int pre_wait;
   // Token tiles of 32 rows and more: split-K tiles combined by all their
   // splits (dl_combine_dist), the phase-2 pairs' h written half by each
   // unit (dl_swiglu_pair_dist).
@@ -1470,7 +1474,8 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
       if (p.dist && splits > 1)
         return dl_combine_dist<MT>(c, U, acc, u, nt, splits, cnt, slices, flag, U.dst, out_y, bad, p.sync,
                                    spin_lds ? *spin_lds : spin, resid, [&] {
-                                     if (next == 0 || u + G < units[next - 1]) return false;
+                                     if (next == 0 || u + G < units[next - 1] || !((p.pre_wait >> (next == 2 ? 0 : 1)) & 1))
+                                       return false;
                                      prefetch_w(next);
                                      return true;
                                    }, ready, rep, dl_tile_counter(p.sync, cnt2 + u % nt));
