@@ -253,9 +253,12 @@ __device__ __forceinline__ void dl_grid_sync(uint64_t* sync, uint64_t gen0, uint
   dl_block_sync();
 }
 
-// Arrival at grid barrier k without waiting for it: the generation still
-// advances once every block has arrived (a launch whose blocks wait on ready
-// flags only, whose epoch is the generation at launch start plus one).
+// Arrival at the launch's next grid barrier without waiting for it (the
+// caller counts it in its barrier number): the generation still advances once
+// every block has arrived.  For a launch whose blocks wait on ready flags
+// only, whose epoch is the generation at launch start plus one: no block's
+// read of that generation can see this launch's advance, which needs its own
+// arrival.
 __device__ __forceinline__ void dl_grid_arrive(uint64_t* sync) {
   if (threadIdx.x == 0) {
     const uint32_t G = gridDim.x, b = blockIdx.x;
