@@ -116,6 +116,9 @@ def _stage_work(T):
                           "big_gemm_kernel XUg.Vg -> bf16 g"),
         "gate_up_xuv_swiglu": (2.0 * T * R * FF, 2 * (T * R + R * FF + 2 * T * FF),
                                "big_gemm_kernel XUu.Vu, SiLU(g)*u epilogue"),
+        "gate_up_xuv_dual": (2 * 2.0 * T * R * FF, 2 * (2 * T * R + 2 * R * FF + T * FF),
+                             "big_gemm_kernel, one launch: every block XUg.Vg -> bf16 g, then XUu.Vu with the "
+                             "SiLU(g)*u epilogue (g's round trip not counted)"),
         "down_xu": (2.0 * T * FF * R, 2 * (T * FF + FF * R + T * R),
                     "big_gemm_kernel h.Ud (split-K fp32 slices)"),
         "down_xuv": (2.0 * T * R * D, 2 * (T * R + R * D + T * D),
@@ -702,7 +705,7 @@ def main(argv=None) -> int:
                 "avg_launch_us": round(dom_ms * 1e3, 2) if dom_ms else None,
             },
             "stages_us": {k: round(v * 1e3, 2) for k, v in stages.items()},
-            # per layer: the split-K reductions ("finalize") run three times per layer
+            # per layer: a stage may take more than one launch per layer (the split-K reductions, "finalize")
             "stages_us_per_layer": {k: round(v[0] / args.steps * 1e3, 2) for k, v in prof.result.items()},
             "ms_per_step_with_stage_events": round(ms_prof, 4),
             "step_us_p10_p50_p90": [round(pct(0.1), 1), round(pct(0.5), 1), round(pct(0.9), 1)],

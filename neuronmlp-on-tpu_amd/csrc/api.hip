@@ -97,12 +97,14 @@ enum Stage : int {
   ST_DEC_CONTRACT,
   ST_QUANT,
   ST_D_XU_F8,
+  ST_GU_XUV_DUAL,
   ST_COUNT
 };
 const char* const kStageNames[ST_COUNT] = {
     "zero_fill",        "gate_up_xu",       "gate_up_xuv_swiglu", "down_xu",           "down_xuv",
     "decode_gate_up_xu", "decode_gate_up_xuv", "decode_down_xu",   "decode_down_xuv", "finalize",
-    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer",  "decode_layer_contracted", "quant_h_e4m3", "down_xu_fp8"
+    "gate_up_xuv_g",    "decode_layer",       "decode_gemv_layer",  "decode_layer_contracted", "quant_h_e4m3", "down_xu_fp8",
+    "gate_up_xuv_dual"
 };
 
 struct Profiler {
@@ -449,6 +451,7 @@ struct Tune {
   bool f8tail = true;  // fp8 x fp8 h.Ud: whole rounds of tiles without a split, K splits for the rest only
   bool xutail = true;  // gate/up X.U with 1-2 rounds of tiles: one round without a split, the rest split
   bool gufuse = true;  // split gate/up XU.V passes: one reduction from both passes' slices
+  bool gudual = true;  // unsplit gate/up XU.V passes in one launch (each block its g tile, then its u tile)
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -538,6 +541,7 @@ const Tune& tune() {
         if (k == "f8tail") r.f8tail = v != 0;
         if (k == "xutail") r.xutail = v != 0;
         if (k == "gufuse") r.gufuse = v != 0;
+        if (k == "gudual") r.gudual = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -596,12 +600,21 @@ struct Entry1 {
   int64_t ldb, ldo, b_bytes;
 };
 
+// The second pass of a BEPI_GU_DUAL launch (entry 1: XU_u . Vu): its A
+// pitch and bytes, K, and B pitch and bytes.
+struct DualEntry {
+  int64_t lda, a_bytes;
+  int K;
+  int64_t ldb, b_bytes;
+};
+
 int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
              const void* b0, const void* b1, int64_t ldb, int64_t b_bytes, bool b_kc, int M, int N, int K, int batch,
              int fn, int epi, int k_split, void* out, int64_t ldo, int64_t out_bstride, const uint16_t* gmem,
              bool out_f32 = false, int64_t out_sstride = 0, const float* s0 = nullptr, const float* s1 = nullptr,
              int gfrag = 0, int out_frag = 0, const Entry1* e1 = nullptr, const uint16_t* resid = nullptr,
-             int kg = 1, int out_blk = 0, int a_blk = 0, int tile0 = 0, int tiles = 0) {
+             int kg = 1, int out_blk = 0, int a_blk = 0, int tile0 = 0, int tiles = 0,
+             const DualEntry* du = nullptr) {
   BigParams p{};
   p.tile0 = tile0;
   p.tiles = tiles;
@@ -642,6 +655,20 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
     p.nt0 = p.ntiles;
     p.ntiles += (e1->N + 32 * fn - 1) / (32 * fn);
     batch = 1;
+  }
+  if (du) {  // BEPI_GU_DUAL: entry 1 is the second pass of every block
+    if (epi != BEPI_GU_DUAL || batch != 1 || e1 || k_split < std::max(K, du->K) || tiles)
+      return fail("large-tile GEMM: a dual gate/up launch takes one batch entry, no K split, no tile range");
+    p.lda1 = du->lda;
+    p.a_bytes[1] = (uint32_t)du->a_bytes;
+    p.K1 = du->K;
+    p.ldb[1] = du->ldb;
+    p.b_bytes[1] = (uint32_t)du->b_bytes;
+    p.ldo[1] = ldo;
+    p.N[1] = N;
+    p.out_bstride = 0;
+  } else if (epi == BEPI_GU_DUAL) {
+    return fail("large-tile GEMM: a dual gate/up launch needs its second entry");
   }
   p.k_split = k_split;
   const int splits = (K + k_split - 1) / k_split;
@@ -1039,6 +1066,14 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
                                          big_nw(fn, BEPI_STORE, v_lin), 1, c.st, fused ? nullptr : gbuf, nullptr, 1,
                                          fused ? part : nullptr, fused ? splits : 0),
                  "split-K SwiGLU reduce");
+  }
+  if (tune().gudual && (fn == 7 || fn == 8) && !v_lin) {
+    // both passes in one launch: each block its g tile, then its u tile
+    const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes};
+    if (want_blk) *h_blk = true;
+    return big_gemm(c, ST_GU_XUV_DUAL, xu_g, xu_u, r, xu_bytes, vg, vu, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
+                    BEPI_GU_DUAL, std::max(r, r_u), out, ff, 0, gbuf, false, 0, s_vg, s_vu, 1, 0, nullptr, nullptr, 1,
+                    want_blk ? 1 : 0, 0, 0, 0, &du);
   }
   int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r,
                     1, fn, BEPI_STORE_FRAG, r, gbuf, ff, 0, nullptr, false, 0, s_vg);

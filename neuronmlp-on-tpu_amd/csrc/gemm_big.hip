@@ -51,6 +51,13 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
     case BEPI_STORE_FRAG:
       if constexpr (FN != 6) return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
       break;
+    case BEPI_GU_DUAL:  // natural-layout B (bf16 or fp8), 8 waves
+      if constexpr (FN == 7 || FN == 8) {
+        if (!d.b_kc && d.nw == 8)
+          return d.fp8 ? go<FN, false, BEPI_GU_DUAL, false, true>(p, splits, batch, st)
+                       : go<FN, false, BEPI_GU_DUAL>(p, splits, batch, st);
+      }
+      break;
     default: break;
   }
   *why = "big GEMM: unsupported epilogue for this tile";

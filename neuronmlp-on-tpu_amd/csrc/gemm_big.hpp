@@ -36,6 +36,8 @@
 // youngest stages landed" is the constant wait vmcnt(8).
 #pragma once
 
+#include <type_traits>
+
 #include "gemm.hpp"
 
 namespace svdmlp {
@@ -186,7 +188,11 @@ __device__ __forceinline__ int f8nat_swz(int k) { return (k & 7) | (((k >> 3) & 
 // store (and the SwiGLU epilogue's matching load, with p.gfrag) moves one
 // contiguous 512-byte piece.  Padded tiles are written too (zeros): the
 // buffer holds mtiles * 256 x ntiles * BN elements.
-enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2, BEPI_STORE_FRAG = 3 };
+// BEPI_GU_DUAL: the gate/up XU.V passes of one tile in one block, entry 0
+// (XU_g . Vg, bf16 g stored to gmem in fragment order) then entry 1 (XU_u .
+// Vu, SwiGLU epilogue reading those gate values back): one launch instead of
+// two, the same arithmetic.
+enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2, BEPI_STORE_FRAG = 3, BEPI_GU_DUAL = 4 };
 
 struct BigParams {
   const void* a[2];  // per batch entry
@@ -211,6 +217,8 @@ struct BigParams {
   int out_frag;          // fp32 output (split-K slices) in fragment order, padded tiles included
   int M, K;
   int N[2];    // output columns per batch entry
+  int K1;      // BEPI_GU_DUAL: entry 1's K (the up rank; K is the gate rank)
+  int64_t lda1;  // BEPI_GU_DUAL: entry 1's A row pitch (elements)
   int mtiles, ntiles;
   // 0: the batch entry is blockIdx.z and both entries have ntiles column
   // tiles; > 0: the grid's z is 1, entry 0 has the first nt0 of the ntiles
@@ -248,6 +256,7 @@ struct BigCfg {
   static constexpr int FM = BM / (WT / 2) / 16, FN = FN_;  // per wave: 16*FM x 16*FN
   static constexpr bool B_KC = B_KC_;
   static constexpr int EPI = EPI_;
+  static constexpr bool DUAL = EPI_ == BEPI_GU_DUAL;
   static constexpr bool OUT_F32 = OUT_F32_;
   // fp8 e4m3fn B in natural layout: 1-byte elements staged as they lie in
   // HBM, widened to bf16 after the transposing LDS read.
@@ -312,11 +321,15 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     zb = 1;
     nt -= p.nt0;
   }
+  // One pass: the tile's k-loop over batch entry zb (K = Kp) and the
+  // epilogue EP; a BEPI_GU_DUAL block runs two (below).
+  auto run_pass = [&](const int zb, const int Kp, auto epi_c) {
+  constexpr int EP = decltype(epi_c)::value;
   const int n0 = nt * BN;
   const int N = p.N[zb];
   const int64_t ldb = p.ldb[zb], ldo = p.ldo[zb];
   const int kbeg = split * p.k_split;
-  const int kend = min(p.K, kbeg + p.k_split);
+  const int kend = min(Kp, kbeg + p.k_split);
   const int nk = (kend - kbeg + BK - 1) / BK;
 
   const int tid = threadIdx.x;
@@ -330,7 +343,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
 
   const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
   const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
-  const uint32_t lda2 = (uint32_t)p.lda * 2u, ldb2 = (uint32_t)ldb * 2u;
+  const uint32_t lda2 = (uint32_t)(C::DUAL && zb ? p.lda1 : p.lda) * 2u, ldb2 = (uint32_t)ldb * 2u;
   const uint32_t lbase = lds_addr(lds);
 
   // ---- per-lane DMA geometry (constant along K) ----
@@ -351,7 +364,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   for (int i = 0; i < C::A_UNITS; ++i) {
     const int row = m0 + a_row0 + (C::KG == 1 ? 16 * NW * i : 0);
     if (p.a_blk) {  // block (row / 16, k / 16), row % 16, k % 16 (k = a_kk within the stage)
-      const uint32_t blk = (uint32_t)(row >> 4) * (uint32_t)(p.K >> 4) + (uint32_t)(a_kk >> 4);
+      const uint32_t blk = (uint32_t)(row >> 4) * (uint32_t)(Kp >> 4) + (uint32_t)(a_kk >> 4);
       a_voff[i] = row < p.M ? (blk * 256u + (uint32_t)(row & 15) * 16u + (uint32_t)(a_kk & 15)) * 2u : kOOB;
     } else {
       a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
@@ -584,9 +597,9 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   }
 
   // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
-  const size_t esz = (C::OUT_F32 || C::EPI == BEPI_ATOMIC) ? 4 : 2;
+  const size_t esz = (C::OUT_F32 || EP == BEPI_ATOMIC) ? 4 : 2;
   char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
-  constexpr bool FRAG = C::EPI == BEPI_STORE_FRAG;
+  constexpr bool FRAG = EP == BEPI_STORE_FRAG;
   // fp32 split-K slices in fragment order: every lane's 16 bytes of a
   // fragment are contiguous with its neighbours' (the row-major stores write
   // 16 rows x 64 bytes per instruction; 8B layer: epilogue 9.1K -> 6K cycles)
@@ -600,8 +613,8 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // h store (the stores could alias the loads as far as the compiler knows,
   // which would serialise one load round trip per fragment); the main
   // loop's fragment registers are free by now.
-  u32x2 gv[C::EPI == BEPI_SWIGLU_MEM ? FM : 1][C::EPI == BEPI_SWIGLU_MEM ? FN : 1];
-  if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
+  u32x2 gv[EP == BEPI_SWIGLU_MEM ? FM : 1][EP == BEPI_SWIGLU_MEM ? FN : 1];
+  if constexpr (EP == BEPI_SWIGLU_MEM) {
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int m = m0 + wm0 + 16 * i + lr;
@@ -633,12 +646,13 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         if (n < N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
       const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
       if constexpr (FRAG) {
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + fo) =
+        // (a dual block's gate values go to gmem, its own buffer)
+        *reinterpret_cast<u32x2*>((C::DUAL ? const_cast<uint16_t*>(p.gmem) : reinterpret_cast<uint16_t*>(p.out)) + fo) =
             u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
         continue;
       }
       const int64_t o = (int64_t)m * ldo + n;
-      if constexpr (C::EPI == BEPI_ATOMIC) {
+      if constexpr (EP == BEPI_ATOMIC) {
         float* op = reinterpret_cast<float*>(outp) + o;
         unsafeAtomicAdd(op + 0, v.x);
         unsafeAtomicAdd(op + 1, v.y);
@@ -646,7 +660,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         unsafeAtomicAdd(op + 3, v.w);
       } else if constexpr (C::OUT_F32) {
         *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + (ffrag ? fo : o)) = v;
-      } else if constexpr (C::EPI == BEPI_SWIGLU_MEM) {
+      } else if constexpr (EP == BEPI_SWIGLU_MEM) {
         const u32x2 g = gv[i][j];
         const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
         const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
@@ -660,6 +674,18 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) = ov;
       }
     }
+  }
+  };
+  if constexpr (C::DUAL) {
+    run_pass(0, p.K, std::integral_constant<int, BEPI_STORE_FRAG>{});
+    // every wave's LDS reads of the first pass are complete before the
+    // second pass's first DMAs refill the ring; its gate-value stores are
+    // read back by the same lanes
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    run_pass(1, p.K1, std::integral_constant<int, BEPI_SWIGLU_MEM>{});
+  } else {
+    run_pass(zb, p.K, std::integral_constant<int, C::EPI>{});
   }
 }
 

@@ -835,6 +835,44 @@ def test_gate_up_split_tail(gpu, ranks):
     assert np.array_equal(got, _np(ops.svd_mlp(*t)))  # replays are bitwise identical
 
 
+# The gate/up XU.V passes above 512 tokens run as one launch (every block its
+# g tile, then its u tile, reading its own gate values back): the bits of the
+# two-launch form, which SVDMLP_TUNE=gudual=0 (read once per process) keeps,
+# computed in a child process on the same seeded inputs.  256 x 224 tiles
+# (ff a multiple of 224) and 256 x 256 with distinct gate and up ranks.
+_DUAL_CHILD = """
+import sys, numpy as np, torch
+sys.path[:0] = sys.argv[1].split("|")
+from svdmlp import inputs, ops
+d, ff, rg, ru, rd, T, seed = (int(a) for a in sys.argv[2:9])
+rng = np.random.default_rng(seed)
+f = [inputs.random_matrix(rng, a, b) for a, b in ((d, rg), (rg, ff), (d, ru), (ru, ff), (ff, rd), (rd, d))]
+t = [inputs.to_torch(a, torch.bfloat16, torch.device("cuda:0")) for a in (inputs.make_x(rng, T, d), *f)]
+np.save(sys.argv[9], ops.svd_mlp(*t).view(torch.int16).cpu().numpy())
+"""
+
+
+@pytest.mark.parametrize("T,d,ff,ranks", [(600, 1024, 3584, (512, 512, 384)), (700, 1024, 4096, (384, 640, 256)),
+                                          (1000, 2048, 4096, (768, 768, 512))])
+def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks):
+    import os
+    import subprocess
+    import sys
+
+    r_g, r_u, r_d = ranks
+    seed = 1700 + T
+    rng = np.random.default_rng(seed)
+    f = [inputs.random_matrix(rng, a, b) for a, b in ((d, r_g), (r_g, ff), (d, r_u), (r_u, ff), (ff, r_d), (r_d, d))]
+    t = [inputs.to_torch(a, torch.bfloat16, gpu) for a in (inputs.make_x(rng, T, d), *f)]
+    got = ops.svd_mlp(*t).view(torch.int16).cpu().numpy()
+    out = tmp_path / "two_launch.npy"
+    env = dict(os.environ, SVDMLP_TUNE="gudual=0")
+    paths = "|".join(p for p in sys.path if p)
+    subprocess.run([sys.executable, "-c", _DUAL_CHILD, paths, *map(str, (d, ff, r_g, r_u, r_d, T, seed)), str(out)],
+                   env=env, check=True, timeout=120)
+    assert np.array_equal(got, np.load(out)), (T, d, ff, ranks)
+
+
 def test_distinct_gate_up_ranks_fp8(gpu):
     T, d, ff, r_g, r_u, r_d = 300, 1024, 2048, 512, 256, 384
     xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 950)
