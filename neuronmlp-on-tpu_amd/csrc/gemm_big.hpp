@@ -324,357 +324,357 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
   // One pass: the tile's k-loop over batch entry zb (K = Kp) and the
   // epilogue EP; a BEPI_GU_DUAL block runs two (below).
   auto run_pass = [&](const int zb, const int Kp, auto epi_c) {
-  constexpr int EP = decltype(epi_c)::value;
-  const int n0 = nt * BN;
-  const int N = p.N[zb];
-  const int64_t ldb = p.ldb[zb], ldo = p.ldo[zb];
-  const int kbeg = split * p.k_split;
-  const int kend = min(Kp, kbeg + p.k_split);
-  const int nk = (kend - kbeg + BK - 1) / BK;
+    constexpr int EP = decltype(epi_c)::value;
+    const int n0 = nt * BN;
+    const int N = p.N[zb];
+    const int64_t ldb = p.ldb[zb], ldo = p.ldo[zb];
+    const int kbeg = split * p.k_split;
+    const int kend = min(Kp, kbeg + p.k_split);
+    const int nk = (kend - kbeg + BK - 1) / BK;
 
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int lr = lane & 15, lg = lane >> 4;
-  // wave tile wt of the block; K group kg (0 with KG = 1)
-  constexpr int WT = C::WT;
-  const int wt = wave % WT, kg = wave / WT;
-  const int wm0 = (wt >> 1) * (16 * FM);
-  const int wn0 = (wt & 1) * (BN / 2);
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int lr = lane & 15, lg = lane >> 4;
+    // wave tile wt of the block; K group kg (0 with KG = 1)
+    constexpr int WT = C::WT;
+    const int wt = wave % WT, kg = wave / WT;
+    const int wm0 = (wt >> 1) * (16 * FM);
+    const int wn0 = (wt & 1) * (BN / 2);
 
-  const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
-  const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
-  const uint32_t lda2 = (uint32_t)(C::DUAL && zb ? p.lda1 : p.lda) * 2u, ldb2 = (uint32_t)ldb * 2u;
-  const uint32_t lbase = lds_addr(lds);
+    const i32x4 ra = make_rsrc_sgpr(p.a[zb], p.a_bytes[zb]);
+    const i32x4 rb = make_rsrc_sgpr(p.b[zb], p.b_bytes[zb]);
+    const uint32_t lda2 = (uint32_t)(C::DUAL && zb ? p.lda1 : p.lda) * 2u, ldb2 = (uint32_t)ldb * 2u;
+    const uint32_t lbase = lds_addr(lds);
 
-  // ---- per-lane DMA geometry (constant along K) ----
-  // The lane's byte offset without the stage's k (which goes into the
-  // instruction's scalar offset), or kOOB for rows / columns outside the
-  // matrix.  K and the split length are whole 32-k stages, so a stage lies
-  // either below kend or wholly past it; stages past it (the pipeline's
-  // run-out) use a descriptor with no records and fetch zeros.
-  // A: instruction i of this wave fills LDS rows 16*(wave + NW*i) + lane/4;
-  // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row).  With K groups
-  // the A region of a stage is KG sub-tiles of BM = 128 rows (16 * NW), one
-  // per 32-k half: instruction i fills rows 16*wave + lane/4 of half i.
-  const i32x4 r_none = make_rsrc_sgpr(p.a[zb], 0);
-  const int a_row0 = 16 * wave + (lane >> 2);
-  const int a_kk = 8 * ((lane & 3) ^ a_swz(a_row0));  // k within the stage
-  uint32_t a_voff[C::A_UNITS];
+    // ---- per-lane DMA geometry (constant along K) ----
+    // The lane's byte offset without the stage's k (which goes into the
+    // instruction's scalar offset), or kOOB for rows / columns outside the
+    // matrix.  K and the split length are whole 32-k stages, so a stage lies
+    // either below kend or wholly past it; stages past it (the pipeline's
+    // run-out) use a descriptor with no records and fetch zeros.
+    // A: instruction i of this wave fills LDS rows 16*(wave + NW*i) + lane/4;
+    // slot lane%4 holds logical chunk (lane%4) ^ a_swz(row).  With K groups
+    // the A region of a stage is KG sub-tiles of BM = 128 rows (16 * NW), one
+    // per 32-k half: instruction i fills rows 16*wave + lane/4 of half i.
+    const i32x4 r_none = make_rsrc_sgpr(p.a[zb], 0);
+    const int a_row0 = 16 * wave + (lane >> 2);
+    const int a_kk = 8 * ((lane & 3) ^ a_swz(a_row0));  // k within the stage
+    uint32_t a_voff[C::A_UNITS];
 #pragma unroll
-  for (int i = 0; i < C::A_UNITS; ++i) {
-    const int row = m0 + a_row0 + (C::KG == 1 ? 16 * NW * i : 0);
-    if (p.a_blk) {  // block (row / 16, k / 16), row % 16, k % 16 (k = a_kk within the stage)
-      const uint32_t blk = (uint32_t)(row >> 4) * (uint32_t)(Kp >> 4) + (uint32_t)(a_kk >> 4);
-      a_voff[i] = row < p.M ? (blk * 256u + (uint32_t)(row & 15) * 16u + (uint32_t)(a_kk & 15)) * 2u : kOOB;
-    } else {
-      a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
-    }
-  }
-  // B natural: instruction i fills LDS k-row 2*(wave + NW*i) + lane/32, slot
-  // lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
-  // B Linear: like A with rows n.
-  uint32_t b_voff[C::B_UNITS];
-  if constexpr (C::B_KC) {
-    const int row0 = 16 * wave + (lane >> 2);
-    const int kk = 8 * ((lane & 3) ^ a_swz(row0));
-#pragma unroll
-    for (int i = 0; i < C::B_UNITS; ++i) {
-      const int row = row0 + 16 * NW * i;
-      b_voff[i] = (row < BN && n0 + row < N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
-    }
-  } else if constexpr (C::FP8_B) {
-    // fp8 natural: instruction i fills k-rows 4*(wave + NW*i) + lane/16
-    // (256 bytes each); slot lane%16 holds logical 16-byte chunk
-    // (lane%16) ^ f8nat_swz(row), i.e. columns 16 * that chunk .. +15.
-#pragma unroll
-    for (int i = 0; i < C::B_UNITS; ++i) {
-      const int kk = 4 * (wave + NW * i) + (lane >> 4);
-      const int col = 16 * ((lane & 15) ^ f8nat_swz(kk));
-      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * (uint32_t)ldb + (uint32_t)(n0 + col) : kOOB;
-    }
-  } else if constexpr (C::B_PITCH == 384) {
-    // 384-byte rows: instruction i fills bytes (wave + NW*i) KB .. +1 KB of
-    // the stage's B tile; the lane's 16 bytes are half (byte >> 4) & 1 of
-    // physical unit byte >> 5 of row byte_pos / 384
-#pragma unroll
-    for (int i = 0; i < C::B_UNITS; ++i) {
-      const int pos = (wave + NW * i) * 1024 + 16 * lane;
-      const int kk = pos / 384, byte = pos % 384;
-      const int col = 16 * ((byte >> 5) ^ b384_swz(kk)) + 8 * ((byte >> 4) & 1);
-      b_voff[i] = n0 + col < N ? (uint32_t)kk * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
-    }
-  } else {
-    // instruction i fills RPI k-rows from RPI * (wave + NW * i), LPR lanes per
-    // row (512-byte rows: 2 rows of 32 lanes; 256-byte rows: 4 of 16)
-    // (with 4 waves and 512-byte rows the rows of successive instructions
-    // differ by 8, which changes bnat_swz: one column per instruction)
-    constexpr int RPI = 1024 / C::B_PITCH, LPR = C::B_PITCH / 16;
-    const int q = lane % LPR;
-#pragma unroll
-    for (int i = 0; i < C::B_UNITS; ++i) {
-      const int kk = RPI * (wave + NW * i) + lane / LPR;
-      const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
-      b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
-    }
-  }
-
-  // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
-  auto dma_one = [&](int kt, int s, int d) {
-    const int k0 = kbeg + kt * BK;
-    const bool live = k0 < kend;  // uniform
-    if (d < C::A_UNITS) {
-      // k0 * 2 bytes along a row-major row, k0 * 32 (two 512-byte blocks per 32 k) in block-major A
-      const uint32_t kshift = p.a_blk ? 5u : 1u;
-      const uint32_t ksub = C::KG == 2 ? (uint32_t)(d * 32) << kshift : 0u;  // 32-k half of the stage (bytes)
-      dma16(live ? ra : r_none, a_voff[d], ((uint32_t)k0 << kshift) + ksub, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
-    } else {
-      const int i = d - C::A_UNITS;
-      const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)ldb : (uint32_t)k0 * ldb2);
-      dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + NW * i) * 1024);
-    }
-  };
-  constexpr int NDMA = C::A_UNITS + C::B_UNITS;
-
-  // ---- fragment read addresses (constant over stages) ----
-  // A: rows wm0 + 16i + lr share one swizzle; fragment i of stage s is at
-  // a_rd + s * A_BYTES + 1 KB * i.
-  const lds_cptr l0 = (lds_cptr)lds;
-  // K group kg reads its 32-k half: A sub-tile kg, B k-rows 32*kg ..
-  const lds_cptr a_rd = l0 + kg * C::A_SUB + (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
-  // B natural: the lane reads k rows k_lo = 8*lg + lr/4 (and k_lo + 4 for
-  // the upper half, same swizzle) in 32-byte unit U = wn0/16 + j for
-  // fragment j, stored at unit U ^ bnat_swz(k_lo): fragment j of stage s is
-  // at b_rd[j] + s * B_BYTES (+ 2 KB for the upper half).
-  // B Linear: like A, fragment j of stage s at b_rd[0] + s * B_BYTES + 1 KB * j.
-  lds_cptr b_rd[FN];
-  if constexpr (C::B_KC) {
-    const int row0 = wn0 + lr;
-    b_rd[0] = l0 + B_REGION + row0 * 64 + ((lg ^ a_swz(row0)) << 4);
-  } else {
-    const int k_lo = 8 * lg + (lr >> 2);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int u = (wn0 >> 4) + j;
-      const int pu = C::B_PITCH == 384 ? (u ^ b384_swz(k_lo)) : (u ^ bnat_swz(k_lo));
-      b_rd[j] = l0 + B_REGION + (kg * 32 + k_lo) * C::B_PITCH + (pu << 5) + ((lr & 3) << 3);
-    }
-  }
-  // fp8 B: lane s = lr of group lg points at k-row 8*lg + lr/2, bytes
-  // 8*(lr & 1) of 16-byte chunk c = wn0/16 + j (fragment j's 16 columns),
-  // stored at chunk c ^ f8nat_swz(row); one base per fragment.
-  lds_cptr b8[C::FP8_B ? FN : 1];
-  if constexpr (C::FP8_B) {
-    const int row = 8 * lg + (lr >> 1);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int cc = (wn0 >> 4) + j;
-      b8[j] = l0 + B_REGION + row * C::B_PITCH + ((cc ^ f8nat_swz(row)) << 4) + ((lr & 1) << 3);
-    }
-  }
-
-  f32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Fragment registers: A as one 16-byte read per 16-row block; B as two
-  // 8-byte halves (k rows 0-3 and 4-7 of each lane's 8) so that natural and
-  // Linear layouts share one schedule (a Linear fragment is one 16-byte
-  // read split across the pair).
-  struct Frags {
-    u32x4 a[FM];
-    u32x2 b[2 * FN];
-  };
-  // Read number r of stage slot s's fragments: A blocks first, then B.
-  auto read_one = [&](int s, int r, Frags& f) {
-    if (r < FM) {
-      f.a[r] = lds_read_b128(a_rd + s * C::A_BYTES + 1024 * r);
-    } else if constexpr (C::FP8_B) {
-      f.b[r - FM] = lds_read_tr8(b8[r - FM] + s * C::B_BYTES);
-    } else if constexpr (C::B_KC) {
-      const u32x4 v = lds_read_b128(b_rd[0] + s * C::B_BYTES + 1024 * (r - FM));
-      f.b[2 * (r - FM)] = u32x2{v.x, v.y};
-      f.b[2 * (r - FM) + 1] = u32x2{v.z, v.w};
-    } else {
-      const int j = (r - FM) >> 1, hi = (r - FM) & 1;
-      f.b[2 * j + hi] = lds_read_tr(b_rd[j] + s * C::B_BYTES + hi * 4 * C::B_PITCH);
-    }
-  };
-  constexpr int NREAD = FM + ((C::B_KC || C::FP8_B) ? FN : 2 * FN);
-  // fp8 B: fragment j widened to bf16 once per step (fbw[j]), interleaved
-  // with the first FN MFMAs, which are the first to use them.
-  u32x4 fbw[C::FP8_B ? FN : 1];
-  auto mfma_one = [&](int m, const Frags& f) {
-    const int i = m / FN, j = m % FN;
-    if constexpr (C::FP8_B) {
-      if (m < FN) fbw[j] = fp8x8_to_bf16x8(f.b[j]);
-      acc[i][j] = mfma_chunk(fbw[j], f.a[i], acc[i][j], __bf16{});
-    } else {
-      const u32x2 lo = f.b[2 * j], hi = f.b[2 * j + 1];
-      acc[i][j] = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, f.a[i], acc[i][j], __bf16{});
-    }
-  };
-
-  // Stage kt sits in slot kt % NS.  Step kt runs the MFMAs of stage kt
-  // (fragments already in registers, read in step kt-1) and, interleaved
-  // one per MFMA so that no wave holds its MFMAs behind a burst of memory
-  // instructions:
-  //  * the fragment reads of stage kt+1;
-  //  * the DMA of stage kt+NS into slot kt % NS, free since every wave's
-  //    reads of stage kt completed before the barrier that ended step kt-1.
-  // Then it waits until stage kt+2 landed (stages kt+3 .. kt+NS may still be
-  // in flight: (NS-2) * NDMA instructions) and meets the other waves at the
-  // barrier.  DMAs past kend fetch zeros and keep the per-wave count
-  // constant.  The sched_barriers pin this instruction order.
-  Frags f0, f1;
-  constexpr int NMFMA = FM * FN;
-  static_assert(NREAD <= NMFMA && NDMA <= NMFMA / 2, "one fragment read per MFMA slot");
-  auto step = [&](int kt, int s, const Frags& cur, Frags& nxt) {
-#pragma unroll
-    for (int m = 0; m < NMFMA; ++m) {
-      if (m < NREAD) read_one((s + 1) % NS, m, nxt);
-#pragma unroll
-      for (int d = 0; d < NDMA; ++d)
-        if (m == d * NMFMA / NDMA + 1) dma_one(kt + NS, s, d);
-      mfma_one(m, cur);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    wait_dma<(NS - 2) * NDMA>();
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  if (nk > 0) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int d = 0; d < NDMA; ++d) dma_one(s, s, d);
-    wait_dma<(NS - 2) * NDMA>();  // stages 0 and 1 landed
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < NREAD; ++r) read_one(0, r, f0);
-    __syncthreads();  // every wave holds stage 0 before step 0 refills its slot
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // unrolled over the slot cycle and the f0/f1 alternation
-  constexpr int UNROLL = NS % 2 ? 2 * NS : NS;
-  for (int kt = 0; kt < nk; kt += UNROLL) {
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      if (kt + u < nk) {
-        if (u % 2 == 0)
-          step(kt + u, u % NS, f0, f1);
-        else
-          step(kt + u, u % NS, f1, f0);
+    for (int i = 0; i < C::A_UNITS; ++i) {
+      const int row = m0 + a_row0 + (C::KG == 1 ? 16 * NW * i : 0);
+      if (p.a_blk) {  // block (row / 16, k / 16), row % 16, k % 16 (k = a_kk within the stage)
+        const uint32_t blk = (uint32_t)(row >> 4) * (uint32_t)(Kp >> 4) + (uint32_t)(a_kk >> 4);
+        a_voff[i] = row < p.M ? (blk * 256u + (uint32_t)(row & 15) * 16u + (uint32_t)(a_kk & 15)) * 2u : kOOB;
+      } else {
+        a_voff[i] = row < p.M ? (uint32_t)row * lda2 + (uint32_t)(a_kk * 2) : kOOB;
       }
     }
-  }
-  wait_dma<0>();  // drain DMAs of stages past the end before the block exits
+    // B natural: instruction i fills LDS k-row 2*(wave + NW*i) + lane/32, slot
+    // lane%32 -> logical column 16*((slot/2) ^ swz(row)) + 8*(slot%2).
+    // B Linear: like A with rows n.
+    uint32_t b_voff[C::B_UNITS];
+    if constexpr (C::B_KC) {
+      const int row0 = 16 * wave + (lane >> 2);
+      const int kk = 8 * ((lane & 3) ^ a_swz(row0));
+#pragma unroll
+      for (int i = 0; i < C::B_UNITS; ++i) {
+        const int row = row0 + 16 * NW * i;
+        b_voff[i] = (row < BN && n0 + row < N) ? (uint32_t)(n0 + row) * ldb2 + (uint32_t)(kk * 2) : kOOB;
+      }
+    } else if constexpr (C::FP8_B) {
+      // fp8 natural: instruction i fills k-rows 4*(wave + NW*i) + lane/16
+      // (256 bytes each); slot lane%16 holds logical 16-byte chunk
+      // (lane%16) ^ f8nat_swz(row), i.e. columns 16 * that chunk .. +15.
+#pragma unroll
+      for (int i = 0; i < C::B_UNITS; ++i) {
+        const int kk = 4 * (wave + NW * i) + (lane >> 4);
+        const int col = 16 * ((lane & 15) ^ f8nat_swz(kk));
+        b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * (uint32_t)ldb + (uint32_t)(n0 + col) : kOOB;
+      }
+    } else if constexpr (C::B_PITCH == 384) {
+      // 384-byte rows: instruction i fills bytes (wave + NW*i) KB .. +1 KB of
+      // the stage's B tile; the lane's 16 bytes are half (byte >> 4) & 1 of
+      // physical unit byte >> 5 of row byte_pos / 384
+#pragma unroll
+      for (int i = 0; i < C::B_UNITS; ++i) {
+        const int pos = (wave + NW * i) * 1024 + 16 * lane;
+        const int kk = pos / 384, byte = pos % 384;
+        const int col = 16 * ((byte >> 5) ^ b384_swz(kk)) + 8 * ((byte >> 4) & 1);
+        b_voff[i] = n0 + col < N ? (uint32_t)kk * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+      }
+    } else {
+      // instruction i fills RPI k-rows from RPI * (wave + NW * i), LPR lanes per
+      // row (512-byte rows: 2 rows of 32 lanes; 256-byte rows: 4 of 16)
+      // (with 4 waves and 512-byte rows the rows of successive instructions
+      // differ by 8, which changes bnat_swz: one column per instruction)
+      constexpr int RPI = 1024 / C::B_PITCH, LPR = C::B_PITCH / 16;
+      const int q = lane % LPR;
+#pragma unroll
+      for (int i = 0; i < C::B_UNITS; ++i) {
+        const int kk = RPI * (wave + NW * i) + lane / LPR;
+        const int col = 16 * ((q >> 1) ^ bnat_swz(kk)) + 8 * (q & 1);
+        b_voff[i] = (col < BN && n0 + col < N) ? (uint32_t)kk * ldb2 + (uint32_t)((n0 + col) * 2) : kOOB;
+      }
+    }
 
-  // K groups: add the two groups' sums.  Group g finishes fragment rows
-  // [g * FM/2, (g+1) * FM/2) of its wave tile: it stores the other half to
-  // LDS (1 KB per fragment, lane-contiguous) for its partner wave (same wave
-  // tile, other group) and adds the partner's half of its own rows.  fp32
-  // addition commutes, so both sides of a pair compute the same bits.
-  if constexpr (C::KG == 2) {
-    constexpr int H = FM / 2;
-    __syncthreads();  // every wave's reads of the last stages are done
-    SVDMLP_LDS char* const lw = (SVDMLP_LDS char*)lds;
-    SVDMLP_LDS char* const xw = lw + ((wt * 2 + kg) * H * FN) * 1024 + 16 * lane;  // this wave's outgoing half
-    const lds_cptr xr = l0 + ((wt * 2 + (kg ^ 1)) * H * FN) * 1024 + 16 * lane;     // the partner's
+    // DMA instruction d (0, 1: A; 2, 3: B) of stage kt into LDS stage slot s.
+    auto dma_one = [&](int kt, int s, int d) {
+      const int k0 = kbeg + kt * BK;
+      const bool live = k0 < kend;  // uniform
+      if (d < C::A_UNITS) {
+        // k0 * 2 bytes along a row-major row, k0 * 32 (two 512-byte blocks per 32 k) in block-major A
+        const uint32_t kshift = p.a_blk ? 5u : 1u;
+        const uint32_t ksub = C::KG == 2 ? (uint32_t)(d * 32) << kshift : 0u;  // 32-k half of the stage (bytes)
+        dma16(live ? ra : r_none, a_voff[d], ((uint32_t)k0 << kshift) + ksub, lbase + s * C::A_BYTES + (wave + NW * d) * 1024);
+      } else {
+        const int i = d - C::A_UNITS;
+        const uint32_t soff = C::B_KC ? (uint32_t)k0 * 2u : (C::FP8_B ? (uint32_t)k0 * (uint32_t)ldb : (uint32_t)k0 * ldb2);
+        dma16(live ? rb : r_none, b_voff[i], soff, lbase + B_REGION + s * C::B_BYTES + (wave + NW * i) * 1024);
+      }
+    };
+    constexpr int NDMA = C::A_UNITS + C::B_UNITS;
+
+    // ---- fragment read addresses (constant over stages) ----
+    // A: rows wm0 + 16i + lr share one swizzle; fragment i of stage s is at
+    // a_rd + s * A_BYTES + 1 KB * i.
+    const lds_cptr l0 = (lds_cptr)lds;
+    // K group kg reads its 32-k half: A sub-tile kg, B k-rows 32*kg ..
+    const lds_cptr a_rd = l0 + kg * C::A_SUB + (wm0 + lr) * 64 + ((lg ^ a_swz(wm0 + lr)) << 4);
+    // B natural: the lane reads k rows k_lo = 8*lg + lr/4 (and k_lo + 4 for
+    // the upper half, same swizzle) in 32-byte unit U = wn0/16 + j for
+    // fragment j, stored at unit U ^ bnat_swz(k_lo): fragment j of stage s is
+    // at b_rd[j] + s * B_BYTES (+ 2 KB for the upper half).
+    // B Linear: like A, fragment j of stage s at b_rd[0] + s * B_BYTES + 1 KB * j.
+    lds_cptr b_rd[FN];
+    if constexpr (C::B_KC) {
+      const int row0 = wn0 + lr;
+      b_rd[0] = l0 + B_REGION + row0 * 64 + ((lg ^ a_swz(row0)) << 4);
+    } else {
+      const int k_lo = 8 * lg + (lr >> 2);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int u = (wn0 >> 4) + j;
+        const int pu = C::B_PITCH == 384 ? (u ^ b384_swz(k_lo)) : (u ^ bnat_swz(k_lo));
+        b_rd[j] = l0 + B_REGION + (kg * 32 + k_lo) * C::B_PITCH + (pu << 5) + ((lr & 3) << 3);
+      }
+    }
+    // fp8 B: lane s = lr of group lg points at k-row 8*lg + lr/2, bytes
+    // 8*(lr & 1) of 16-byte chunk c = wn0/16 + j (fragment j's 16 columns),
+    // stored at chunk c ^ f8nat_swz(row); one base per fragment.
+    lds_cptr b8[C::FP8_B ? FN : 1];
+    if constexpr (C::FP8_B) {
+      const int row = 8 * lg + (lr >> 1);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int cc = (wn0 >> 4) + j;
+        b8[j] = l0 + B_REGION + row * C::B_PITCH + ((cc ^ f8nat_swz(row)) << 4) + ((lr & 1) << 3);
+      }
+    }
+
+    f32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        if ((i / H) != kg) *reinterpret_cast<SVDMLP_LDS f32x4*>(xw + ((i % H) * FN + j) * 1024) = acc[i][j];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        if ((i / H) == kg) acc[i][j] += *reinterpret_cast<const SVDMLP_LDS f32x4*>(xr + ((i % H) * FN + j) * 1024);
-  }
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
-  const size_t esz = (C::OUT_F32 || EP == BEPI_ATOMIC) ? 4 : 2;
-  char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
-  constexpr bool FRAG = EP == BEPI_STORE_FRAG;
-  // fp32 split-K slices in fragment order: every lane's 16 bytes of a
-  // fragment are contiguous with its neighbours' (the row-major stores write
-  // 16 rows x 64 bytes per instruction; 8B layer: epilogue 9.1K -> 6K cycles)
-  const bool ffrag = C::OUT_F32 && p.out_frag;
-  // fragment-order element offset of this lane's block (0, 0): tiles in
-  // (m-tile, column tile) order per batch entry, or, in a tile-range launch,
-  // the launch's tiles in order from its first (entries included, out_bstride 0)
-  const int64_t ftl = C::TR && p.tiles > 0 ? (int64_t)(t - p.tile0) : (int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN);
-  const int64_t frag0 = ((ftl * WT + wt) * FM * FN) * 256 + 4 * lane;
-  // SwiGLU: every gate value of the wave's tile is loaded before the first
-  // h store (the stores could alias the loads as far as the compiler knows,
-  // which would serialise one load round trip per fragment); the main
-  // loop's fragment registers are free by now.
-  u32x2 gv[EP == BEPI_SWIGLU_MEM ? FM : 1][EP == BEPI_SWIGLU_MEM ? FN : 1];
-  if constexpr (EP == BEPI_SWIGLU_MEM) {
+    // Fragment registers: A as one 16-byte read per 16-row block; B as two
+    // 8-byte halves (k rows 0-3 and 4-7 of each lane's 8) so that natural and
+    // Linear layouts share one schedule (a Linear fragment is one 16-byte
+    // read split across the pair).
+    struct Frags {
+      u32x4 a[FM];
+      u32x2 b[2 * FN];
+    };
+    // Read number r of stage slot s's fragments: A blocks first, then B.
+    auto read_one = [&](int s, int r, Frags& f) {
+      if (r < FM) {
+        f.a[r] = lds_read_b128(a_rd + s * C::A_BYTES + 1024 * r);
+      } else if constexpr (C::FP8_B) {
+        f.b[r - FM] = lds_read_tr8(b8[r - FM] + s * C::B_BYTES);
+      } else if constexpr (C::B_KC) {
+        const u32x4 v = lds_read_b128(b_rd[0] + s * C::B_BYTES + 1024 * (r - FM));
+        f.b[2 * (r - FM)] = u32x2{v.x, v.y};
+        f.b[2 * (r - FM) + 1] = u32x2{v.z, v.w};
+      } else {
+        const int j = (r - FM) >> 1, hi = (r - FM) & 1;
+        f.b[2 * j + hi] = lds_read_tr(b_rd[j] + s * C::B_BYTES + hi * 4 * C::B_PITCH);
+      }
+    };
+    constexpr int NREAD = FM + ((C::B_KC || C::FP8_B) ? FN : 2 * FN);
+    // fp8 B: fragment j widened to bf16 once per step (fbw[j]), interleaved
+    // with the first FN MFMAs, which are the first to use them.
+    u32x4 fbw[C::FP8_B ? FN : 1];
+    auto mfma_one = [&](int m, const Frags& f) {
+      const int i = m / FN, j = m % FN;
+      if constexpr (C::FP8_B) {
+        if (m < FN) fbw[j] = fp8x8_to_bf16x8(f.b[j]);
+        acc[i][j] = mfma_chunk(fbw[j], f.a[i], acc[i][j], __bf16{});
+      } else {
+        const u32x2 lo = f.b[2 * j], hi = f.b[2 * j + 1];
+        acc[i][j] = mfma_chunk(u32x4{lo.x, lo.y, hi.x, hi.y}, f.a[i], acc[i][j], __bf16{});
+      }
+    };
+
+    // Stage kt sits in slot kt % NS.  Step kt runs the MFMAs of stage kt
+    // (fragments already in registers, read in step kt-1) and, interleaved
+    // one per MFMA so that no wave holds its MFMAs behind a burst of memory
+    // instructions:
+    //  * the fragment reads of stage kt+1;
+    //  * the DMA of stage kt+NS into slot kt % NS, free since every wave's
+    //    reads of stage kt completed before the barrier that ended step kt-1.
+    // Then it waits until stage kt+2 landed (stages kt+3 .. kt+NS may still be
+    // in flight: (NS-2) * NDMA instructions) and meets the other waves at the
+    // barrier.  DMAs past kend fetch zeros and keep the per-wave count
+    // constant.  The sched_barriers pin this instruction order.
+    Frags f0, f1;
+    constexpr int NMFMA = FM * FN;
+    static_assert(NREAD <= NMFMA && NDMA <= NMFMA / 2, "one fragment read per MFMA slot");
+    auto step = [&](int kt, int s, const Frags& cur, Frags& nxt) {
+#pragma unroll
+      for (int m = 0; m < NMFMA; ++m) {
+        if (m < NREAD) read_one((s + 1) % NS, m, nxt);
+#pragma unroll
+        for (int d = 0; d < NDMA; ++d)
+          if (m == d * NMFMA / NDMA + 1) dma_one(kt + NS, s, d);
+        mfma_one(m, cur);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      wait_dma<(NS - 2) * NDMA>();
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    if (nk > 0) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int d = 0; d < NDMA; ++d) dma_one(s, s, d);
+      wait_dma<(NS - 2) * NDMA>();  // stages 0 and 1 landed
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < NREAD; ++r) read_one(0, r, f0);
+      __syncthreads();  // every wave holds stage 0 before step 0 refills its slot
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // unrolled over the slot cycle and the f0/f1 alternation
+    constexpr int UNROLL = NS % 2 ? 2 * NS : NS;
+    for (int kt = 0; kt < nk; kt += UNROLL) {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        if (kt + u < nk) {
+          if (u % 2 == 0)
+            step(kt + u, u % NS, f0, f1);
+          else
+            step(kt + u, u % NS, f1, f0);
+        }
+      }
+    }
+    wait_dma<0>();  // drain DMAs of stages past the end before the block exits
+
+    // K groups: add the two groups' sums.  Group g finishes fragment rows
+    // [g * FM/2, (g+1) * FM/2) of its wave tile: it stores the other half to
+    // LDS (1 KB per fragment, lane-contiguous) for its partner wave (same wave
+    // tile, other group) and adds the partner's half of its own rows.  fp32
+    // addition commutes, so both sides of a pair compute the same bits.
+    if constexpr (C::KG == 2) {
+      constexpr int H = FM / 2;
+      __syncthreads();  // every wave's reads of the last stages are done
+      SVDMLP_LDS char* const lw = (SVDMLP_LDS char*)lds;
+      SVDMLP_LDS char* const xw = lw + ((wt * 2 + kg) * H * FN) * 1024 + 16 * lane;  // this wave's outgoing half
+      const lds_cptr xr = l0 + ((wt * 2 + (kg ^ 1)) * H * FN) * 1024 + 16 * lane;     // the partner's
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          if ((i / H) != kg) *reinterpret_cast<SVDMLP_LDS f32x4*>(xw + ((i % H) * FN + j) * 1024) = acc[i][j];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          if ((i / H) == kg) acc[i][j] += *reinterpret_cast<const SVDMLP_LDS f32x4*>(xr + ((i % H) * FN + j) * 1024);
+    }
+
+    // ---- epilogue: lane holds D[n = 4*lg + t][m = lr] of each 16x16 block ----
+    const size_t esz = (C::OUT_F32 || EP == BEPI_ATOMIC) ? 4 : 2;
+    char* outp = reinterpret_cast<char*>(p.out) + ((int64_t)zb * p.out_bstride + (int64_t)split * p.out_sstride) * esz;
+    constexpr bool FRAG = EP == BEPI_STORE_FRAG;
+    // fp32 split-K slices in fragment order: every lane's 16 bytes of a
+    // fragment are contiguous with its neighbours' (the row-major stores write
+    // 16 rows x 64 bytes per instruction; 8B layer: epilogue 9.1K -> 6K cycles)
+    const bool ffrag = C::OUT_F32 && p.out_frag;
+    // fragment-order element offset of this lane's block (0, 0): tiles in
+    // (m-tile, column tile) order per batch entry, or, in a tile-range launch,
+    // the launch's tiles in order from its first (entries included, out_bstride 0)
+    const int64_t ftl = C::TR && p.tiles > 0 ? (int64_t)(t - p.tile0) : (int64_t)(m0 / BM) + (int64_t)p.mtiles * (n0 / BN);
+    const int64_t frag0 = ((ftl * WT + wt) * FM * FN) * 256 + 4 * lane;
+    // SwiGLU: every gate value of the wave's tile is loaded before the first
+    // h store (the stores could alias the loads as far as the compiler knows,
+    // which would serialise one load round trip per fragment); the main
+    // loop's fragment registers are free by now.
+    u32x2 gv[EP == BEPI_SWIGLU_MEM ? FM : 1][EP == BEPI_SWIGLU_MEM ? FN : 1];
+    if constexpr (EP == BEPI_SWIGLU_MEM) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int m = m0 + wm0 + 16 * i + lr;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int n = n0 + wn0 + 16 * j + 4 * lg;
+          // Unconditional loads (fragment order covers the padded tile; a
+          // row-major g is read at a clamped in-bounds address) so that all of
+          // them issue before the first store: a load under a branch left a
+          // vmcnt(0) per fragment, which also waited for every earlier h store.
+          const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
+          const bool in = m < p.M && n < N;
+          const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (in ? (int64_t)m * ldo + n : 0)));
+          gv[i][j] = in ? g : u32x2{0u, 0u};
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+      if (C::KG == 2 && (i / (FM / 2)) != kg) continue;  // the partner wave's rows
       const int m = m0 + wm0 + 16 * i + lr;
+      if (!FRAG && !ffrag && m >= p.M) continue;
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int n = n0 + wn0 + 16 * j + 4 * lg;
-        // Unconditional loads (fragment order covers the padded tile; a
-        // row-major g is read at a clamped in-bounds address) so that all of
-        // them issue before the first store: a load under a branch left a
-        // vmcnt(0) per fragment, which also waited for every earlier h store.
+        if (!FRAG && !ffrag && n >= N) continue;  // N % 8 == 0: n < N implies n + 3 < N
+        f32x4 v = acc[i][j];
+        if constexpr (C::FP8_B)
+          if (n < N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
         const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
-        const bool in = m < p.M && n < N;
-        const u32x2 g = *reinterpret_cast<const u32x2*>(p.gmem + (p.gfrag ? fo : (in ? (int64_t)m * ldo + n : 0)));
-        gv[i][j] = in ? g : u32x2{0u, 0u};
+        if constexpr (FRAG) {
+          // (a dual block's gate values go to gmem, its own buffer)
+          uint16_t* const fout = C::DUAL ? const_cast<uint16_t*>(p.gmem) : reinterpret_cast<uint16_t*>(p.out);
+          *reinterpret_cast<u32x2*>(fout + fo) = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+          continue;
+        }
+        const int64_t o = (int64_t)m * ldo + n;
+        if constexpr (EP == BEPI_ATOMIC) {
+          float* op = reinterpret_cast<float*>(outp) + o;
+          unsafeAtomicAdd(op + 0, v.x);
+          unsafeAtomicAdd(op + 1, v.y);
+          unsafeAtomicAdd(op + 2, v.z);
+          unsafeAtomicAdd(op + 3, v.w);
+        } else if constexpr (C::OUT_F32) {
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + (ffrag ? fo : o)) = v;
+        } else if constexpr (EP == BEPI_SWIGLU_MEM) {
+          const u32x2 g = gv[i][j];
+          const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
+          const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
+          const int64_t ob = p.out_blk ? (((int64_t)(m >> 4) * (N >> 4) + (n >> 4)) * 256 + (m & 15) * 16 + (n & 15)) : o;
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + ob) =
+              u32x2{pack_bf16x2(silu_f32(g0) * v.x, silu_f32(g1) * v.y),
+                    pack_bf16x2(silu_f32(g2) * v.z, silu_f32(g3) * v.w)};
+        } else {
+          u32x2 ov = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+          if (p.resid) ov = add_bf16x4(*reinterpret_cast<const u32x2*>(p.resid + o), ov);
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) = ov;
+        }
       }
     }
-  }
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    if (C::KG == 2 && (i / (FM / 2)) != kg) continue;  // the partner wave's rows
-    const int m = m0 + wm0 + 16 * i + lr;
-    if (!FRAG && !ffrag && m >= p.M) continue;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int n = n0 + wn0 + 16 * j + 4 * lg;
-      if (!FRAG && !ffrag && n >= N) continue;  // N % 8 == 0: n < N implies n + 3 < N
-      f32x4 v = acc[i][j];
-      if constexpr (C::FP8_B)
-        if (n < N) v *= *reinterpret_cast<const f32x4*>(p.scale[zb] + n);  // per-column dequant
-      const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
-      if constexpr (FRAG) {
-        // (a dual block's gate values go to gmem, its own buffer)
-        *reinterpret_cast<u32x2*>((C::DUAL ? const_cast<uint16_t*>(p.gmem) : reinterpret_cast<uint16_t*>(p.out)) + fo) =
-            u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
-        continue;
-      }
-      const int64_t o = (int64_t)m * ldo + n;
-      if constexpr (EP == BEPI_ATOMIC) {
-        float* op = reinterpret_cast<float*>(outp) + o;
-        unsafeAtomicAdd(op + 0, v.x);
-        unsafeAtomicAdd(op + 1, v.y);
-        unsafeAtomicAdd(op + 2, v.z);
-        unsafeAtomicAdd(op + 3, v.w);
-      } else if constexpr (C::OUT_F32) {
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(outp) + (ffrag ? fo : o)) = v;
-      } else if constexpr (EP == BEPI_SWIGLU_MEM) {
-        const u32x2 g = gv[i][j];
-        const float g0 = bf16_bits_to_f32(g.x & 0xffffu), g1 = bf16_bits_to_f32(g.x >> 16);
-        const float g2 = bf16_bits_to_f32(g.y & 0xffffu), g3 = bf16_bits_to_f32(g.y >> 16);
-        const int64_t ob = p.out_blk ? (((int64_t)(m >> 4) * (N >> 4) + (n >> 4)) * 256 + (m & 15) * 16 + (n & 15)) : o;
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + ob) =
-            u32x2{pack_bf16x2(silu_f32(g0) * v.x, silu_f32(g1) * v.y),
-                  pack_bf16x2(silu_f32(g2) * v.z, silu_f32(g3) * v.w)};
-      } else {
-        u32x2 ov = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
-        if (p.resid) ov = add_bf16x4(*reinterpret_cast<const u32x2*>(p.resid + o), ov);
-        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(outp) + o) = ov;
-      }
-    }
-  }
   };
   if constexpr (C::DUAL) {
     run_pass(0, p.K, std::integral_constant<int, BEPI_STORE_FRAG>{});
