@@ -1467,7 +1467,7 @@ __global__ __launch_bounds__(kDlThreads, 1) void decode_layer_kernel(DecLayerPar
   // `ready`: the tile's ready flag, set to `rep` once the tile is written; a
   // tile that all its splits write counts their second arrivals on the
   // counters from `cnt2` (phase 1: the XU tiles, phase 3: the XU_d tiles).
-  // `bank`: the slice bank (DlSlices) of the phase.
+  // `bank`: the phase's slice bank (kDlBank24 for phases 2 and 4, else 0).
   auto combine = [&](const DlUnit& U, f32x4(&acc)[MT], int u, int nt, int splits, int cnt_base, bool out_y,
                      int next, int bank, uint64_t* ready = nullptr, uint64_t rep = 0, int cnt2 = 0) -> bool {
     uint32_t* cnt = dl_tile_counter(p.sync, cnt_base + u % nt);
