@@ -451,7 +451,7 @@ struct Tune {
   bool f8tail = true;  // fp8 x fp8 h.Ud: whole rounds of tiles without a split, K splits for the rest only
   bool xutail = true;  // gate/up X.U with 1-2 rounds of tiles: one round without a split, the rest split
   bool gufuse = true;  // split gate/up XU.V passes: one reduction from both passes' slices
-  bool gudual = true;  // unsplit gate/up XU.V passes in one launch (each block its g tile, then its u tile)
+  bool gudual = true;  // gate/up XU.V passes in one launch (each block its g tile or split, then its u one)
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -600,12 +600,13 @@ struct Entry1 {
   int64_t ldb, ldo, b_bytes;
 };
 
-// The second pass of a BEPI_GU_DUAL launch (entry 1: XU_u . Vu): its A
-// pitch and bytes, K, and B pitch and bytes.
+// The second pass of a dual launch (entry 1: XU_u . Vu): its A pitch and
+// bytes, K, B pitch and bytes, and (BEPI_DUAL_F32) K per split.
 struct DualEntry {
   int64_t lda, a_bytes;
   int K;
   int64_t ldb, b_bytes;
+  int k_split = 0;
 };
 
 int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t lda, int64_t a_bytes,
@@ -656,9 +657,14 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
     p.ntiles += (e1->N + 32 * fn - 1) / (32 * fn);
     batch = 1;
   }
-  if (du) {  // BEPI_GU_DUAL: entry 1 is the second pass of every block
-    if (epi != BEPI_GU_DUAL || batch != 1 || e1 || k_split < std::max(K, du->K) || tiles)
-      return fail("large-tile GEMM: a dual gate/up launch takes one batch entry, no K split, no tile range");
+  if (du) {  // dual launches: entry 1 is the second pass of every block
+    const bool f32 = epi == BEPI_DUAL_F32;
+    if ((epi != BEPI_GU_DUAL && !f32) || batch != 1 || e1 || tiles)
+      return fail("large-tile GEMM: a dual gate/up launch takes one batch entry and no tile range");
+    if (f32 ? (du->k_split <= 0 || (K + k_split - 1) / k_split != (du->K + du->k_split - 1) / du->k_split)
+            : k_split < std::max(K, du->K))
+      return fail("large-tile GEMM: a dual launch's passes take the same K splits (none with the SwiGLU epilogue)");
+    p.k_split1 = du->k_split;
     p.lda1 = du->lda;
     p.a_bytes[1] = (uint32_t)du->a_bytes;
     p.K1 = du->K;
@@ -666,8 +672,8 @@ int big_gemm(const Common& c, int stage, const void* a0, const void* a1, int64_t
     p.b_bytes[1] = (uint32_t)du->b_bytes;
     p.ldo[1] = ldo;
     p.N[1] = N;
-    p.out_bstride = 0;
-  } else if (epi == BEPI_GU_DUAL) {
+    if (!f32) p.out_bstride = 0;
+  } else if (epi == BEPI_GU_DUAL || epi == BEPI_DUAL_F32) {
     return fail("large-tile GEMM: a dual gate/up launch needs its second entry");
   }
   p.k_split = k_split;
@@ -1049,16 +1055,27 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
     // trip fewer); else g is reduced to bf16 before the u pass reuses the area.
     const bool fused = tune().gufuse && (int64_t)(splits + splits_u) * per * 4 <= part_cap;
     float* upart = fused ? part + (int64_t)splits * per : part;
-    int rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
-                      BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
-    if (rc) return rc;
-    if (!fused) {
-      StageScope fin(ST_FINALIZE, c.st);
-      if ((rc = check(launch_reduce_bf16(part, splits, per, gbuf, per, c.st), "split-K reduce"))) return rc;
+    int rc;
+    if (fused && tune().gudual && splits == splits_u && !v_lin) {
+      // both passes' slices from one launch: every block its g split, then
+      // its u split of the same tile
+      const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes, ks_u};
+      rc = big_gemm(c, ST_GU_XUV_DUAL, xu_g, xu_u, r, xu_bytes, vg, vu, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
+                    BEPI_DUAL_F32, ks, part, ff, (int64_t)splits * per, nullptr, true, per, s_vg, s_vu, 0, 1, nullptr,
+                    nullptr, 1, 0, 0, 0, 0, &du);
+      if (rc) return rc;
+    } else {
+      rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
+                    BEPI_STORE, ks, part, ff, per, nullptr, true, per, s_vg, nullptr, 0, 1);
+      if (rc) return rc;
+      if (!fused) {
+        StageScope fin(ST_FINALIZE, c.st);
+        if ((rc = check(launch_reduce_bf16(part, splits, per, gbuf, per, c.st), "split-K reduce"))) return rc;
+      }
+      rc = big_gemm(c, ST_GU_XUV, xu_u, nullptr, r_u, xuu_bytes, vu, nullptr, ldb_u, vu_bytes, v_lin, T, ff, r_u, 1,
+                    fn, BEPI_STORE, ks_u, upart, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
+      if (rc) return rc;
     }
-    rc = big_gemm(c, ST_GU_XUV, xu_u, nullptr, r_u, xuu_bytes, vu, nullptr, ldb_u, vu_bytes, v_lin, T, ff, r_u, 1, fn,
-                  BEPI_STORE, ks_u, upart, ff, per, nullptr, true, per, s_vu, nullptr, 0, 1);
-    if (rc) return rc;
     StageScope fin(ST_FINALIZE, c.st);
     const int mt = (T + 255) / 256;
     return check(launch_reduce_frag_bf16(upart, splits_u, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff,
@@ -1067,7 +1084,7 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
                                          fused ? part : nullptr, fused ? splits : 0),
                  "split-K SwiGLU reduce");
   }
-  if (tune().gudual && (fn == 7 || fn == 8) && !v_lin) {
+  if (tune().gudual && (fn == 4 || fn == 7 || fn == 8) && !v_lin) {
     // both passes in one launch: each block its g tile, then its u tile
     const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes};
     if (want_blk) *h_blk = true;

@@ -52,10 +52,17 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
       if constexpr (FN != 6) return go_b<FN, BEPI_STORE_FRAG>(d, p, splits, batch, st);
       break;
     case BEPI_GU_DUAL:  // natural-layout B (bf16 or fp8), 8 waves
-      if constexpr (FN == 7 || FN == 8) {
+      if constexpr (FN == 4 || FN == 7 || FN == 8) {
         if (!d.b_kc && d.nw == 8)
           return d.fp8 ? go<FN, false, BEPI_GU_DUAL, false, true>(p, splits, batch, st)
-                       : go<FN, false, BEPI_GU_DUAL>(p, splits, batch, st);
+                       : go<FN, false, BEPI_GU_DUAL, false, false, 8, FN == 4 ? 6 : 4>(p, splits, batch, st);
+      }
+      break;
+    case BEPI_DUAL_F32:  // the split passes' fp32 slices; natural-layout B, 8 waves
+      if constexpr (FN == 4 || FN == 8) {
+        if (!d.b_kc && d.nw == 8 && d.out_f32)
+          return d.fp8 ? go<FN, false, BEPI_DUAL_F32, true, true>(p, splits, batch, st)
+                       : go<FN, false, BEPI_DUAL_F32, true, false, 8, FN == 4 ? 6 : 4>(p, splits, batch, st);
       }
       break;
     default: break;

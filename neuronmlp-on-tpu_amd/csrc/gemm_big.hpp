@@ -191,8 +191,17 @@ __device__ __forceinline__ int f8nat_swz(int k) { return (k & 7) | (((k >> 3) & 
 // BEPI_GU_DUAL: the gate/up XU.V passes of one tile in one block, entry 0
 // (XU_g . Vg, bf16 g stored to gmem in fragment order) then entry 1 (XU_u .
 // Vu, SwiGLU epilogue reading those gate values back): one launch instead of
-// two, the same arithmetic.
-enum BigEpi : int { BEPI_STORE = 0, BEPI_ATOMIC = 1, BEPI_SWIGLU_MEM = 2, BEPI_STORE_FRAG = 3, BEPI_GU_DUAL = 4 };
+// two, the same arithmetic.  BEPI_DUAL_F32: the same two passes of one tile
+// and K split, each storing its fp32 split-K slice (fragment order; entry 1's
+// slices out_bstride elements after entry 0's).
+enum BigEpi : int {
+  BEPI_STORE = 0,
+  BEPI_ATOMIC = 1,
+  BEPI_SWIGLU_MEM = 2,
+  BEPI_STORE_FRAG = 3,
+  BEPI_GU_DUAL = 4,
+  BEPI_DUAL_F32 = 5
+};
 
 struct BigParams {
   const void* a[2];  // per batch entry
@@ -217,8 +226,9 @@ struct BigParams {
   int out_frag;          // fp32 output (split-K slices) in fragment order, padded tiles included
   int M, K;
   int N[2];    // output columns per batch entry
-  int K1;      // BEPI_GU_DUAL: entry 1's K (the up rank; K is the gate rank)
-  int64_t lda1;  // BEPI_GU_DUAL: entry 1's A row pitch (elements)
+  int K1;      // dual launches: entry 1's K (the up rank; K is the gate rank)
+  int64_t lda1;  // dual launches: entry 1's A row pitch (elements)
+  int k_split1;  // BEPI_DUAL_F32: entry 1's K per split (its split count is entry 0's)
   int mtiles, ntiles;
   // 0: the batch entry is blockIdx.z and both entries have ntiles column
   // tiles; > 0: the grid's z is 1, entry 0 has the first nt0 of the ntiles
@@ -256,7 +266,7 @@ struct BigCfg {
   static constexpr int FM = BM / (WT / 2) / 16, FN = FN_;  // per wave: 16*FM x 16*FN
   static constexpr bool B_KC = B_KC_;
   static constexpr int EPI = EPI_;
-  static constexpr bool DUAL = EPI_ == BEPI_GU_DUAL;
+  static constexpr bool DUAL = EPI_ == BEPI_GU_DUAL || EPI_ == BEPI_DUAL_F32;
   static constexpr bool OUT_F32 = OUT_F32_;
   // fp8 e4m3fn B in natural layout: 1-byte elements staged as they lie in
   // HBM, widened to bf16 after the transposing LDS read.
@@ -328,8 +338,9 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     const int n0 = nt * BN;
     const int N = p.N[zb];
     const int64_t ldb = p.ldb[zb], ldo = p.ldo[zb];
-    const int kbeg = split * p.k_split;
-    const int kend = min(Kp, kbeg + p.k_split);
+    const int ksp = C::EPI == BEPI_DUAL_F32 && zb ? p.k_split1 : p.k_split;
+    const int kbeg = split * ksp;
+    const int kend = min(Kp, kbeg + ksp);
     const int nk = (kend - kbeg + BK - 1) / BK;
 
     const int tid = threadIdx.x;
@@ -647,7 +658,7 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
         const int64_t fo = frag0 + (int64_t)(i * FN + j) * 256;
         if constexpr (FRAG) {
           // (a dual block's gate values go to gmem, its own buffer)
-          uint16_t* const fout = C::DUAL ? const_cast<uint16_t*>(p.gmem) : reinterpret_cast<uint16_t*>(p.out);
+          uint16_t* const fout = C::EPI == BEPI_GU_DUAL ? const_cast<uint16_t*>(p.gmem) : reinterpret_cast<uint16_t*>(p.out);
           *reinterpret_cast<u32x2*>(fout + fo) = u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
           continue;
         }
@@ -677,13 +688,14 @@ __global__ __launch_bounds__(C::THREADS, 1) void big_gemm_kernel(BigParams p) {
     }
   };
   if constexpr (C::DUAL) {
-    run_pass(0, p.K, std::integral_constant<int, BEPI_STORE_FRAG>{});
+    constexpr bool F = C::EPI == BEPI_DUAL_F32;
+    run_pass(0, p.K, std::integral_constant<int, F ? BEPI_STORE : BEPI_STORE_FRAG>{});
     // every wave's LDS reads of the first pass are complete before the
     // second pass's first DMAs refill the ring; its gate-value stores are
     // read back by the same lanes
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __syncthreads();
-    run_pass(1, p.K1, std::integral_constant<int, BEPI_SWIGLU_MEM>{});
+    run_pass(1, p.K1, std::integral_constant<int, F ? BEPI_STORE : BEPI_SWIGLU_MEM>{});
   } else {
     run_pass(zb, p.K, std::integral_constant<int, C::EPI>{});
   }

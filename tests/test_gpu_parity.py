@@ -835,11 +835,14 @@ def test_gate_up_split_tail(gpu, ranks):
     assert np.array_equal(got, _np(ops.svd_mlp(*t)))  # replays are bitwise identical
 
 
-# The gate/up XU.V passes above 512 tokens run as one launch (every block its
-# g tile, then its u tile, reading its own gate values back): the bits of the
+# The gate/up XU.V passes run as one launch: above 512 tokens every block its
+# g tile, then its u tile, reading its own gate values back; at one or two
+# row tiles (the passes split K) every block its g split, then its u split,
+# both storing fp32 slices for the one reduction.  The bits of the
 # two-launch form, which SVDMLP_TUNE=gudual=0 (read once per process) keeps,
-# computed in a child process on the same seeded inputs.  256 x 224 tiles
-# (ff a multiple of 224) and 256 x 256 with distinct gate and up ranks.
+# computed in a child process on the same seeded inputs: 256 x 224 tiles (ff
+# a multiple of 224), 256 x 256 with distinct gate and up ranks, 256 x 128 in
+# four K splits (T=200), 256 x 256 in two (T=500), 256 x 128 unsplit (T=384).
 _DUAL_CHILD = """
 import sys, numpy as np, torch
 sys.path[:0] = sys.argv[1].split("|")
@@ -853,7 +856,8 @@ np.save(sys.argv[9], ops.svd_mlp(*t).view(torch.int16).cpu().numpy())
 
 
 @pytest.mark.parametrize("T,d,ff,ranks", [(600, 1024, 3584, (512, 512, 384)), (700, 1024, 4096, (384, 640, 256)),
-                                          (1000, 2048, 4096, (768, 768, 512))])
+                                          (1000, 2048, 4096, (768, 768, 512)), (200, 1024, 4096, (512, 384, 256)),
+                                          (500, 1024, 4096, (512, 512, 384)), (384, 1024, 4096, (384, 512, 256))])
 def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks):
     import os
     import subprocess
