@@ -842,23 +842,27 @@ def test_gate_up_split_tail(gpu, ranks):
 # two-launch form, which SVDMLP_TUNE=gudual=0 (read once per process) keeps,
 # computed in a child process on the same seeded inputs: 256 x 224 tiles (ff
 # a multiple of 224), 256 x 256 with distinct gate and up ranks, 256 x 128 in
-# four K splits (T=200), 256 x 256 in two (T=500), 256 x 128 unsplit (T=384).
+# four K splits (T=200), 256 x 256 in two (T=500), 256 x 128 unsplit (T=384),
+# a ragged last column tile (ff=1088) and fp8 factors.
 _DUAL_CHILD = """
 import sys, numpy as np, torch
 sys.path[:0] = sys.argv[1].split("|")
-from svdmlp import inputs, ops
-d, ff, rg, ru, rd, T, seed = (int(a) for a in sys.argv[2:9])
+from svdmlp import fp8, inputs, ops
+d, ff, rg, ru, rd, T, seed, q = (int(a) for a in sys.argv[2:10])
 rng = np.random.default_rng(seed)
 f = [inputs.random_matrix(rng, a, b) for a, b in ((d, rg), (rg, ff), (d, ru), (ru, ff), (ff, rd), (rd, d))]
 t = [inputs.to_torch(a, torch.bfloat16, torch.device("cuda:0")) for a in (inputs.make_x(rng, T, d), *f)]
-np.save(sys.argv[9], ops.svd_mlp(*t).view(torch.int16).cpu().numpy())
+if q:
+    t = t[:1] + [fp8.quantize_per_channel(a) for a in t[1:]]
+np.save(sys.argv[10], ops.svd_mlp(*t).view(torch.int16).cpu().numpy())
 """
 
 
-@pytest.mark.parametrize("T,d,ff,ranks", [(600, 1024, 3584, (512, 512, 384)), (700, 1024, 4096, (384, 640, 256)),
-                                          (1000, 2048, 4096, (768, 768, 512)), (200, 1024, 4096, (512, 384, 256)),
-                                          (500, 1024, 4096, (512, 512, 384)), (384, 1024, 4096, (384, 512, 256))])
-def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks):
+@pytest.mark.parametrize("T,d,ff,ranks,q", [(600, 1024, 3584, (512, 512, 384), 0), (700, 1024, 4096, (384, 640, 256), 0),
+                                            (1000, 2048, 4096, (768, 768, 512), 0), (200, 1024, 4096, (512, 384, 256), 0),
+                                            (500, 1024, 4096, (512, 512, 384), 0), (384, 1024, 4096, (384, 512, 256), 0),
+                                            (600, 1024, 1088, (256, 320, 192), 0), (700, 1024, 3584, (512, 384, 256), 1)])
+def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks, q):
     import os
     import subprocess
     import sys
@@ -868,11 +872,13 @@ def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks):
     rng = np.random.default_rng(seed)
     f = [inputs.random_matrix(rng, a, b) for a, b in ((d, r_g), (r_g, ff), (d, r_u), (r_u, ff), (ff, r_d), (r_d, d))]
     t = [inputs.to_torch(a, torch.bfloat16, gpu) for a in (inputs.make_x(rng, T, d), *f)]
+    if q:  # fp8 e4m3 factors with per-column scales (the 70B configuration's format)
+        t = t[:1] + [fp8.quantize_per_channel(a) for a in t[1:]]
     got = ops.svd_mlp(*t).view(torch.int16).cpu().numpy()
     out = tmp_path / "two_launch.npy"
     env = dict(os.environ, SVDMLP_TUNE="gudual=0")
     paths = "|".join(p for p in sys.path if p)
-    subprocess.run([sys.executable, "-c", _DUAL_CHILD, paths, *map(str, (d, ff, r_g, r_u, r_d, T, seed)), str(out)],
+    subprocess.run([sys.executable, "-c", _DUAL_CHILD, paths, *map(str, (d, ff, r_g, r_u, r_d, T, seed, q)), str(out)],
                    env=env, check=True, timeout=120)
     assert np.array_equal(got, np.load(out)), (T, d, ff, ranks)
 
