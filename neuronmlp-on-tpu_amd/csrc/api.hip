@@ -166,16 +166,16 @@ size_t a256(int64_t x) { return ((size_t)x + 255) & ~(size_t)255; }
 
 // Token counts the contracted decode layer (SVDMLP_CONTRACT) takes: its
 // partial XU_d slices grow with T (8B layer: 2.5 MB per token).  It is the
-// default where it is the fastest layer, measured on the 8B layer: with
-// padded V rows at one token (three-barrier layer against contracted: T=1
-// 71.6 vs 70.0 us, T=2 72.3 vs 72.7, T=3 71.9 vs 73.5), with dense factors
-// up to three (the streaming-GEMV layer at T <= 2, the three-barrier layer
-// at 3, against contracted: 77.4 vs 73.6, 80.7 vs 76.0, 78.3 vs 76.8; T=4
-// 78.6 vs 78.8).  With dense factors it applies only where the three-barrier
-// layer cannot run one-branch phase-2 units (p2split_fits): with them that
-// layer is faster at 1-3 tokens too (72.6 / 71.7 / 71.6 us).
+// default where it is the fastest layer, measured on the 8B layer (one box,
+// the better of two 200-step groups each): with padded V rows up to two
+// tokens (four-phase layer against contracted: T=1 63.76 vs 63.75 us, T=2
+// 66.54 vs 65.47, T=3 66.69 vs 67.44, T=4 67.02 vs 69.10), with dense factors
+// up to three (the four-phase layer with one-branch phase-2 units against
+// contracted: T=1 72.47 vs 71.05, T=2 71.77 vs 71.04, T=3 73.32 vs 72.82, T=4
+// 73.40 vs 74.78; before this round's decode changes the four-phase layer
+// was the faster one with dense factors).
 constexpr int64_t kDlContractMaxT = 4;
-constexpr int64_t kDlContractAutoPadded = 1;
+constexpr int64_t kDlContractAutoPadded = 2;
 constexpr int64_t kDlContractAutoDense = 3;
 
 struct Ws {
@@ -2060,22 +2060,22 @@ int svd_mlp_run(const void* x, const void* ug, const void* vg, const void* uu, c
     return big_v(c, reinterpret_cast<const uint16_t*>(ws + L.xu_bf16), vd, v_lin, T, r_d, d, ws, L, y, S[5], ld.vd);
   }
 
-  // With padded V rows the MFMA decode layer is the faster one at every T
+  // With padded V rows the MFMA decode layers are the faster ones at every T
   // (8B layer at T=1: 75.5 us against 78 us): the streaming-GEMV layer reads
   // whole 1 KB row pieces, which the padding does not spread over channels.
-  // With dense factors the three-barrier MFMA layer runs one-branch phase-2
-  // units at every T where they fit (decode_layer), and then beats the
-  // contracted and the streaming-GEMV layers too (8B layer, dense V, T=1 / 2
-  // / 3: 72.6 / 71.7 / 71.6 us against 73.2 / 74.0 / 75.0 contracted and
-  // 78.0 / 81.3 (T=1 / 2) streaming-GEMV).  Otherwise the contracted instance
-  // first wherever it applies (asked for, or where it is the fastest), then
-  // the streaming-GEMV layer, then the three-barrier MFMA layer.
+  // With dense factors the four-phase MFMA layer runs one-branch phase-2
+  // units at every T where they fit (decode_layer) and beats the
+  // streaming-GEMV layer (8B layer, dense V, T=1 / 2: 72.6 / 71.7 us against
+  // 78.0 / 81.3).  The contracted instance first wherever it applies (asked
+  // for, or where it is the fastest: kDlContractAuto*), then the
+  // streaming-GEMV layer where the MFMA layers cannot run one-branch units,
+  // then the four-phase MFMA layer.
   const bool mfma_layer = decode_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld);
   const bool dense_p2 = mfma_layer && ld.dense && tune().p2split > 0 &&
                         p2split_fits(d, ff, r_gu, r_d, decode_layer_grid(decode_layer_mt((int)T)));
   const bool contract =
       contract_asked ||
-      (tune().contract && !dense_p2 && T <= (ld.dense ? kDlContractAutoDense : kDlContractAutoPadded));
+      (tune().contract && T <= (ld.dense ? kDlContractAutoDense : kDlContractAutoPadded));
   if (mfma_layer && contract && decode_contract_ok(T, ff, r_gu, r_d, L, ws_bytes))
     return decode_layer(c, x, ug, vg, uu, vu, ud, vd, y, T, d, ff, r_gu, r_d, ws, L, ld, true);
   if (!(mfma_layer && (!ld.dense || dense_p2)) && gemv_layer_ok(c, T, d, ff, r_gu, r_d, flags, vec, ld)) {

@@ -59,8 +59,8 @@ def test_outliers_prefill(gpu, shape, T, rows):
 @pytest.mark.parametrize("T,padded", [(1, True), (1, False), (8, False), (64, True)])
 def test_outliers_decode_8b(gpu, T, padded):
     """The decode layers at the 8B shape: the contracted layer (one token,
-    padded V rows), the three-barrier layer with one-branch phase-2 units
-    (dense factors) and the two-branch units (padded, 64 tokens)."""
+    padded V rows and dense factors) and the four-phase layer with one-branch
+    phase-2 units (dense, 8 tokens; padded, 64 tokens)."""
     x, f = inputs.make_outlier_layer(SHAPE_8B, T, seed=41 + T)
     xb, *fb = _bf16((x, *f))
     t = [inputs.to_torch(a, torch.bfloat16, gpu) for a in (xb, *fb)]

@@ -21,9 +21,9 @@ BF16_TOL = 1e-2
 FP8_TOL = 3e-2
 GEMV_LAYER_MAX_T = 2   # kGvMaxT in csrc/decode_gemv.hpp
 # kDlContractAutoPadded / kDlContractAutoDense in csrc/api.hip: the contracted
-# decode layer by default at 1 token with padded factor rows, up to 3 with dense
-# factors whose shape the one-branch phase 2 does not fit (_contracted)
-CONTRACT_AUTO_T = {True: 1, False: 3}
+# decode layer by default up to 2 tokens with padded factor rows, up to 3 with
+# dense factors (_contracted)
+CONTRACT_AUTO_T = {True: 2, False: 3}
 
 
 def _mfma_layer(shape):
@@ -44,10 +44,9 @@ def _p2split_fits(shape, cus=256, max_tiles=384):
 def _contracted(shape, T, padded=False):
     """Whether a bf16 natural-layout call runs the contracted decode layer by
     default: its token counts, d and ranks multiples of 128, ff of 64, gate/up
-    rank >= 320, a block per h strip and per XU_d tile (256 CUs); with dense
-    factors only where one-branch phase-2 units do not fit."""
+    rank >= 320, a block per h strip and per XU_d tile (256 CUs)."""
     return (T <= CONTRACT_AUTO_T[padded] and _mfma_layer(shape) and shape.r >= 320
-            and shape.ff // 64 + shape.rd // 128 <= 256 and (padded or not _p2split_fits(shape)))
+            and shape.ff // 64 + shape.rd // 128 <= 256)
 
 
 def _dl_barriers(T, contracted):
@@ -269,9 +268,9 @@ def _tile_counters(ws):
     (inputs.LayerShape(16640, 1024, 128), (8, 64)),                     # 130 output tiles: phase 4 unsplit
 ])
 def test_decode_layer_workspace_reuse(gpu, shape, Ts):
-    """The persistent decode kernels (the three-barrier MFMA layer, or where
-    its one-branch phase 2 does not fit the contracted layer at 1-3 tokens of
-    dense factors and the streaming-GEMV layer up to 2 tokens; one launch
+    """The persistent decode kernels (the contracted layer at 1-3 tokens of
+    dense factors, the four-phase MFMA layer above them, the streaming-GEMV
+    layer up to 2 tokens where neither MFMA layer runs; one launch
     each, grid barriers and split-K tile
     counters in the workspace's first 4096 bytes) over one reused workspace:
     results match the oracle, every call advances the shared barrier
@@ -437,7 +436,7 @@ def test_decode_activation_reads_through_the_caches(gpu, T, padded):
     (inputs.LayerShape(1040, 2064, 400, 272), 1, False),   # streaming-GEMV layer
     (inputs.LayerShape(1040, 2064, 400, 272), 2, False),   # GEMV, ragged strips
     (inputs.LayerShape(1024, 2048, 512), 4, True),         # contracted layer (asked for): tile-combine waits too
-    (inputs.LayerShape(1024, 2048, 512), 1, False)])       # MFMA layer, one-branch phase 2 at one token tile (dense)
+    (inputs.LayerShape(1024, 2048, 512), 4, False)])       # four-phase layer, one-branch phase 2 at one token tile (dense)
 def test_barrier_timeout_poisons_output_and_recovers(gpu, shape, T, contracted):
     """A persistent decode launch whose grid-barrier waits give up (forced
     from the host with a bound of one poll, so every block still runs to its
