@@ -46,7 +46,7 @@ def _call_both(lib, x, fs, dims, dev):
 
 
 @pytest.mark.parametrize("shape,Ts,pad", [
-    (inputs.LayerShape(4096, 14336, 2816), (64, 8, 1), 64),    # LLaMA3-8B decode: MFMA decode layer (contracted at 1)
+    (inputs.LayerShape(4096, 14336, 2816), (64, 8, 2, 1), 64),  # LLaMA3-8B decode: MFMA decode layer (contracted at 1, 2)
     (inputs.LayerShape(1024, 2048, 512, 384), (300, 160), 0),   # large-tile prefill path (fits the scratch)
     (inputs.LayerShape(1040, 2064, 400, 272), (2, 1), 0),       # streaming-GEMV layer (1-2 tokens, d % 128 != 0)
 ])
