@@ -529,6 +529,14 @@ def test_transposed_launchers_bf16(gpu, S, H, R, I):
     y = compat.fused_three_mm_XTUV(_to(np.ascontiguousarray(h_ref.T), torch.bfloat16, gpu), t[5], t[6])
     assert tuple(y.shape) == (S, H)
     assert _rel(_np(y), O.fused_xuv_ref(h_ref, ud, vd, "bfloat16")) < BF16_TOL
+    if S % 8 == 0:
+        # the 16-byte transpose (partial 64-row / 64-column tiles at S=200):
+        # bitwise the natural-layout entry points' results
+        h = ops.fused_gate_up(t[0], *t[1:5])
+        assert torch.equal(hT.view(torch.int16), h.t().contiguous().view(torch.int16))
+        hn = _to(h_ref, torch.bfloat16, gpu)
+        yn = ops.fused_xuv(hn, t[5], t[6])
+        assert torch.equal(y.view(torch.int16), yn.view(torch.int16))
     both = compat.svd_mlp_with_fused_kernel(t[0], t[3], t[4], t[1], t[2], t[5], t[6])
     assert _rel(_np(both), O.svd_mlp_ref(*f, dtype="bfloat16")) < BF16_TOL
 
