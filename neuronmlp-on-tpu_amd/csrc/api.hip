@@ -452,6 +452,7 @@ struct Tune {
   bool xutail = true;  // gate/up X.U with 1-2 rounds of tiles: one round without a split, the rest split
   bool gufuse = true;  // split gate/up XU.V passes: one reduction from both passes' slices
   bool gudual = true;  // gate/up XU.V passes in one launch (each block its g tile or split, then its u one)
+  bool gukg = true;    // ... split and at most 128 token rows: 128 x 128 K-group tiles
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -542,6 +543,7 @@ const Tune& tune() {
         if (k == "xutail") r.xutail = v != 0;
         if (k == "gufuse") r.gufuse = v != 0;
         if (k == "gudual") r.gudual = v != 0;
+        if (k == "gukg") r.gukg = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -1044,11 +1046,28 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   // At one or two row tiles of tokens the passes split K (gu_split_plan).
   int sfn = 0, nsp = 0;
   gu_split_plan(T, ff, &sfn, &nsp);
-  const int64_t per = (int64_t)((T + 255) / 256 * 256) * ((ff + 32 * sfn - 1) / (32 * sfn) * (32 * sfn));
+  // Up to 128 token rows the one-launch split passes run 128 x 128 K-group
+  // tiles: a 256-row tile there spends half its MFMAs and A stages on rows of
+  // zeros (8B factors, T=128: 50.5 us in 256-row tiles).  The same tiles and
+  // splits otherwise; K splits in whole 64-k stages.
+  bool kg2 = tune().gukg && T <= 128 && sfn == 4 && c.wt == SVDMLP_BF16 && !v_lin && tune().gufuse &&
+             tune().gudual && r % 64 == 0 && r_u % 64 == 0;
+  const int kq = kg2 ? 64 : 32;
+  int ks = nsp >= 2 ? (r / nsp + kq - 1) / kq * kq : r, ks_u = nsp >= 2 ? (r_u / nsp + kq - 1) / kq * kq : r_u;
+  int splits = (r + ks - 1) / ks, splits_u = (r_u + ks_u - 1) / ks_u;
+  const int64_t np = (ff + 32 * sfn - 1) / (32 * sfn) * (32 * sfn);
+  int64_t per = (int64_t)((T + 127) / 128 * 128) * np;
+  if (kg2 && (splits != splits_u || (int64_t)(splits + splits_u) * per * 4 > part_cap)) {
+    kg2 = false;  // the K-group tiles run the one-launch passes only
+    ks = nsp >= 2 ? (r / nsp + 31) / 32 * 32 : r;
+    ks_u = nsp >= 2 ? (r_u / nsp + 31) / 32 * 32 : r_u;
+    splits = (r + ks - 1) / ks;
+    splits_u = (r_u + ks_u - 1) / ks_u;
+  }
+  if (!kg2) per = (int64_t)((T + 255) / 256 * 256) * np;
+  const int bm = kg2 ? 128 : 256;
   if (nsp >= 2 && fn == 4 && r >= 32 * nsp && r_u >= 32 * nsp && nsp * per * 4 <= part_cap) {
     fn = sfn;
-    const int ks = (r / nsp + 31) / 32 * 32, splits = (r + ks - 1) / ks;
-    const int ks_u = (r_u / nsp + 31) / 32 * 32, splits_u = (r_u + ks_u - 1) / ks_u;
     // Both passes' slices side by side when the area holds them: one
     // reduction then rounds g from its slices and applies SiLU(g) to the u
     // sum (bitwise the two-reduction result, one launch and the bf16 g round
@@ -1062,7 +1081,7 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
       const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes, ks_u};
       rc = big_gemm(c, ST_GU_XUV_DUAL, xu_g, xu_u, r, xu_bytes, vg, vu, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
                     BEPI_DUAL_F32, ks, part, ff, (int64_t)splits * per, nullptr, true, per, s_vg, s_vu, 0, 1, nullptr,
-                    nullptr, 1, 0, 0, 0, 0, &du);
+                    nullptr, kg2 ? 2 : 1, 0, 0, 0, 0, &du);
       if (rc) return rc;
     } else {
       rc = big_gemm(c, ST_GU_XUV_G, xu_g, nullptr, r, xu_bytes, vg, nullptr, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
@@ -1077,11 +1096,11 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
       if (rc) return rc;
     }
     StageScope fin(ST_FINALIZE, c.st);
-    const int mt = (T + 255) / 256;
+    const int mt = (T + bm - 1) / bm;
     return check(launch_reduce_frag_bf16(upart, splits_u, per, per, static_cast<uint16_t*>(out), ff, (int64_t)T * ff,
-                                         T, ff, mt, (int)(per / (256 * mt) / (32 * fn)), fn,
-                                         big_nw(fn, BEPI_STORE, v_lin), 1, c.st, fused ? nullptr : gbuf, nullptr, 1,
-                                         fused ? part : nullptr, fused ? splits : 0),
+                                         T, ff, mt, (int)(per / ((int64_t)bm * mt) / (32 * fn)), fn,
+                                         kg2 ? 8 : big_nw(fn, BEPI_STORE, v_lin), 1, c.st, fused ? nullptr : gbuf,
+                                         nullptr, kg2 ? 2 : 1, fused ? part : nullptr, fused ? splits : 0),
                  "split-K SwiGLU reduce");
   }
   if (tune().gudual && (fn == 4 || fn == 7 || fn == 8) && !v_lin) {

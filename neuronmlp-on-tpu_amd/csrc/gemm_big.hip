@@ -60,9 +60,16 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
       break;
     case BEPI_DUAL_F32:  // the split passes' fp32 slices; natural-layout B, 8 waves
       if constexpr (FN == 4 || FN == 8) {
-        if (!d.b_kc && d.nw == 8 && d.out_f32)
+        if (!d.b_kc && d.nw == 8 && d.out_f32) {
+          // 128 x 128 K-group tiles (bf16 B) for up to 128 token rows
+          if (d.kg == 2) {
+            if constexpr (FN == 4)
+              if (!d.fp8) return go<FN, false, BEPI_DUAL_F32, true, false, 8, 5, 2>(p, splits, batch, st);
+            break;
+          }
           return d.fp8 ? go<FN, false, BEPI_DUAL_F32, true, true>(p, splits, batch, st)
                        : go<FN, false, BEPI_DUAL_F32, true, false, 8, FN == 4 ? 6 : 4>(p, splits, batch, st);
+        }
       }
       break;
     default: break;
@@ -190,8 +197,9 @@ hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batc
     *why = "big GEMM: tile ranges take 256 x 256 tiles of natural-layout bf16 B with 8 waves and a store epilogue";
     return hipErrorInvalidValue;
   }
-  if (d.kg != 1 && !(d.kg == 2 && (d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE && !d.fp8 && !d.b_kc && d.nw == 8)) {
-    *why = "big GEMM: K groups take natural-layout bf16 B, store epilogues and 128 x 128 or 128 x 192 tiles";
+  if (d.kg != 1 && !(d.kg == 2 && !d.fp8 && !d.b_kc && d.nw == 8 &&
+                     (((d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE) || (d.fn == 4 && d.epi == BEPI_DUAL_F32)))) {
+    *why = "big GEMM: K groups take natural-layout bf16 B, store (or split dual) epilogues and 128 x 128 or 128 x 192 tiles";
     return hipErrorInvalidValue;
   }
   if (d.fn == 8) return go_e<8>(d, p, splits, batch, st, why);

@@ -890,6 +890,50 @@ def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks, q):
     assert np.array_equal(got, np.load(out)), (T, d, ff, ranks)
 
 
+_GU_CHILD = """
+import sys, numpy as np, torch
+sys.path[:0] = sys.argv[1].split("|")
+from svdmlp import inputs, ops
+d, ff, r, T, seed = (int(a) for a in sys.argv[2:7])
+rng = np.random.default_rng(seed)
+f = [inputs.random_matrix(rng, a, b) for a, b in ((d, r), (r, ff), (d, r), (r, ff))]
+t = [inputs.to_torch(a, torch.bfloat16, torch.device("cuda:0")) for a in (inputs.make_x(rng, T, d), *f)]
+np.save(sys.argv[7], ops.fused_gate_up(*t).view(torch.int16).cpu().numpy())
+"""
+
+
+@pytest.mark.parametrize("T,d,ff,r", [(72, 1024, 4096, 512), (100, 1024, 4096, 512), (128, 4096, 14336, 2816)])
+def test_gate_up_split_kgroup_tiles(gpu, tmp_path, T, d, ff, r):
+    """fused_gate_up at 65-128 tokens on the large-tile path: the one-launch
+    split passes on 128 x 128 K-group tiles (each 64-k stage summed in two
+    32-k halves): against the oracle, bitwise on replay, and within the
+    tolerance of the 256-row tiles (SVDMLP_TUNE=gukg=0, another process),
+    whose differently ordered sums show the K-group instance ran."""
+    import os
+    import subprocess
+    import sys
+
+    seed = 1900 + T
+    rng = np.random.default_rng(seed)
+    f = [inputs.random_matrix(rng, a, b) for a, b in ((d, r), (r, ff), (d, r), (r, ff))]
+    x = inputs.make_x(rng, T, d)
+    t = [inputs.to_torch(a, torch.bfloat16, gpu) for a in (x, *f)]
+    h = ops.fused_gate_up(*t)
+    again = ops.fused_gate_up(*t)
+    assert torch.equal(h.view(torch.int16), again.view(torch.int16))
+    xb, *fb = (inputs.as_float32(a, torch.bfloat16) for a in (x, *f))
+    rows = slice(0, min(T, 32))
+    assert _rel(_np(h)[rows], O.fused_gate_up_ref(xb[rows], *fb, "bfloat16")) < BF16_TOL
+    out = tmp_path / "kg1.npy"
+    env = dict(os.environ, SVDMLP_TUNE="gukg=0")
+    paths = "|".join(p for p in sys.path if p)
+    subprocess.run([sys.executable, "-c", _GU_CHILD, paths, *map(str, (d, ff, r, T, seed)), str(out)],
+                   env=env, check=True, timeout=120)
+    h1 = torch.from_numpy(np.load(out)).view(torch.bfloat16).float().numpy()
+    assert _rel(_np(h), h1) < 5e-3
+    assert not np.array_equal(_np(h), h1)
+
+
 def test_distinct_gate_up_ranks_fp8(gpu):
     T, d, ff, r_g, r_u, r_d = 300, 1024, 2048, 512, 256, 384
     xb, *fb = _two_rank_layer(d, ff, r_g, r_u, r_d, T, 950)
