@@ -382,22 +382,24 @@ def _bench_decode_ranks(torch, dev, stream, args, x, rates):
 REF_TPU_US_S128 = {"fused_mlp_up_T": 503.6, "fused_three_mm_XTUV": 339.3, "svd_mlp_with_fused_kernel": 698.1}
 
 
-def _bench_launchers(torch, dev, stream, args, layer, x, S=128):
+def _bench_launchers(torch, dev, stream, args, layers, x, S=128):
     """compat.fused_mlp_up_T ((I, S) output) and compat.fused_three_mm_XTUV
     ((I, S) input) -- test_speedup.py:500-544 -- and their composition
     (test_speedup.py:631-655) on the 8B factors at S=128, timed back to back
-    like the other lines (GPU only); the reference's TPU figures beside them
-    for context."""
+    like the other lines (GPU only), with the factors rotating over the layers
+    (1.25 GB) so that no call finds them in the memory-side cache; the
+    reference's TPU figures beside them for context."""
     from svdmlp import compat
 
     xs = x[:S].contiguous()
-    ug, vg, uu, vu, ud, vd = layer
-    hT = compat.fused_mlp_up_T(xs, ug, vg, uu, vu)
-    out = {"S": S, "d": D, "ff": FF, "r": R, "reference_tpu_us": REF_TPU_US_S128}
+    hT = compat.fused_mlp_up_T(xs, *layers[0][:4])
+    out = {"S": S, "d": D, "ff": FF, "r": R, "layers_rotated": len(layers), "reference_tpu_us": REF_TPU_US_S128}
+    n = len(layers)
     calls = {
-        "fused_mlp_up_T": lambda i: compat.fused_mlp_up_T(xs, ug, vg, uu, vu),
-        "fused_three_mm_XTUV": lambda i: compat.fused_three_mm_XTUV(hT, ud, vd),
-        "svd_mlp_with_fused_kernel": lambda i: compat.svd_mlp_with_fused_kernel(xs, uu, vu, ug, vg, ud, vd),
+        "fused_mlp_up_T": lambda i: compat.fused_mlp_up_T(xs, *layers[i % n][:4]),
+        "fused_three_mm_XTUV": lambda i: compat.fused_three_mm_XTUV(hT, *layers[i % n][4:]),
+        "svd_mlp_with_fused_kernel": lambda i: compat.svd_mlp_with_fused_kernel(
+            xs, layers[i % n][2], layers[i % n][3], layers[i % n][0], layers[i % n][1], *layers[i % n][4:]),
     }
     flops = {"fused_mlp_up_T": 2.0 * S * 2 * R * (D + FF), "fused_three_mm_XTUV": 2.0 * S * R * (FF + D),
              "svd_mlp_with_fused_kernel": 2.0 * S * 3 * R * (D + FF)}
@@ -629,7 +631,7 @@ def main(argv=None) -> int:
                                                    tokens=[t for t in (1, 8, 32, 64) if t <= x.shape[0]],
                                                    rates=rates, layout="natural")
             if x.shape[0] >= 128:
-                record["launchers_s128"] = _bench_launchers(torch, dev, stream, args, dense[0], x)
+                record["launchers_s128"] = _bench_launchers(torch, dev, stream, args, dense, x)
             del dense
             record["decode_two_ranks"] = _bench_decode_ranks(torch, dev, stream, args, x, rates)
     if args.only in (None, "stack"):
