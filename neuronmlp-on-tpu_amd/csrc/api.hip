@@ -453,6 +453,7 @@ struct Tune {
   bool gufuse = true;  // split gate/up XU.V passes: one reduction from both passes' slices
   bool gudual = true;  // gate/up XU.V passes in one launch (each block its g tile or split, then its u one)
   bool gukg = true;    // ... split and at most 128 token rows: 128 x 128 K-group tiles
+  bool gukgu = true;   // ... unsplit at 129-256 token rows on 128 x 128 K-group tiles
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -544,6 +545,7 @@ const Tune& tune() {
         if (k == "gufuse") r.gufuse = v != 0;
         if (k == "gudual") r.gudual = v != 0;
         if (k == "gukg") r.gukg = v != 0;
+        if (k == "gukgu") r.gukgu = v != 0;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -1043,6 +1045,19 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   const int64_t ldb = v_lin ? r : (ldv ? ldv : ff), ldb_u = v_lin ? r_u : (ldv_u ? ldv_u : ldb);
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? ff : r) * ldb * wbytes(c);
   const int64_t xuu_bytes = (int64_t)T * r_u * 2, vu_bytes = (int64_t)(v_lin ? ff : r_u) * ldb_u * wbytes(c);
+  // 129-256 token rows on 128 x 128 K-group tiles: twice the tiles of the
+  // 256-row ones, so the one-launch SwiGLU passes fill the CUs without a K
+  // split (no fp32 slices, no reduction) where ff / 128 tiles per row tile do
+  // (8B layer, two alternating runs: T=160 / 200 / 256 154.2 / 161.9 / 169.7
+  // -> 135.5 / 143.1 / 155.6 us)
+  if (tune().gukgu && T > 128 && T <= 256 && fn == 4 && c.wt == SVDMLP_BF16 && !v_lin && tune().gudual &&
+      r % 64 == 0 && r_u % 64 == 0 && ff % 128 == 0) {
+    const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes};
+    if (want_blk) *h_blk = true;
+    return big_gemm(c, ST_GU_XUV_DUAL, xu_g, xu_u, r, xu_bytes, vg, vu, ldb, v_bytes, v_lin, T, ff, r, 1, fn,
+                    BEPI_GU_DUAL, std::max(r, r_u), out, ff, 0, gbuf, false, 0, s_vg, s_vu, 1, 0, nullptr, nullptr, 2,
+                    want_blk ? 1 : 0, 0, 0, 0, &du);
+  }
   // At one or two row tiles of tokens the passes split K (gu_split_plan).
   int sfn = 0, nsp = 0;
   gu_split_plan(T, ff, &sfn, &nsp);

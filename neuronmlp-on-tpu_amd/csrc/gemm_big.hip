@@ -53,9 +53,16 @@ hipError_t go_e(const BigDesc& d, const BigParams& p, int splits, int batch, hip
       break;
     case BEPI_GU_DUAL:  // natural-layout B (bf16 or fp8), 8 waves
       if constexpr (FN == 4 || FN == 7 || FN == 8) {
-        if (!d.b_kc && d.nw == 8)
+        if (!d.b_kc && d.nw == 8) {
+          // 128 x 128 K-group tiles (bf16 B) for 129-256 token rows
+          if (d.kg == 2) {
+            if constexpr (FN == 4)
+              if (!d.fp8) return go<FN, false, BEPI_GU_DUAL, false, false, 8, 5, 2>(p, splits, batch, st);
+            break;
+          }
           return d.fp8 ? go<FN, false, BEPI_GU_DUAL, false, true>(p, splits, batch, st)
                        : go<FN, false, BEPI_GU_DUAL, false, false, 8, FN == 4 ? 6 : 4>(p, splits, batch, st);
+        }
       }
       break;
     case BEPI_DUAL_F32:  // the split passes' fp32 slices; natural-layout B, 8 waves
@@ -198,8 +205,9 @@ hipError_t launch_big(const BigDesc& d, const BigParams& p, int splits, int batc
     return hipErrorInvalidValue;
   }
   if (d.kg != 1 && !(d.kg == 2 && !d.fp8 && !d.b_kc && d.nw == 8 &&
-                     (((d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE) || (d.fn == 4 && d.epi == BEPI_DUAL_F32)))) {
-    *why = "big GEMM: K groups take natural-layout bf16 B, store (or split dual) epilogues and 128 x 128 or 128 x 192 tiles";
+                     (((d.fn == 4 || d.fn == 6) && d.epi == BEPI_STORE) ||
+                      (d.fn == 4 && (d.epi == BEPI_DUAL_F32 || d.epi == BEPI_GU_DUAL))))) {
+    *why = "big GEMM: K groups take natural-layout bf16 B, store (or dual) epilogues and 128 x 128 or 128 x 192 tiles";
     return hipErrorInvalidValue;
   }
   if (d.fn == 8) return go_e<8>(d, p, splits, batch, st, why);

@@ -284,8 +284,8 @@ struct BigCfg {
   static constexpr int A_UNITS = A_BYTES / 1024 / NW;  // DMA instructions per wave: 2 (NW 4: 4)
   static constexpr int B_UNITS = B_BYTES / 1024 / NW;  // 2 (256-byte rows: 1); NW 4: 4 (2); KG 2: twice
   static_assert(NW == 8 || NW == 4, "8 or 4 waves");
-  static_assert(KG == 1 || (KG == 2 && NW == 8 && !B_KC && !FP8_B && (EPI == BEPI_STORE || EPI == BEPI_DUAL_F32)),
-                "K groups: 8 waves, natural-layout bf16 B, store epilogues (the split dual's included)");
+  static_assert(KG == 1 || (KG == 2 && NW == 8 && !B_KC && !FP8_B && (EPI == BEPI_STORE || DUAL)),
+                "K groups: 8 waves, natural-layout bf16 B, store epilogues (the dual launches' included)");
   static_assert(A_UNITS * NW == 16 && B_UNITS * NW * 1024 == B_BYTES, "DMA instructions per wave and stage");
   static_assert(!(FP8_B && B_KC), "fp8 B is read in natural layout only");
   static_assert(B_KC || BN <= 256, "natural-layout B rows hold at most 256 columns");

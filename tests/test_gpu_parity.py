@@ -881,13 +881,19 @@ def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks, q):
     t = [inputs.to_torch(a, torch.bfloat16, gpu) for a in (inputs.make_x(rng, T, d), *f)]
     if q:  # fp8 e4m3 factors with per-column scales (the 70B configuration's format)
         t = t[:1] + [fp8.quantize_per_channel(a) for a in t[1:]]
-    got = ops.svd_mlp(*t).view(torch.int16).cpu().numpy()
-    out = tmp_path / "two_launch.npy"
-    env = dict(os.environ, SVDMLP_TUNE="gudual=0")
     paths = "|".join(p for p in sys.path if p)
-    subprocess.run([sys.executable, "-c", _DUAL_CHILD, paths, *map(str, (d, ff, r_g, r_u, r_d, T, seed, q)), str(out)],
-                   env=env, check=True, timeout=120)
-    assert np.array_equal(got, np.load(out)), (T, d, ff, ranks)
+
+    def child(tune, name):
+        out = tmp_path / name
+        subprocess.run([sys.executable, "-c", _DUAL_CHILD, paths, *map(str, (d, ff, r_g, r_u, r_d, T, seed, q)),
+                        str(out)], env=dict(os.environ, SVDMLP_TUNE=tune), check=True, timeout=120)
+        return np.load(out)
+
+    # (at 129-256 tokens the default runs 128-row K-group tiles, whose sums are
+    # ordered differently: there the one- and two-launch forms on 256-row tiles)
+    kg = 128 < T <= 256
+    got = child("gukgu=0", "one_launch.npy") if kg else ops.svd_mlp(*t).view(torch.int16).cpu().numpy()
+    assert np.array_equal(got, child("gudual=0,gukgu=0" if kg else "gudual=0", "two_launch.npy")), (T, d, ff, ranks)
 
 
 _GU_CHILD = """
@@ -902,13 +908,15 @@ np.save(sys.argv[7], ops.fused_gate_up(*t).view(torch.int16).cpu().numpy())
 """
 
 
-@pytest.mark.parametrize("T,d,ff,r", [(72, 1024, 4096, 512), (100, 1024, 4096, 512), (128, 4096, 14336, 2816)])
-def test_gate_up_split_kgroup_tiles(gpu, tmp_path, T, d, ff, r):
-    """fused_gate_up at 65-128 tokens on the large-tile path: the one-launch
-    split passes on 128 x 128 K-group tiles (each 64-k stage summed in two
-    32-k halves): against the oracle, bitwise on replay, and within the
-    tolerance of the 256-row tiles (SVDMLP_TUNE=gukg=0, another process),
-    whose differently ordered sums show the K-group instance ran."""
+@pytest.mark.parametrize("T,d,ff,r", [(72, 1024, 4096, 512), (100, 1024, 4096, 512), (128, 4096, 14336, 2816),
+                                      (160, 1024, 4096, 512), (200, 4096, 14336, 2816), (256, 1024, 4096, 384)])
+def test_gate_up_kgroup_tiles(gpu, tmp_path, T, d, ff, r):
+    """fused_gate_up at 65-256 tokens on the large-tile path: the one-launch
+    passes on 128 x 128 K-group tiles (each 64-k stage summed in two 32-k
+    halves), split at up to 128 tokens and unsplit (the SwiGLU epilogue) at
+    129-256: against the oracle, bitwise on replay, and within the tolerance
+    of the 256-row tiles (SVDMLP_TUNE=gukg=0,gukgu=0, another process), whose
+    differently ordered sums show the K-group instance ran."""
     import os
     import subprocess
     import sys
@@ -925,7 +933,7 @@ def test_gate_up_split_kgroup_tiles(gpu, tmp_path, T, d, ff, r):
     rows = slice(0, min(T, 32))
     assert _rel(_np(h)[rows], O.fused_gate_up_ref(xb[rows], *fb, "bfloat16")) < BF16_TOL
     out = tmp_path / "kg1.npy"
-    env = dict(os.environ, SVDMLP_TUNE="gukg=0")
+    env = dict(os.environ, SVDMLP_TUNE="gukg=0,gukgu=0")
     paths = "|".join(p for p in sys.path if p)
     subprocess.run([sys.executable, "-c", _GU_CHILD, paths, *map(str, (d, ff, r, T, seed)), str(out)],
                    env=env, check=True, timeout=120)
