@@ -1046,10 +1046,13 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   const int64_t xu_bytes = (int64_t)T * r * 2, v_bytes = (int64_t)(v_lin ? ff : r) * ldb * wbytes(c);
   const int64_t xuu_bytes = (int64_t)T * r_u * 2, vu_bytes = (int64_t)(v_lin ? ff : r_u) * ldb_u * wbytes(c);
   // 129-256 token rows on 128 x 128 K-group tiles: twice the tiles of the
-  // 256-row ones, so the one-launch SwiGLU passes fill the CUs without a K
-  // split (no fp32 slices, no reduction) where ff / 128 tiles per row tile do
-  // (8B layer, two alternating runs: T=160 / 200 / 256 154.2 / 161.9 / 169.7
-  // -> 135.5 / 143.1 / 155.6 us)
+  // 256-row ones, so the one-launch SwiGLU passes run without a K split (no
+  // fp32 slices, no reduction), and the rows past T of a 256-row tile no
+  // longer cost MFMAs.  Faster on every shape measured, also where the tiles
+  // fill half the CUs (layer, two alternating runs, 256-row split passes ->
+  // these: 8B T=160 / 200 / 256 154.2 / 161.9 / 169.7 -> 135.5 / 143.1 /
+  // 155.6 us; 3B (3072, 8192, 1792) T=160 / 256 104.6 / 109.2 -> 98.5 / 108.0;
+  // (1024, 4096, 512) 66.5 / 62.8 -> 58.8 / 55.5)
   if (tune().gukgu && T > 128 && T <= 256 && fn == 4 && c.wt == SVDMLP_BF16 && !v_lin && tune().gudual &&
       r % 64 == 0 && r_u % 64 == 0 && ff % 128 == 0) {
     const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes};
