@@ -453,7 +453,7 @@ struct Tune {
   bool gufuse = true;  // split gate/up XU.V passes: one reduction from both passes' slices
   bool gudual = true;  // gate/up XU.V passes in one launch (each block its g tile or split, then its u one)
   bool gukg = true;    // ... split and at most 128 token rows: 128 x 128 K-group tiles
-  bool gukgu = true;   // ... unsplit at 129-256 token rows on 128 x 128 K-group tiles
+  int gukgu = 2;       // ... unsplit on 128 x 128 K-group tiles: 1 at 129-256 token rows, 2 while they fit one round
   int dlmin = 1 << 30; // lowest T for the persistent decode layer (min with kDlMinT)
   int gvmax = kGvMaxT; // highest T for the streaming-GEMV decode layer (0: off)
   int gvrw = 1;        // GEMV layer: rows per wave load (1: 1 KB rows, 2: 512-byte rows)
@@ -545,7 +545,7 @@ const Tune& tune() {
         if (k == "gufuse") r.gufuse = v != 0;
         if (k == "gudual") r.gudual = v != 0;
         if (k == "gukg") r.gukg = v != 0;
-        if (k == "gukgu") r.gukgu = v != 0;
+        if (k == "gukgu") r.gukgu = v;
         if (k == "dlmin") r.dlmin = v;
         if (k == "gvmax") r.gvmax = v;
         if (k == "gvrw") r.gvrw = v;
@@ -1052,9 +1052,12 @@ int big_swiglu(const Common& c, const uint16_t* xu_g, const uint16_t* xu_u, cons
   // fill half the CUs (layer, two alternating runs, 256-row split passes ->
   // these: 8B T=160 / 200 / 256 154.2 / 161.9 / 169.7 -> 135.5 / 143.1 /
   // 155.6 us; 3B (3072, 8192, 1792) T=160 / 256 104.6 / 109.2 -> 98.5 / 108.0;
-  // (1024, 4096, 512) 66.5 / 62.8 -> 58.8 / 55.5)
-  if (tune().gukgu && T > 128 && T <= 256 && fn == 4 && c.wt == SVDMLP_BF16 && !v_lin && tune().gudual &&
-      r % 64 == 0 && r_u % 64 == 0 && ff % 128 == 0) {
+  // (1024, 4096, 512) 66.5 / 62.8 -> 58.8 / 55.5).  Up to 512 rows while the
+  // tiles fit one round of the CUs (3B T=384 / 512: 128.1 / 145.0 -> 116.1 /
+  // 124.7 us; the 8B shape's 336 tiles at T=384 would take two rounds).
+  const int64_t kg_tiles = (int64_t)(T + 127) / 128 * ((ff + 127) / 128);
+  if (tune().gukgu && T > 128 && (tune().gukgu >= 2 ? kg_tiles <= tune().split : T <= 256) && fn == 4 &&
+      c.wt == SVDMLP_BF16 && !v_lin && tune().gudual && r % 64 == 0 && r_u % 64 == 0 && ff % 128 == 0) {
     const DualEntry du{r_u, xuu_bytes, r_u, ldb_u, vu_bytes};
     if (want_blk) *h_blk = true;
     return big_gemm(c, ST_GU_XUV_DUAL, xu_g, xu_u, r, xu_bytes, vg, vu, ldb, v_bytes, v_lin, T, ff, r, 1, fn,

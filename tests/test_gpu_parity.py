@@ -889,9 +889,10 @@ def test_gate_up_dual_launch_bitwise(gpu, tmp_path, T, d, ff, ranks, q):
                         str(out)], env=dict(os.environ, SVDMLP_TUNE=tune), check=True, timeout=120)
         return np.load(out)
 
-    # (at 129-256 tokens the default runs 128-row K-group tiles, whose sums are
-    # ordered differently: there the one- and two-launch forms on 256-row tiles)
-    kg = 128 < T <= 256
+    # (at 129-512 tokens, while the 128-row K-group tiles fit one round of the
+    # CUs, the default runs them, whose sums are ordered differently: there the
+    # one- and two-launch forms on 256-row tiles)
+    kg = 128 < T <= 512 and not q and -(-T // 128) * -(-ff // 128) <= 256
     got = child("gukgu=0", "one_launch.npy") if kg else ops.svd_mlp(*t).view(torch.int16).cpu().numpy()
     assert np.array_equal(got, child("gudual=0,gukgu=0" if kg else "gudual=0", "two_launch.npy")), (T, d, ff, ranks)
 
@@ -909,12 +910,13 @@ np.save(sys.argv[7], ops.fused_gate_up(*t).view(torch.int16).cpu().numpy())
 
 
 @pytest.mark.parametrize("T,d,ff,r", [(72, 1024, 4096, 512), (100, 1024, 4096, 512), (128, 4096, 14336, 2816),
-                                      (160, 1024, 4096, 512), (200, 4096, 14336, 2816), (256, 1024, 4096, 384)])
+                                      (160, 1024, 4096, 512), (200, 4096, 14336, 2816), (256, 1024, 4096, 384),
+                                      (384, 1024, 8192, 512), (512, 3072, 8192, 1792)])
 def test_gate_up_kgroup_tiles(gpu, tmp_path, T, d, ff, r):
-    """fused_gate_up at 65-256 tokens on the large-tile path: the one-launch
+    """fused_gate_up at 65-512 tokens on the large-tile path: the one-launch
     passes on 128 x 128 K-group tiles (each 64-k stage summed in two 32-k
     halves), split at up to 128 tokens and unsplit (the SwiGLU epilogue) at
-    129-256: against the oracle, bitwise on replay, and within the tolerance
+    129-512 while the tiles fit one round of the CUs: against the oracle, bitwise on replay, and within the tolerance
     of the 256-row tiles (SVDMLP_TUNE=gukg=0,gukgu=0, another process), whose
     differently ordered sums show the K-group instance ran."""
     import os
